@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+# SPDX-License-Identifier: Apache-2.0
+"""Benchmark of the routed-expert MoE layer out of MXFP4 on one MI355X.
+
+A step is one pass of the layer over one batch of 64 synthetic decode tokens: router
+(384 experts, top-8, fp64 logits, libm-exact sigmoid), expert-major gather, fused
+gate/up + SiLU on the matrix cores, down projection, weighted combine in slot order.
+All inputs are resident in HBM before the timed region (4 token batches rotated; the
+8.98 GB expert bank is far larger than the last-level cache).
+
+Also measured (extra keys of the same JSON line): the same layer at batch 1, and the
+single 2048x7168 MXFP4 GEMV rotating over >= 1 GB of weight copies. Per-kernel times come
+from HIP events the library records between its own launches (k3d_prof_*), on the
+stream the kernels run on.
+
+usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "kimi-k3-in-c_amd"))
+
+import k3amd  # noqa: E402
+import workloads as wl  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+E, I, N, K = wl.HIDDEN, wl.INTER, wl.N_EXPERTS, wl.TOPK
+MAT_BYTES = I * E // 2 + I * E // 32          # one 2048x7168 MXFP4 matrix: 7,798,784 B
+EXPERT_BYTES = 3 * MAT_BYTES                   # 23,396,352 B
+ROUTER_BYTES = N * E * 4
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Layer:
+    """The 384-expert layer resident on the device."""
+
+    def __init__(self):
+        L = k3amd.lib()
+        k3amd.check(L.k3d_init(), "k3d_init")
+        slot = (EXPERT_BYTES + 6 * 256 + 4095) // 4096 * 4096
+        self.bank = k3amd.DevBuf(N * slot)
+        table = (k3amd.K3ExpertQ * N)()
+        t0 = time.time()
+        for e in range(N):
+            ex = wl.expert(e)
+            off = e * slot
+            ptrs = []
+            for a in ex.t:
+                self.bank.upload(a, off)
+                ptrs.append(self.bank.ptr + off)
+                off += (a.nbytes + 255) // 256 * 256
+            table[e] = k3amd.K3ExpertQ(*ptrs)
+            if e % 64 == 63:
+                log(f"bench: expert bank {e + 1}/{N} resident ({time.time() - t0:.1f} s)")
+        self.table = k3amd.DevBuf(C.sizeof(table))
+        k3amd.check(L.k3d_h2d(self.table.ptr, C.addressof(table), C.sizeof(table), None))
+        self.router = k3amd.DevBuf(ROUTER_BYTES).upload(wl.router_weights())
+
+    def run(self, x, out, idx, wt, T, ws, prec=0):
+        k3amd.check(k3amd.lib().k3d_moe_routed(
+            out.ptr, idx.ptr, wt.ptr, x.ptr, T, self.router.ptr, None, self.table.ptr, E, I, N, K,
+            1, 1.0, k3amd.K3_ACT_SILU, 4.0, 25.0, prec, ws.ptr, ws.nbytes, None, None, None, None),
+            "k3d_moe_routed")
+
+
+def time_layer(layer, T, steps, warmup, nbatch=4):
+    L = k3amd.lib()
+    xs = [k3amd.DevBuf(T * E * 4).upload(wl.tokens(T, tag=f"bench.tokens.{b}")) for b in range(nbatch)]
+    out = k3amd.DevBuf(T * E * 4)
+    idx = k3amd.DevBuf(T * K * 4)
+    wt = k3amd.DevBuf(T * K * 4)
+    ws = k3amd.DevBuf(L.k3d_moe_ws(T, E, I, N, K, 0))
+    uniq = []
+    for b in range(nbatch):                       # routing of each batch (outside timing)
+        layer.run(xs[b], out, idx, wt, T, ws)
+        h = idx.download(np.empty((T, K), np.int32))
+        uniq.append(len(np.unique(h)))
+    for s in range(warmup):
+        layer.run(xs[s % nbatch], out, idx, wt, T, ws)
+    k3amd.check(L.k3d_sync(None))
+    prof = k3amd.Profile(max_marks=16 * steps + 64)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        layer.run(xs[s % nbatch], out, idx, wt, T, ws)
+    k3amd.check(L.k3d_sync(None))
+    t1 = time.perf_counter()
+    stages = prof.end()
+    for b in xs + [out, idx, wt, ws]:
+        b.free()
+    u_mean = float(np.mean([uniq[s % nbatch] for s in range(steps)]))
+    return (t1 - t0), stages, u_mean, uniq
+
+
+def time_gemv(steps=200, copies=128):
+    """2048x7168 MXFP4 GEMV, one token, rotating over `copies` distinct weight copies
+    (>= 1 GB, well past the last-level cache) so every launch streams from HBM."""
+    L = k3amd.lib()
+    packed, scales, x = wl.gemv_inputs()
+    rows, inn = packed.shape[0], packed.shape[1] * 2
+    pk_b, sc_b = packed.nbytes, scales.nbytes
+    stride = (pk_b + sc_b + 4095) // 4096 * 4096
+    w = k3amd.DevBuf(copies * stride)
+    w.upload(packed, 0).upload(scales, pk_b)
+    for c in range(1, copies):
+        k3amd.check(L.k3d_h2d(w.ptr + c * stride, packed.ctypes.data, pk_b, None))
+        k3amd.check(L.k3d_h2d(w.ptr + c * stride + pk_b, scales.ctypes.data, sc_b, None))
+    k3amd.check(L.k3d_sync(None))
+    dx = k3amd.DevBuf(inn * 4).upload(x)
+    dy = k3amd.DevBuf(rows * 4)
+    ws = k3amd.DevBuf(L.k3d_matmul_mxfp4_ws(1, inn))
+
+    def launch(c):
+        base = w.ptr + (c % copies) * stride
+        k3amd.check(L.k3d_matmul_mxfp4(dy.ptr, dx.ptr, 1, base, base + pk_b, inn, rows, 0, ws.ptr,
+                                       ws.nbytes, None), "k3d_matmul_mxfp4")
+    for c in range(20):
+        launch(c)
+    k3amd.check(L.k3d_sync(None))
+    prof = k3amd.Profile(max_marks=4 * steps + 16)
+    t0 = time.perf_counter()
+    for c in range(steps):
+        launch(c)
+    k3amd.check(L.k3d_sync(None))
+    t1 = time.perf_counter()
+    st = prof.end()
+    for b in (w, dx, dy, ws):
+        b.free()
+    algo = pk_b + sc_b + inn * 4 + rows * 4        # weights + x + y: 7,835,648 B
+    ms, n = st.get("gemv", (0.0, 0))
+    kern_ms = ms / max(n, 1)
+    return {"shape": [rows, inn], "copies_rotated": copies, "algorithmic_bytes": algo,
+            "kernel_us": round(kern_ms * 1e3, 3),
+            "kernel_GBps": round(algo / (kern_ms * 1e-3) / 1e9, 1),
+            "launch_rate_us": round((t1 - t0) / steps * 1e6, 3),
+            "frac_of_peak": round(algo / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+
+def cpu_baseline(T_sample=8, budget_s=10.0):
+    """The reference's own kernels (oracle/_ref, compiled from its src/core/k3_ops.c) in
+    the reference composition, on the host cores, over a bounded sample of the batch-64
+    workload: the first T_sample tokens of batch 0."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Oracle, Ref
+    kind = "reference" if Ref.available() else "port"
+    impl = Ref() if kind == "reference" else Oracle()
+    threads = Oracle().threads()
+    W = wl.router_weights()
+    X = wl.tokens(64, tag="bench.tokens.0")[:T_sample]
+    idx = np.stack([impl.router(X[t], W, None, K)[0] for t in range(T_sample)])
+    bank = wl.lazy_bank(idx)
+    impl.moe_routed(X[:1], W, None, bank, E, I, K)          # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        impl.moe_routed(X, W, None, bank, E, I, K)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": round(T_sample / med, 3), "unit": "tokens/s", "cores": threads,
+            "kind": kind,
+            "sample": f"{T_sample} tokens of the batch-64 decode layer (router + 8 experts each, "
+                      f"SiLU), {len(times)} reps, median; spread {min(times):.3f}-{max(times):.3f} s",
+            "ms_per_token": round(med / T_sample * 1e3, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this build does not shard the layer across GPUs)", file=sys.stderr)
+        sys.exit(2)
+
+    layer = Layer()
+    T = 64
+    secs, stages, u_mean, uniq = time_layer(layer, T, args.steps, args.warmup)
+    ms_step = secs / args.steps * 1e3
+    tok_s = T * args.steps / secs
+    layer_bytes = u_mean * EXPERT_BYTES + ROUTER_BYTES + 2 * T * E * 4
+    gu_ms, gu_n = stages.get("gateup", (0.0, 1))
+    gu_ms /= max(gu_n, 1)
+    gu_bytes = u_mean * 2 * MAT_BYTES + T * E * 4 + T * K * I * 4
+    gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9 if gu_ms > 0 else 0.0
+    log(f"bench: batch-64 layer {ms_step:.3f} ms/step, {tok_s:.0f} tok/s; stages "
+        + ", ".join(f"{k} {v[0] / max(v[1], 1):.3f} ms" for k, v in stages.items()))
+
+    s1, st1, u1, _ = time_layer(layer, 1, max(args.steps * 5, 50), args.warmup)
+    b1_ms = s1 / max(args.steps * 5, 50) * 1e3
+    b1_bytes = u1 * EXPERT_BYTES + ROUTER_BYTES
+    log(f"bench: batch-1 layer {b1_ms:.3f} ms/step")
+    gemv = time_gemv()
+    log(f"bench: gemv {gemv}")
+
+    line = {
+        "metric": "MoE-layer tokens/s + achieved HBM GB/s (MXFP4 expert GEMV), batch 1 & 64",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "compute": "MXFP4 weights dequantized exactly to bf16 in registers; activations as bf16 "
+                   "hi+lo; MFMA with fp32 accumulation; fp64 router logits",
+        "data": "synthetic",
+        "config": {"workload": "moe_decode_batch64", "tokens": T, "hidden": E, "inter": I,
+                   "experts": N, "topk": K, "activation": "silu", "bank_GB": round(N * EXPERT_BYTES / 1e9, 3),
+                   "unique_experts_per_step": round(u_mean, 1)},
+        "roofline": {"bound": "hbm", "kernel": "mx_gemm GATEUP (fused gate/up + SiLU)",
+                     "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel_ms": round(gu_ms, 4), "algorithmic_bytes": int(gu_bytes)},
+        "layer_GBps": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in stages.items()},
+        "batch1": {"tokens_per_s": round(1e3 / b1_ms, 1), "ms_per_step": round(b1_ms, 4),
+                   "layer_GBps": round(b1_bytes / (b1_ms * 1e-3) / 1e9, 1),
+                   "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st1.items()}},
+        "gemv_2048x7168": gemv,
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline()
+        line["cpu_baseline"] = cb
+        line["gpu_over_cpu"] = round(tok_s / cb["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

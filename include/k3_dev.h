@@ -1,0 +1,85 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * k3_dev.h -- device-pointer entry points of libk3amd.so.
+ *
+ * The reference has no device: its kernels take host buffers (include/k3/k3.h). These
+ * entry points are the same operations for callers whose activations and weights are
+ * already resident in HBM (a serving loop, the benchmark): every pointer is a DEVICE
+ * pointer, work is enqueued on the caller's HIP stream (NULL = the null stream) and the
+ * call returns without synchronising. None of them allocates: scratch comes from a
+ * caller-provided workspace of the size the matching *_ws() function reports. They
+ * return 0, or a negative value with a message available from k3d_error().
+ *
+ * Each names the reference function whose arithmetic it performs.
+ */
+#ifndef K3_DEV_H
+#define K3_DEV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int k3d_init(void);
+const char *k3d_error(void);
+void *k3d_malloc(size_t bytes);
+int k3d_free(void *p);
+int k3d_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int k3d_d2h(void *dst, const void *src, size_t bytes, void *stream);
+int k3d_sync(void *stream);
+
+/* Stage profiler (HIP events). Between k3d_prof_begin and k3d_prof_end, the MoE and GEMV
+ * entry points record an event at each stage boundary; k3d_prof_end synchronises and
+ * returns, per stage, the summed milliseconds and the number of samples. Stage ids: */
+enum { K3D_STAGE_BEGIN = 0, K3D_STAGE_ROUTER = 1, K3D_STAGE_GATHER = 2, K3D_STAGE_GATEUP = 3,
+       K3D_STAGE_DOWN = 4, K3D_STAGE_COMBINE = 5, K3D_STAGE_GEMV = 6, K3D_STAGE_COUNT = 7 };
+int k3d_prof_begin(int max_marks);
+int k3d_prof_mark(void *stream, int stage);
+int k3d_prof_end(double *ms, int *count, int n_stages);
+
+/* Y[ntok][rows] = X[ntok][in] . W^T, W packed MXFP4 with group 32, in % 32 == 0.
+ * prec 0: fp32-accurate (activations split into two bf16 terms), prec 1: activations
+ * rounded to bf16. Arithmetic of k3_matmul_mxfp4 (reference k3_ops.c:1380-1785). */
+size_t k3d_matmul_mxfp4_ws(int ntok, int in);
+int k3d_matmul_mxfp4(float *y, const float *x, int ntok, const uint8_t *packed,
+                     const uint8_t *scales, int in, int rows, int prec, void *ws,
+                     size_t ws_bytes, void *stream);
+
+/* Y[ntok][out] = X[ntok][in] . W^T for fp32 / bf16 weights (reference k3_ops.c:265-291,
+ * 1108-1213). */
+int k3d_matmul_f32(float *y, const float *x, int ntok, const float *W, int in, int out,
+                   void *stream);
+int k3d_matmul_bf16(float *y, const float *x, int ntok, const uint16_t *W, int in, int out,
+                    void *stream);
+
+/* Router over T tokens: idx/wt [T][topk] (reference k3_ops.c:419-478, per token). */
+size_t k3d_router_ws(int T, int hidden, int n_experts);
+int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const float *bias,
+               int hidden, int n_experts, int topk, int renorm, float routed_scale, void *ws,
+               size_t ws_bytes, void *stream);
+
+/* The routed MoE layer (k3_moe's routed loop, reference k3_ops.c:576-643, with z := x),
+ * expert-major. bank is a DEVICE array of n_experts K3ExpertQ (k3.h) whose pointers are
+ * device pointers; an entry with a NULL pointer is a dropped expert. perm_out (T*topk) and
+ * offsets_out (n_experts+1), when not NULL, receive the gather permutation. *drops_out,
+ * when not NULL, receives (after the stream reaches it) the number of dropped
+ * assignments; it must be a device int. */
+size_t k3d_moe_ws(int T, int hidden, int inter, int n_experts, int topk, int prec);
+int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T,
+                   const float *router_w, const float *bias, const void *bank, int hidden,
+                   int inter, int n_experts, int topk, int renorm, float routed_scale, int act,
+                   float b1, float b2, int prec, void *ws, size_t ws_bytes, int *perm_out,
+                   int *offsets_out, int *drops_out, void *stream);
+
+/* The expert half of the layer for a routing already in idx/wt (device). */
+int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x, int T,
+                    const void *bank, int hidden, int inter, int n_experts, int topk, int act,
+                    float b1, float b2, int prec, void *ws, size_t ws_bytes, int *perm_out,
+                    int *offsets_out, int *drops_out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,114 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* k3_common.h -- device-side helpers shared by the HIP translation units. */
+#ifndef K3_COMMON_H
+#define K3_COMMON_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 k3_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 k3_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float k3_f32x4 __attribute__((ext_vector_type(4)));
+typedef float k3_f32x2 __attribute__((ext_vector_type(2)));
+
+/* Upper bound on top-k, as the reference's K3_MAX_TOPK (include/k3/k3.h:557). */
+#define K3_MAX_TOPK_DEV 64
+
+/* Record a launch/runtime failure for k3k_error() (defined in k3_rt.hip). */
+extern "C" int k3k_fail(const char *what, hipError_t e);
+#define K3K_LAUNCH_CHECK(what)                                   \
+    do {                                                         \
+        hipError_t e_ = hipGetLastError();                       \
+        if (e_ != hipSuccess) return k3k_fail(what, e_);         \
+    } while (0)
+
+/* fp32 -> bf16 bits, round to nearest even. Infinities stay infinite, NaN stays NaN. */
+__device__ __forceinline__ uint16_t k3_bf16_rne(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7F800000u) == 0x7F800000u)                 /* inf or NaN */
+        return (uint16_t)((u >> 16) | ((u & 0x007FFFFFu) ? 0x0040u : 0u));
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float k3_bf16_to_f32(uint16_t h)
+{
+    return __uint_as_float((uint32_t)h << 16);
+}
+
+/* Two-term bf16 split: x = hi + lo + r with |r| <= 2^-17 |x|. x - hi is exact in fp32. */
+__device__ __forceinline__ void k3_split2(float x, uint16_t &hi, uint16_t &lo)
+{
+    hi = k3_bf16_rne(x);
+    const float h = k3_bf16_to_f32(hi);
+    const float d = (__float_as_uint(x) & 0x7F800000u) == 0x7F800000u ? 0.0f : x - h;
+    lo = k3_bf16_rne(d);
+}
+
+/* E8M0 scale byte as the f32 operand of v_cvt_scalef32_pk_*_fp4. The instruction takes
+ * only the exponent field of that operand (checked on gfx950 for every byte 0..254,
+ * including 0 -> 2^-127), so the byte goes straight into the exponent bits. Byte 255
+ * (NaN by the OCP spec, zero in the reference) is handled by the caller zeroing the
+ * block's codes, because no exponent field yields a zero scale. */
+__device__ __forceinline__ float k3_e8m0_operand(uint32_t s)
+{
+    return __uint_as_float(s << 23);
+}
+
+/* E8M0 byte to its value for fp32 arithmetic: 2^(s-127), 255 -> 0. s = 0 gives the fp32
+ * subnormal 2^-127, which the device keeps (fp32 denormals are not flushed). */
+__device__ __forceinline__ float k3_e8m0_value(uint32_t s)
+{
+    if (s == 255u) return 0.0f;
+    if (s == 0u) return __uint_as_float(0x00400000u);
+    return __uint_as_float(s << 23);
+}
+
+__device__ __forceinline__ float k3_e2m1_value(uint32_t code)
+{
+    const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    const float m = mag[code & 7u];
+    return (code & 8u) ? -m : m;
+}
+
+/* Eight E2M1 codes (one dword, low nibble first) scaled by 2^(s-127) into eight bf16
+ * lanes, exact for every s in 0..254. */
+__device__ __forceinline__ k3_bf16x8 k3_dequant8_bf16(uint32_t codes, float scale_op)
+{
+    const k3_bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, scale_op, 0);
+    const k3_bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, scale_op, 1);
+    const k3_bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, scale_op, 2);
+    const k3_bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, scale_op, 3);
+    k3_bf16x8 r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+__device__ __forceinline__ k3_bf16x8 k3_as_bf16x8(uint4 v)
+{
+    return __builtin_bit_cast(k3_bf16x8, v);
+}
+
+/* Sigmoid in the reference's form 1/(1+expf(-x)) with the device expf. The router does
+ * NOT use this one: it reproduces the host libm expf bit for bit (k3_route.hip). */
+__device__ __forceinline__ float k3_sigmoid_dev(float x)
+{
+    return 1.0f / (1.0f + expf(-x));
+}
+
+/* Expert activations on one (gate, up) pair, evaluated in the reference's operation
+ * order: SiTU-GLU k3_ops.c:115-121, SiLU-GLU (g*sigmoid(g))*u after k3_ops.c:160. */
+__device__ __forceinline__ float k3_act_pair(float g, float u, int act, float b1, float b2)
+{
+    if (act == 1) {
+        const float a = g * k3_sigmoid_dev(g);
+        return a * u;
+    }
+    const float a = b1 * tanhf(g / b1) * k3_sigmoid_dev(g);
+    const float v = b2 * tanhf(u / b2);
+    return a * v;
+}
+
+#endif

@@ -1,0 +1,331 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * k3_devapi.c -- the device-pointer entry points (include/k3_dev.h), in C99 over the
+ * kernel ABI (k3k.h). Each call carves its scratch from the caller's workspace with the
+ * same layout function that sizes it, so sizing and use cannot drift apart.
+ */
+#include "k3_dev.h"
+#include "k3.h"
+#include "k3k.h"
+
+#include <stdio.h>
+#include <string.h>
+
+extern const int k3_expf_exc_n;
+extern const uint32_t k3_expf_exc[];
+
+static char g_msg[512];
+
+static int fail(const char *what)
+{
+    snprintf(g_msg, sizeof g_msg, "%s: %s", what, k3k_error());
+    return -1;
+}
+
+static int bad(const char *what)
+{
+    snprintf(g_msg, sizeof g_msg, "%s", what);
+    return -2;
+}
+
+const char *k3d_error(void) { return g_msg; }
+
+int k3d_init(void) { return k3k_init() ? fail("init") : 0; }
+void *k3d_malloc(size_t bytes)
+{
+    if (k3d_init()) return NULL;
+    void *p = k3k_malloc(bytes);
+    if (!p) fail("k3d_malloc");
+    return p;
+}
+int k3d_free(void *p) { return k3k_free(p) ? fail("k3d_free") : 0; }
+int k3d_h2d(void *d, const void *h, size_t n, void *s) { return k3k_h2d(d, h, n, s) ? fail("h2d") : 0; }
+int k3d_d2h(void *h, const void *d, size_t n, void *s) { return k3k_d2h(h, d, n, s) ? fail("d2h") : 0; }
+int k3d_sync(void *s) { return k3k_sync(s) ? fail("sync") : 0; }
+
+int k3d_prof_begin(int max_marks) { return k3k_prof_enable(max_marks) ? fail("prof_begin") : 0; }
+int k3d_prof_end(double *ms, int *count, int n_stages)
+{
+    return k3k_prof_collect(ms, count, n_stages) ? fail("prof_end") : 0;
+}
+int k3d_prof_mark(void *stream, int stage) { return k3k_prof_mark(stream, stage) ? fail("prof_mark") : 0; }
+
+/* The libm exception table of the router score, uploaded once per process. */
+static const uint32_t *g_exc_dev = NULL;
+static int exc_table(const uint32_t **tab, int *n)
+{
+    if (!g_exc_dev) {
+        uint32_t *d = (uint32_t *)k3k_malloc((size_t)(2 * k3_expf_exc_n + 2) * 4);
+        if (!d) return -1;
+        if (k3k_h2d(d, k3_expf_exc, (size_t)(2 * k3_expf_exc_n + 2) * 4, NULL) || k3k_sync(NULL))
+            return -1;
+        g_exc_dev = d;
+    }
+    *tab = g_exc_dev;
+    *n = k3_expf_exc_n;
+    return 0;
+}
+
+/* ---- workspace carving ------------------------------------------------------------- */
+typedef struct {
+    char *base;
+    size_t off;
+} Carve;
+
+static void *take(Carve *c, size_t bytes)
+{
+    const size_t o = (c->off + 255u) & ~(size_t)255u;
+    c->off = o + (bytes ? bytes : 1);
+    return c->base ? (void *)(c->base + o) : NULL;
+}
+
+/* ---- MXFP4 GEMV / GEMM --------------------------------------------------------------- */
+typedef struct {
+    uint16_t *xhi, *xlo;
+} MxWs;
+
+static size_t mx_layout(Carve *c, MxWs *w, int ntok, int in)
+{
+    w->xhi = (uint16_t *)take(c, (size_t)ntok * in * 2);
+    w->xlo = (uint16_t *)take(c, (size_t)ntok * in * 2);
+    return c->off;
+}
+
+size_t k3d_matmul_mxfp4_ws(int ntok, int in)
+{
+    Carve c = {NULL, 0};
+    MxWs w;
+    return mx_layout(&c, &w, ntok, in);
+}
+
+int k3d_matmul_mxfp4(float *y, const float *x, int ntok, const uint8_t *packed,
+                     const uint8_t *scales, int in, int rows, int prec, void *ws, size_t ws_bytes,
+                     void *stream)
+{
+    if (in <= 0 || (in % 32) || rows < 0 || ntok < 0) return bad("k3d_matmul_mxfp4: need in % 32 == 0");
+    if (ntok == 0 || rows == 0) return 0;
+    if (ws_bytes < k3d_matmul_mxfp4_ws(ntok, in)) return bad("k3d_matmul_mxfp4: workspace too small");
+    Carve c = {(char *)ws, 0};
+    MxWs w;
+    mx_layout(&c, &w, ntok, in);
+    if (k3k_split_bf16(w.xhi, prec == 0 ? w.xlo : NULL, x, (size_t)ntok * in, stream))
+        return fail("split");
+    K3kMxArgs a;
+    memset(&a, 0, sizeof a);
+    a.packed = packed;
+    a.scales = scales;
+    a.xhi = w.xhi;
+    a.xlo = w.xlo;
+    a.y = y;
+    a.ntok = ntok;
+    a.ldy = rows;
+    a.rows = rows;
+    a.K = in;
+    a.nsplit = prec == 0 ? 2 : 1;
+    k3k_prof_mark(stream, K3D_STAGE_BEGIN);
+    if (k3k_mx_gemm(K3K_MX_PLAIN, &a, stream)) return fail("mx_gemm");
+    k3k_prof_mark(stream, K3D_STAGE_GEMV);
+    return 0;
+}
+
+int k3d_matmul_f32(float *y, const float *x, int ntok, const float *W, int in, int out, void *stream)
+{
+    return k3k_gemv_f32(y, x, W, in, out, ntok, out, stream) ? fail("gemv_f32") : 0;
+}
+
+int k3d_matmul_bf16(float *y, const float *x, int ntok, const uint16_t *W, int in, int out,
+                    void *stream)
+{
+    return k3k_gemv_bf16(y, x, W, in, out, ntok, out, stream) ? fail("gemv_bf16") : 0;
+}
+
+/* ---- router -------------------------------------------------------------------------- */
+static int router_ksplit(int T, int hidden, int n_experts)
+{
+    const int tiles = ((n_experts + 63) / 64) * ((T + 15) / 16);
+    int ks = (512 + tiles - 1) / tiles;
+    int kmax = hidden / 512;
+    if (kmax < 1) kmax = 1;
+    if (ks > kmax) ks = kmax;
+    if (ks < 1) ks = 1;
+    return ks;
+}
+
+typedef struct {
+    double *part;
+} RtWs;
+
+static size_t router_layout(Carve *c, RtWs *w, int T, int hidden, int n_experts)
+{
+    const int ks = router_ksplit(T, hidden, n_experts);
+    w->part = (double *)take(c, (size_t)ks * T * n_experts * 8);
+    return c->off;
+}
+
+size_t k3d_router_ws(int T, int hidden, int n_experts)
+{
+    Carve c = {NULL, 0};
+    RtWs w;
+    return router_layout(&c, &w, T, hidden, n_experts);
+}
+
+int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const float *bias,
+               int hidden, int n_experts, int topk, int renorm, float routed_scale, void *ws,
+               size_t ws_bytes, void *stream)
+{
+    if (T <= 0) return 0;
+    if (topk < 1 || topk > K3_MAX_TOPK) return bad("k3d_router: topk outside 1..64");
+    if (ws_bytes < k3d_router_ws(T, hidden, n_experts)) return bad("k3d_router: workspace too small");
+    Carve c = {(char *)ws, 0};
+    RtWs w;
+    router_layout(&c, &w, T, hidden, n_experts);
+    const int ks = router_ksplit(T, hidden, n_experts);
+    const uint32_t *exc;
+    int nexc;
+    if (exc_table(&exc, &nexc)) return fail("router exception table");
+    if (k3k_router_partial(w.part, x, T, W, hidden, n_experts, ks, stream)) return fail("router_partial");
+    if (k3k_router_final(idx, wt, NULL, w.part, ks, x, W, bias, T, hidden, n_experts, topk, renorm,
+                         routed_scale, exc, nexc, stream))
+        return fail("router_final");
+    return 0;
+}
+
+/* ---- MoE experts ----------------------------------------------------------------------- */
+typedef struct {
+    uint16_t *xhi, *xlo, *ahi, *alo;
+    int *offsets, *perm, *job_expert, *job_off, *job_cnt, *pass_job, *pass_tp, *counts;
+    float *contrib;
+    int max_passes;
+} MoeWs;
+
+static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n_experts, int topk,
+                         int prec)
+{
+    const size_t N = (size_t)T * topk;
+    const int maxjobs = (int)(N < (size_t)n_experts ? N : (size_t)n_experts);
+    w->max_passes = maxjobs + (int)(N / 16) + 1;
+    w->xhi = (uint16_t *)take(c, (size_t)T * hidden * 2);
+    w->xlo = prec == 0 ? (uint16_t *)take(c, (size_t)T * hidden * 2) : NULL;
+    w->ahi = (uint16_t *)take(c, N * inter * 2);
+    w->alo = prec == 0 ? (uint16_t *)take(c, N * inter * 2) : NULL;
+    w->offsets = (int *)take(c, (size_t)(n_experts + 1) * 4);
+    w->perm = (int *)take(c, N * 4);
+    w->job_expert = (int *)take(c, (size_t)maxjobs * 4);
+    w->job_off = (int *)take(c, (size_t)maxjobs * 4);
+    w->job_cnt = (int *)take(c, (size_t)maxjobs * 4);
+    w->pass_job = (int *)take(c, (size_t)w->max_passes * 4);
+    w->pass_tp = (int *)take(c, (size_t)w->max_passes * 4);
+    w->counts = (int *)take(c, 16);
+    w->contrib = (float *)take(c, N * hidden * 4);
+    return c->off;
+}
+
+size_t k3d_moe_ws(int T, int hidden, int inter, int n_experts, int topk, int prec)
+{
+    Carve c = {NULL, 0};
+    MoeWs w;
+    RtWs r;
+    moe_layout(&c, &w, T, hidden, inter, n_experts, topk, prec);
+    router_layout(&c, &r, T, hidden, n_experts);
+    return c.off;
+}
+
+static int moe_experts_ws(float *out, const int *idx, const float *wt, const float *x, int T,
+                          const void *bank, int hidden, int inter, int n_experts, int topk,
+                          int act, float b1, float b2, int prec, const MoeWs *w, int *perm_out,
+                          int *offsets_out, int *drops_out, void *stream)
+{
+    int *perm = perm_out ? perm_out : w->perm;
+    int *offsets = offsets_out ? offsets_out : w->offsets;
+    if (k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
+    if (k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
+                   w->counts, idx, T, topk, n_experts, bank, 16, stream))
+        return fail("gather");
+    k3k_prof_mark(stream, K3D_STAGE_GATHER);
+    K3kMxArgs a;
+    memset(&a, 0, sizeof a);
+    a.bank = bank;
+    a.job_expert = w->job_expert;
+    a.job_off = w->job_off;
+    a.job_cnt = w->job_cnt;
+    a.pass_job = w->pass_job;
+    a.pass_tp = w->pass_tp;
+    a.n_passes = w->counts + 1;
+    a.perm = perm;
+    a.topk = topk;
+    a.act = act;
+    a.b1 = b1;
+    a.b2 = b2;
+    a.nsplit = prec == 0 ? 2 : 1;
+    a.max_passes = w->max_passes;
+    /* gate/up: K = hidden, rows = inter, activations are the tokens */
+    a.xhi = w->xhi;
+    a.xlo = w->xlo;
+    a.ahi = w->ahi;
+    a.alo = w->alo;
+    a.rows = inter;
+    a.K = hidden;
+    if (k3k_mx_gemm(K3K_MX_GATEUP, &a, stream)) return fail("mx_gemm gateup");
+    k3k_prof_mark(stream, K3D_STAGE_GATEUP);
+    /* down: K = inter, rows = hidden, activations are the assignments */
+    a.xhi = w->ahi;
+    a.xlo = w->alo;
+    a.out = w->contrib;
+    a.rows = hidden;
+    a.K = inter;
+    if (k3k_mx_gemm(K3K_MX_DOWN, &a, stream)) return fail("mx_gemm down");
+    k3k_prof_mark(stream, K3D_STAGE_DOWN);
+    if (k3k_combine(out, w->contrib, wt, idx, bank, n_experts, T, topk, hidden, stream)) return fail("combine");
+    k3k_prof_mark(stream, K3D_STAGE_COMBINE);
+    if (drops_out && k3k_d2d(drops_out, w->counts + 2, 4, stream)) return fail("drops");
+    return 0;
+}
+
+int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x, int T,
+                    const void *bank, int hidden, int inter, int n_experts, int topk, int act,
+                    float b1, float b2, int prec, void *ws, size_t ws_bytes, int *perm_out,
+                    int *offsets_out, int *drops_out, void *stream)
+{
+    if (T <= 0) return 0;
+    if ((hidden % 32) || (inter % 32)) return bad("k3d_moe_experts: hidden and inter must be multiples of 32");
+    if (topk < 1 || topk > K3_MAX_TOPK) return bad("k3d_moe_experts: topk outside 1..64");
+    if (ws_bytes < k3d_moe_ws(T, hidden, inter, n_experts, topk, prec))
+        return bad("k3d_moe_experts: workspace too small");
+    Carve c = {(char *)ws, 0};
+    MoeWs w;
+    moe_layout(&c, &w, T, hidden, inter, n_experts, topk, prec);
+    k3k_prof_mark(stream, K3D_STAGE_BEGIN);
+    return moe_experts_ws(out, idx, wt, x, T, bank, hidden, inter, n_experts, topk, act, b1, b2,
+                          prec, &w, perm_out, offsets_out, drops_out, stream);
+}
+
+int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const float *router_w,
+                   const float *bias, const void *bank, int hidden, int inter, int n_experts,
+                   int topk, int renorm, float routed_scale, int act, float b1, float b2, int prec,
+                   void *ws, size_t ws_bytes, int *perm_out, int *offsets_out, int *drops_out,
+                   void *stream)
+{
+    if (T <= 0) return 0;
+    if ((hidden % 32) || (inter % 32)) return bad("k3d_moe_routed: hidden and inter must be multiples of 32");
+    if (topk < 1 || topk > K3_MAX_TOPK) return bad("k3d_moe_routed: topk outside 1..64");
+    if (ws_bytes < k3d_moe_ws(T, hidden, inter, n_experts, topk, prec))
+        return bad("k3d_moe_routed: workspace too small");
+    Carve c = {(char *)ws, 0};
+    MoeWs w;
+    RtWs r;
+    moe_layout(&c, &w, T, hidden, inter, n_experts, topk, prec);
+    router_layout(&c, &r, T, hidden, n_experts);
+    const int ks = router_ksplit(T, hidden, n_experts);
+    const uint32_t *exc;
+    int nexc;
+    if (exc_table(&exc, &nexc)) return fail("router exception table");
+    k3k_prof_mark(stream, K3D_STAGE_BEGIN);
+    if (k3k_router_partial(r.part, x, T, router_w, hidden, n_experts, ks, stream))
+        return fail("router_partial");
+    if (k3k_router_final(idx, wt, NULL, r.part, ks, x, router_w, bias, T, hidden, n_experts, topk,
+                         renorm, routed_scale, exc, nexc, stream))
+        return fail("router_final");
+    k3k_prof_mark(stream, K3D_STAGE_ROUTER);
+    return moe_experts_ws(out, idx, wt, x, T, bank, hidden, inter, n_experts, topk, act, b1, b2,
+                          prec, &w, perm_out, offsets_out, drops_out, stream);
+}

@@ -1,0 +1,720 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * k3_host.c -- the reference's host-pointer API (include/k3.h) on the MI355X.
+ *
+ * C99. Every entry point takes host buffers exactly as the reference's does, moves the
+ * activations to HBM, resolves weights to their registered device copy (or uploads them
+ * for this call), runs the HIP kernels through the k3k ABI / k3_dev entry points on the
+ * library's stream, and copies the outputs back before returning. A HIP failure aborts
+ * with a FATAL message: these functions return void, and returning with the output
+ * unwritten is the failure the reference refuses to allow (src/core/k3_ops.c:37-78).
+ */
+#include "k3.h"
+#include "k3_dev.h"
+#include "k3k.h"
+
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+long k3_expert_drops = 0;
+
+/* ---------------------------------------------------------------- plumbing ---- */
+static void *g_stream = NULL;
+static char g_regerr[256];
+
+static void fatal(const char *what)
+{
+    fprintf(stderr,
+            "k3: FATAL, %s: %s\n"
+            "    Aborting rather than returning with the output unwritten.\n",
+            what, k3k_error());
+    abort();
+}
+
+static void lib_init(void)
+{
+    if (g_stream) return;
+    if (k3k_init()) fatal("no usable HIP device");
+    g_stream = k3k_stream_create();
+    if (!g_stream) fatal("stream creation");
+}
+
+static void check(int rc, const char *what)
+{
+    if (rc) {
+        fprintf(stderr, "k3: FATAL, %s: %s\n", what, rc == -2 ? k3d_error() : k3k_error());
+        abort();
+    }
+}
+
+/* Reusable device buffers, one per role, grown on demand. */
+enum { B_X, B_Y, B_P, B_S, B_WS, B_BIAS, B_RW, B_IDX, B_WT, B_ARENA, B_BANK, B_Z, B_ACC,
+       B_SGU, B_SDN, B_OUT, B_W2, B_W3, B_T0, B_T1, B_T2, B_COUNT };
+static void *g_buf[B_COUNT];
+static size_t g_cap[B_COUNT];
+
+static void *buf(int slot, size_t bytes)
+{
+    if (bytes == 0) bytes = 4;
+    if (g_cap[slot] < bytes) {
+        if (g_buf[slot]) {
+            check(k3k_sync(g_stream), "synchronize before buffer growth");
+            k3k_free(g_buf[slot]);
+        }
+        size_t cap = bytes + bytes / 4;
+        g_buf[slot] = k3k_malloc(cap);
+        if (!g_buf[slot]) fatal("device allocation");
+        g_cap[slot] = cap;
+    }
+    return g_buf[slot];
+}
+
+static void *upload(int slot, const void *h, size_t bytes)
+{
+    void *d = buf(slot, bytes);
+    check(k3k_h2d(d, h, bytes, g_stream), "host to device copy");
+    return d;
+}
+
+static void download(void *h, const void *d, size_t bytes)
+{
+    check(k3k_d2h(h, d, bytes, g_stream), "device to host copy");
+    check(k3k_sync(g_stream), "synchronize");
+}
+
+/* ---------------------------------------------------------------- registry ---- */
+typedef struct {
+    const unsigned char *host;
+    size_t bytes;
+    void *dev;
+} Reg;
+static Reg *g_reg = NULL;
+static int g_nreg = 0, g_capreg = 0;
+
+static const Reg *reg_find(const void *host)
+{
+    const unsigned char *h = (const unsigned char *)host;
+    for (int i = 0; i < g_nreg; i++)
+        if (h >= g_reg[i].host && h < g_reg[i].host + g_reg[i].bytes) return &g_reg[i];
+    return NULL;
+}
+
+void *k3_dev_lookup(const void *host)
+{
+    const Reg *r = host ? reg_find(host) : NULL;
+    if (!r) return NULL;
+    return (char *)r->dev + ((const unsigned char *)host - r->host);
+}
+
+const char *k3_dev_last_error(void) { return g_regerr; }
+
+int k3_dev_register(const void *host, size_t bytes)
+{
+    if (!host || !bytes) {
+        snprintf(g_regerr, sizeof g_regerr, "k3_dev_register: empty range");
+        return -1;
+    }
+    if (g_stream == NULL && (k3k_init() || !(g_stream = k3k_stream_create()))) {
+        snprintf(g_regerr, sizeof g_regerr, "k3_dev_register: %s", k3k_error());
+        return -1;
+    }
+    const unsigned char *h = (const unsigned char *)host;
+    for (int i = 0; i < g_nreg; i++)
+        if (h < g_reg[i].host + g_reg[i].bytes && g_reg[i].host < h + bytes) {
+            snprintf(g_regerr, sizeof g_regerr, "k3_dev_register: range overlaps a registered one");
+            return -1;
+        }
+    void *d = k3k_malloc(bytes);
+    if (!d || k3k_h2d(d, host, bytes, g_stream) || k3k_sync(g_stream)) {
+        snprintf(g_regerr, sizeof g_regerr, "k3_dev_register: %s", k3k_error());
+        if (d) k3k_free(d);
+        return -1;
+    }
+    if (g_nreg == g_capreg) {
+        int cap = g_capreg ? 2 * g_capreg : 16;
+        Reg *n = (Reg *)realloc(g_reg, (size_t)cap * sizeof(Reg));
+        if (!n) {
+            k3k_free(d);
+            snprintf(g_regerr, sizeof g_regerr, "k3_dev_register: out of host memory");
+            return -1;
+        }
+        g_reg = n;
+        g_capreg = cap;
+    }
+    g_reg[g_nreg].host = h;
+    g_reg[g_nreg].bytes = bytes;
+    g_reg[g_nreg].dev = d;
+    g_nreg++;
+    return 0;
+}
+
+int k3_dev_unregister(const void *host)
+{
+    for (int i = 0; i < g_nreg; i++)
+        if (g_reg[i].host == (const unsigned char *)host) {
+            if (g_stream) k3k_sync(g_stream);
+            k3k_free(g_reg[i].dev);
+            g_reg[i] = g_reg[g_nreg - 1];
+            g_nreg--;
+            return 0;
+        }
+    snprintf(g_regerr, sizeof g_regerr, "k3_dev_unregister: not registered");
+    return -1;
+}
+
+/* Device view of host weights: the registered copy, else an upload into `slot`. */
+static const void *weights(int slot, const void *host, size_t bytes)
+{
+    void *d = k3_dev_lookup(host);
+    if (d) return d;
+    return upload(slot, host, bytes);
+}
+
+static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+/* ------------------------------------------------------------------- GEMVs ---- */
+void k3_matmul(float *y, const float *x, const float *W, int in, int out)
+{
+    if (out <= 0) return;
+    lib_init();
+    const float *dw = (const float *)weights(B_P, W, (size_t)in * out * 4);
+    const float *dx = (const float *)upload(B_X, x, (size_t)(in > 0 ? in : 1) * 4);
+    float *dy = (float *)buf(B_Y, (size_t)out * 4);
+    check(k3k_gemv_f32(dy, dx, dw, in, out, 1, out, g_stream), "k3_matmul");
+    download(y, dy, (size_t)out * 4);
+}
+
+void k3_matmul_bf16(float *y, const float *x, const uint16_t *W, int in, int out)
+{
+    if (out <= 0) return;
+    lib_init();
+    const uint16_t *dw = (const uint16_t *)weights(B_P, W, (size_t)in * out * 2);
+    const float *dx = (const float *)upload(B_X, x, (size_t)(in > 0 ? in : 1) * 4);
+    float *dy = (float *)buf(B_Y, (size_t)out * 4);
+    check(k3k_gemv_bf16(dy, dx, dw, in, out, 1, out, g_stream), "k3_matmul_bf16");
+    download(y, dy, (size_t)out * 4);
+}
+
+void k3_matmul_q8(float *y, const float *x, const void *W, int in, int out)
+{
+    if (out <= 0) return;
+    lib_init();
+    const void *dw = weights(B_P, W, (size_t)out * (4 + (size_t)in));
+    const float *dx = (const float *)upload(B_X, x, (size_t)(in > 0 ? in : 1) * 4);
+    float *dy = (float *)buf(B_Y, (size_t)out * 4);
+    check(k3k_gemv_q8(dy, dx, dw, in, out, 1, out, g_stream), "k3_matmul_q8");
+    download(y, dy, (size_t)out * 4);
+}
+
+/* Preconditions of the reference's k3_matmul_mxfp4 (k3_ops.c:1383-1401), same messages. */
+static void mxfp4_preconditions(int in, int group)
+{
+    if (in & 1) {
+        fprintf(stderr,
+                "k3: FATAL, k3_matmul_mxfp4 called with in=%d, which is odd.\n"
+                "    Packed rows are in/2 bytes, two elements per byte; an odd `in`\n"
+                "    truncates that stride below what the trailing group's odd\n"
+                "    remainder reads, a heap read past the caller's buffer instead\n"
+                "    of failing loudly.\n",
+                in);
+        abort();
+    }
+    if (group > 64) {
+        fprintf(stderr,
+                "k3: FATAL, k3_matmul_mxfp4 called with group=%d, which exceeds 64.\n"
+                "    Each group is expanded into a fixed wf[64] stack buffer before\n"
+                "    the dot product; a larger group overflows it instead of failing\n"
+                "    loudly.\n",
+                group);
+        abort();
+    }
+    if (group <= 0) {
+        fprintf(stderr, "k3: FATAL, k3_matmul_mxfp4 called with group=%d.\n", group);
+        abort();
+    }
+}
+
+void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
+                     const unsigned char *scales, int in, int rows, int group)
+{
+    mxfp4_preconditions(in, group);
+    if (rows <= 0) return;
+    if (in <= 0) {
+        memset(y, 0, (size_t)rows * sizeof(float));
+        return;
+    }
+    lib_init();
+    const int ngrp = (in + group - 1) / group;
+    const uint8_t *dp = (const uint8_t *)weights(B_P, packed, (size_t)rows * (in / 2));
+    const uint8_t *ds = (const uint8_t *)weights(B_S, scales, (size_t)rows * ngrp);
+    const float *dx = (const float *)upload(B_X, x, (size_t)in * 4);
+    float *dy = (float *)buf(B_Y, (size_t)rows * 4);
+    if (group == 32 && in % 32 == 0 && aligned16(dp)) {
+        const size_t wsb = k3d_matmul_mxfp4_ws(1, in);
+        check(k3d_matmul_mxfp4(dy, dx, 1, dp, ds, in, rows, 0, buf(B_WS, wsb), wsb, g_stream),
+              "k3_matmul_mxfp4");
+    } else {
+        check(k3k_mx_gemv_valu(dy, dx, dp, ds, in, rows, group, g_stream), "k3_matmul_mxfp4");
+    }
+    download(y, dy, (size_t)rows * 4);
+}
+
+void k3_mxfp4_dequant(float *out, const unsigned char *packed, const unsigned char *scales,
+                      int rows, int pcols, int group)
+{
+    if (rows <= 0 || pcols <= 0) return;
+    if (group <= 0) {
+        fprintf(stderr, "k3: FATAL, k3_mxfp4_dequant called with group=%d.\n", group);
+        abort();
+    }
+    lib_init();
+    const int width = pcols * 2, ngrp = (width + group - 1) / group;
+    const uint8_t *dp = (const uint8_t *)weights(B_P, packed, (size_t)rows * pcols);
+    const uint8_t *ds = (const uint8_t *)weights(B_S, scales, (size_t)rows * ngrp);
+    float *dy = (float *)buf(B_Y, (size_t)rows * width * 4);
+    check(k3k_mx_dequant(dy, dp, ds, rows, pcols, group, g_stream), "k3_mxfp4_dequant");
+    download(out, dy, (size_t)rows * width * 4);
+}
+
+/* ------------------------------------------------------------ router, norms ---- */
+void k3_router(int *idx, float *w, const float *x, const float *W, const float *bias,
+               int hidden, int n_experts, int topk, int renorm, float routed_scale)
+{
+    if (topk <= 0) return;
+    if (topk > K3_MAX_TOPK) {
+        fprintf(stderr, "k3: FATAL, k3_router called with topk=%d above K3_MAX_TOPK=%d.\n", topk,
+                K3_MAX_TOPK);
+        abort();
+    }
+    lib_init();
+    const float *dW = (const float *)weights(B_RW, W, (size_t)n_experts * hidden * 4);
+    const float *db = bias ? (const float *)weights(B_BIAS, bias, (size_t)n_experts * 4) : NULL;
+    const float *dx = (const float *)upload(B_X, x, (size_t)hidden * 4);
+    int *di = (int *)buf(B_IDX, (size_t)topk * 4);
+    float *dwt = (float *)buf(B_WT, (size_t)topk * 4);
+    const size_t wsb = k3d_router_ws(1, hidden, n_experts);
+    check(k3d_router(di, dwt, dx, 1, dW, db, hidden, n_experts, topk, renorm, routed_scale,
+                     buf(B_WS, wsb), wsb, g_stream),
+          "k3_router");
+    check(k3k_d2h(idx, di, (size_t)topk * 4, g_stream), "device to host copy");
+    download(w, dwt, (size_t)topk * 4);
+}
+
+void k3_situ_glu(float *y, const float *x, int n, float b1, float b2)
+{
+    if (n <= 0) return;
+    lib_init();
+    const float *dx = (const float *)upload(B_X, x, (size_t)2 * n * 4);
+    float *dy = (float *)buf(B_Y, (size_t)n * 4);
+    check(k3k_act(dy, dx, n, 1, K3_ACT_SITU, b1, b2, g_stream), "k3_situ_glu");
+    download(y, dy, (size_t)n * 4);
+}
+
+void k3_rmsnorm(float *y, const float *x, const float *w, int n, float eps)
+{
+    if (n <= 0) return;
+    lib_init();
+    const float *dx = (const float *)upload(B_X, x, (size_t)n * 4);
+    const float *dw = (const float *)weights(B_P, w, (size_t)n * 4);
+    float *dy = (float *)buf(B_Y, (size_t)n * 4);
+    check(k3k_rmsnorm(dy, dx, dw, n, 1, eps, g_stream), "k3_rmsnorm");
+    download(y, dy, (size_t)n * 4);
+}
+
+/* -------------------------------------------------------------- expert bank ---- */
+typedef struct {
+    const unsigned char *p1, *s1, *p3, *s3, *p2, *s2;
+} QPtr;
+
+static size_t pk_bytes(int rows, int in) { return (size_t)rows * (in / 2); }
+static size_t sc_bytes(int rows, int in) { return (size_t)rows * ((in + 31) / 32); }
+
+/* Device copy of one expert's six tensors: registered pieces are referenced in place;
+ * the rest are uploaded into the arena at *arena_off. Packed tensors must be 16-byte
+ * aligned on the device for the matrix-core loads; a misaligned registered piece is
+ * copied to an aligned arena slot. */
+static void resolve_expert(QPtr *d, const K3ExpertQ *h, int hidden, int inter, char *arena,
+                           size_t *arena_off)
+{
+    const void *src[6] = {h->p1, h->s1, h->p3, h->s3, h->p2, h->s2};
+    const size_t sz[6] = {pk_bytes(inter, hidden), sc_bytes(inter, hidden),
+                          pk_bytes(inter, hidden), sc_bytes(inter, hidden),
+                          pk_bytes(hidden, inter), sc_bytes(hidden, inter)};
+    const unsigned char *out[6];
+    for (int k = 0; k < 6; k++) {
+        void *dv = k3_dev_lookup(src[k]);
+        if (dv && (k & 1 || aligned16(dv))) {
+            out[k] = (const unsigned char *)dv;
+            continue;
+        }
+        const size_t o = (*arena_off + 255u) & ~(size_t)255u;
+        if (dv) check(k3k_d2d(arena + o, dv, sz[k], g_stream), "expert copy");
+        else check(k3k_h2d(arena + o, src[k], sz[k], g_stream), "expert upload");
+        out[k] = (const unsigned char *)(arena + o);
+        *arena_off = o + sz[k];
+    }
+    d->p1 = out[0]; d->s1 = out[1]; d->p3 = out[2];
+    d->s3 = out[3]; d->p2 = out[4]; d->s2 = out[5];
+}
+
+static size_t expert_upload_bytes(const K3ExpertQ *h, int hidden, int inter)
+{
+    const void *src[6] = {h->p1, h->s1, h->p3, h->s3, h->p2, h->s2};
+    const size_t sz[6] = {pk_bytes(inter, hidden), sc_bytes(inter, hidden),
+                          pk_bytes(inter, hidden), sc_bytes(inter, hidden),
+                          pk_bytes(hidden, inter), sc_bytes(hidden, inter)};
+    size_t n = 0;
+    for (int k = 0; k < 6; k++) {
+        void *dv = k3_dev_lookup(src[k]);
+        if (!dv || (!(k & 1) && !aligned16(dv))) n += ((sz[k] + 255u) & ~(size_t)255u) + 256u;
+    }
+    return n;
+}
+
+static int expert_ok(const K3ExpertQ *q)
+{
+    return q->p1 && q->s1 && q->p3 && q->s3 && q->p2 && q->s2;
+}
+
+/* Fallback for shapes the matrix-core path does not take (hidden or inter not a multiple
+ * of 32): per assignment, three vector-unit MXFP4 GEMVs and the activation, then the
+ * ordered combine. out_d, idx (host), wt_d, x_d are device/host as named. */
+static void experts_generic(float *out_d, const int *idx, const float *wt_d, const int *idx_d,
+                            const float *x_d, int T, const QPtr *bank, int hidden, int inter,
+                            int n_experts, int topk, int act, float b1, float b2)
+{
+    const size_t N = (size_t)T * topk;
+    float *contrib = (float *)buf(B_T0, N * hidden * 4);
+    float *gu = (float *)buf(B_T1, (size_t)2 * inter * 4);
+    float *a = (float *)buf(B_T2, (size_t)inter * 4);
+    for (int t = 0; t < T; t++)
+        for (int j = 0; j < topk; j++) {
+            const int e = idx[t * topk + j];
+            if (e < 0 || e >= n_experts || !bank[e].p1) continue;
+            const QPtr *q = &bank[e];
+            const float *xt = x_d + (size_t)t * hidden;
+            check(k3k_mx_gemv_valu(gu, xt, q->p1, q->s1, hidden, inter, 32, g_stream), "expert gate");
+            check(k3k_mx_gemv_valu(gu + inter, xt, q->p3, q->s3, hidden, inter, 32, g_stream), "expert up");
+            check(k3k_act(a, gu, inter, 1, act, b1, b2, g_stream), "expert act");
+            check(k3k_mx_gemv_valu(contrib + (size_t)(t * topk + j) * hidden, a, q->p2, q->s2, inter,
+                                   hidden, 32, g_stream),
+                  "expert down");
+        }
+    check(k3k_combine(out_d, contrib, wt_d, idx_d, NULL, n_experts, T, topk, hidden, g_stream),
+          "combine");
+}
+
+/* Runs the expert half for a device bank already resolved into `bank` (host array of
+ * device pointers, NULL where absent): out_d[T][hidden] = sum_j wt * expert(x). */
+static void run_bank(float *out_d, const int *idx, const int *idx_d, const float *wt_d,
+                     const float *x_d, int T, const QPtr *bank, int hidden, int inter,
+                     int n_experts, int topk, int act, float b1, float b2, int prec)
+{
+    if ((hidden % 32) == 0 && (inter % 32) == 0) {
+        void *bank_d = upload(B_BANK, bank, (size_t)n_experts * sizeof(QPtr));
+        const size_t wsb = k3d_moe_ws(T, hidden, inter, n_experts, topk, prec);
+        check(k3d_moe_experts(out_d, idx_d, wt_d, x_d, T, bank_d, hidden, inter, n_experts, topk,
+                              act, b1, b2, prec, buf(B_WS, wsb), wsb, NULL, NULL, NULL, g_stream),
+              "moe experts");
+    } else {
+        experts_generic(out_d, idx, wt_d, idx_d, x_d, T, bank, hidden, inter, n_experts, topk, act,
+                        b1, b2);
+    }
+    check(k3k_sync(g_stream), "synchronize");
+}
+
+/* Resolves the experts selected in idx (host) from a host bank and runs them. */
+static void run_experts_mxfp4(float *out_d, const int *idx, const int *idx_d, const float *wt_d,
+                              const float *x_d, int T, const K3ExpertQ *hbank, int hidden,
+                              int inter, int n_experts, int topk, int act, float b1, float b2,
+                              int prec)
+{
+    QPtr *bank = (QPtr *)calloc((size_t)n_experts, sizeof(QPtr));
+    unsigned char *sel = (unsigned char *)calloc((size_t)n_experts, 1);
+    if (!bank || !sel) {
+        fprintf(stderr, "k3: FATAL, host allocation for the expert bank failed.\n");
+        abort();
+    }
+    size_t need = 0;
+    for (int a = 0; a < T * topk; a++) {
+        const int e = idx[a];
+        if (e < 0 || e >= n_experts || sel[e]) continue;
+        sel[e] = 1;
+        if (expert_ok(&hbank[e])) need += expert_upload_bytes(&hbank[e], hidden, inter);
+    }
+    char *arena = need ? (char *)buf(B_ARENA, need) : NULL;
+    size_t off = 0;
+    for (int e = 0; e < n_experts; e++)
+        if (sel[e] && expert_ok(&hbank[e])) resolve_expert(&bank[e], &hbank[e], hidden, inter, arena, &off);
+    run_bank(out_d, idx, idx_d, wt_d, x_d, T, bank, hidden, inter, n_experts, topk, act, b1, b2, prec);
+    free(bank);
+    free(sel);
+}
+
+static void report_drop(int layer, int expert, const char *what)
+{
+    k3_expert_drops++;
+    fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load; this %s is CORRUPT\n", layer,
+            expert, what);
+}
+
+void k3_expert_ffn(float *out, const float *x, const K3ExpertQ *q, int hidden, int inter, int act,
+                   float b1, float b2, float wt)
+{
+    if (hidden <= 0) return;
+    mxfp4_preconditions(hidden, 32);
+    mxfp4_preconditions(inter, 32);
+    lib_init();
+    const int idx0 = 0;
+    const float *dx = (const float *)upload(B_X, x, (size_t)hidden * 4);
+    const int *di = (const int *)upload(B_IDX, &idx0, 4);
+    const float *dw = (const float *)upload(B_WT, &wt, 4);
+    float *dy = (float *)buf(B_OUT, (size_t)hidden * 4);
+    if (!expert_ok(q)) {
+        report_drop(0, 0, "token");
+        memset(out, 0, (size_t)hidden * 4);
+        return;
+    }
+    run_experts_mxfp4(dy, &idx0, di, dw, dx, 1, q, hidden, inter, 1, 1, act, b1, b2, 0);
+    download(out, dy, (size_t)hidden * 4);
+}
+
+void k3_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const float *router_w,
+                   const float *bias, const K3ExpertQ *bank, int hidden, int inter, int n_experts,
+                   int topk, int renorm, float routed_scale, int act, float b1, float b2, int prec)
+{
+    if (T <= 0) return;
+    if (topk < 1 || topk > K3_MAX_TOPK) {
+        fprintf(stderr, "k3: FATAL, k3_moe_routed called with topk=%d outside 1..%d.\n", topk,
+                K3_MAX_TOPK);
+        abort();
+    }
+    mxfp4_preconditions(hidden, 32);
+    mxfp4_preconditions(inter, 32);
+    lib_init();
+    const float *dW = (const float *)weights(B_RW, router_w, (size_t)n_experts * hidden * 4);
+    const float *db = bias ? (const float *)weights(B_BIAS, bias, (size_t)n_experts * 4) : NULL;
+    const float *dx = (const float *)upload(B_X, x, (size_t)T * hidden * 4);
+    int *di = (int *)buf(B_IDX, (size_t)T * topk * 4);
+    float *dwt = (float *)buf(B_WT, (size_t)T * topk * 4);
+    const size_t wsb = k3d_router_ws(T, hidden, n_experts);
+    check(k3d_router(di, dwt, dx, T, dW, db, hidden, n_experts, topk, renorm, routed_scale,
+                     buf(B_WS, wsb), wsb, g_stream),
+          "k3_moe_routed router");
+    check(k3k_d2h(idx, di, (size_t)T * topk * 4, g_stream), "device to host copy");
+    download(wt, dwt, (size_t)T * topk * 4);
+    for (int a = 0; a < T * topk; a++)
+        if (!expert_ok(&bank[idx[a]])) report_drop(0, idx[a], "token");
+    float *dy = (float *)buf(B_OUT, (size_t)T * hidden * 4);
+    run_experts_mxfp4(dy, idx, di, dwt, dx, T, bank, hidden, inter, n_experts, topk, act, b1, b2,
+                      prec);
+    download(out, dy, (size_t)T * hidden * 4);
+}
+
+/* ------------------------------------------------------------- LatentMoE ---- */
+size_t k3_moe_scratch(const K3Cfg *c)
+{
+    const int SI = c->moe_inter * c->n_shared;
+    return (size_t)2 * c->latent + (size_t)3 * c->moe_inter + (size_t)c->latent +
+           (size_t)3 * SI + (size_t)c->hidden;
+}
+
+static size_t wbytes(int wdt, int in, int out)
+{
+    if (wdt == K3_WBF16) return (size_t)in * out * 2;
+    if (wdt == K3_WI8) return (size_t)out * (4 + (size_t)in);
+    return (size_t)in * out * 4;
+}
+
+/* y[t*ldy + o] = W x[t] for a tagged weight matrix (k3_mmw, reference k3.h:289-295). */
+static void mmw_dev(float *y_d, const float *x_d, int ntok, const void *W, int wdt, int in, int out,
+                    int ldy, int slot)
+{
+    const void *dw = weights(slot, W, wbytes(wdt, in, out));
+    int rc;
+    if (wdt == K3_WBF16) rc = k3k_gemv_bf16(y_d, x_d, (const uint16_t *)dw, in, out, ntok, ldy, g_stream);
+    else if (wdt == K3_WI8) rc = k3k_gemv_q8(y_d, x_d, dw, in, out, ntok, ldy, g_stream);
+    else rc = k3k_gemv_f32(y_d, x_d, (const float *)dw, in, out, ntok, ldy, g_stream);
+    check(rc, "k3_mmw");
+}
+
+/* Stable LatentMoE over T tokens (reference k3_ops.c:556-656), batched on the device:
+ * route all tokens, down-project, run the selected experts expert-major, sum in slot
+ * order, RMSNorm the aggregate, up-project, add the unweighted shared expert. prefill
+ * selects the reference's expert-major drop accounting (k3_ops.c:760-781) over its
+ * per-token one (:616-626); the arithmetic is the same either way, as in the reference. */
+static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T,
+                       int *idx_last, float *wt_last, int prefill)
+{
+    const int E = c->hidden, L = c->latent, I = c->moe_inter, K = c->topk, N = c->n_experts;
+    const int SI = I * c->n_shared;
+    if (T <= 0) return;
+    if (K < 1 || K > K3_MAX_TOPK) {
+        fprintf(stderr, "k3: FATAL, k3_moe called with topk=%d outside 1..%d.\n", K, K3_MAX_TOPK);
+        abort();
+    }
+    lib_init();
+    const size_t TK = (size_t)T * K;
+    int *hidx = (int *)malloc(TK * sizeof(int));
+    float *hwt = (float *)malloc(TK * sizeof(float));
+    if (!hidx || !hwt) {
+        fprintf(stderr, "k3: FATAL, host allocation in k3_moe failed.\n");
+        abort();
+    }
+    /* 1. route on the full width */
+    const float *dx = (const float *)upload(B_X, x, (size_t)T * E * 4);
+    const float *dW = (const float *)weights(B_RW, w->gate, (size_t)N * E * 4);
+    const float *db = w->bias ? (const float *)weights(B_BIAS, w->bias, (size_t)N * 4) : NULL;
+    int *di = (int *)buf(B_IDX, TK * 4);
+    float *dwt = (float *)buf(B_WT, TK * 4);
+    {
+        const size_t wsb = k3d_router_ws(T, E, N);
+        check(k3d_router(di, dwt, dx, T, dW, db, E, N, K, c->moe_renorm, c->routed_scale,
+                         buf(B_WS, wsb), wsb, g_stream),
+              "k3_moe router");
+    }
+    check(k3k_d2h(hidx, di, TK * 4, g_stream), "device to host copy");
+    download(hwt, dwt, TK * 4);
+
+    /* Draft cache-only routing (k3_ops.c:584-593): keep resident experts, renormalise. */
+    if (w->cache_only && w->src && w->src->resident) {
+        for (int t = 0; t < T; t++) {
+            int *it = hidx + (size_t)t * K;
+            float *wtt = hwt + (size_t)t * K;
+            int m = 0;
+            float wsum = 0.0f;
+            for (int j = 0; j < K; j++)
+                if (w->src->resident(w->src, w->layer, it[j], NULL)) {
+                    it[m] = it[j];
+                    wtt[m] = wtt[j];
+                    wsum += wtt[j];
+                    m++;
+                }
+            if (wsum > 0.0f)
+                for (int j = 0; j < m; j++) wtt[j] /= wsum;
+            for (int j = m; j < K; j++) {
+                it[j] = -1;        /* filtered slot: contributes nothing */
+                wtt[j] = 0.0f;
+            }
+        }
+        check(k3k_h2d(di, hidx, TK * 4, g_stream), "host to device copy");
+        check(k3k_h2d(dwt, hwt, TK * 4, g_stream), "host to device copy");
+    }
+
+    /* 2. down-project into the latent space */
+    float *dz = (float *)buf(B_Z, (size_t)T * L * 4);
+    mmw_dev(dz, dx, T, w->down, w->wdt, E, L, L, B_P);
+
+    /* 3. routed experts, weighted sum in slot order */
+    float *dacc = (float *)buf(B_ACC, (size_t)T * L * 4);
+    if (w->src) {
+        /* Expert-major: fetch each unique expert once and take its bytes to the device
+         * before the next get(), which may recycle the source's memory (the reference's
+         * prefill loop also consumes each expert before fetching the next, k3_ops.c:757-795). */
+        QPtr *bank = (QPtr *)calloc((size_t)N, sizeof(QPtr));
+        int *uniq = (int *)malloc(TK * sizeof(int));
+        unsigned char *seen = (unsigned char *)calloc((size_t)N, 1);
+        if (!bank || !uniq || !seen) {
+            fprintf(stderr, "k3: FATAL, host allocation in k3_moe failed.\n");
+            abort();
+        }
+        int nu = 0;
+        for (size_t a = 0; a < TK; a++) {
+            const int e = hidx[a];
+            if (e >= 0 && e < N && !seen[e]) { seen[e] = 1; uniq[nu++] = e; }
+        }
+        const size_t per_expert = 2 * (pk_bytes(I, L) + sc_bytes(I, L)) + pk_bytes(L, I) +
+                                  sc_bytes(L, I) + 6 * 512;
+        char *arena = nu ? (char *)buf(B_ARENA, (size_t)nu * per_expert) : NULL;
+        size_t off = 0;
+        if (!w->cache_only && w->src->getmany) w->src->getmany(w->src, w->layer, uniq, nu);
+        for (int u = 0; u < nu; u++) {
+            const int e = uniq[u];
+            K3ExpertQ q;
+            memset(&q, 0, sizeof q);
+            const int miss = w->cache_only ? !w->src->resident(w->src, w->layer, e, &q)
+                                           : (w->src->get(w->src, w->layer, e, &q) != 0);
+            if (miss || !expert_ok(&q)) {
+                if (w->cache_only) continue;
+                if (prefill) {
+                    report_drop(w->layer, e, "chunk");
+                } else {
+                    for (size_t a = 0; a < TK; a++)
+                        if (hidx[a] == e) report_drop(w->layer, e, "token");
+                }
+                continue;
+            }
+            resolve_expert(&bank[e], &q, L, I, arena, &off);
+            check(k3k_sync(g_stream), "synchronize");      /* bytes taken before next get() */
+        }
+        run_bank(dacc, hidx, di, dwt, dz, T, bank, L, I, N, K, K3_ACT_SITU, c->situ_b1,
+                 c->situ_b2, 0);
+        free(bank);
+        free(uniq);
+        free(seen);
+    } else {
+        /* Resident fp32 bank (fixtures only in the reference, k3_ops.c:632-640). */
+        const size_t per13 = (size_t)I * L, per2 = (size_t)L * I;
+        const float *w1 = (const float *)weights(B_W2, w->w1, per13 * N * 4);
+        const float *w3 = (const float *)weights(B_W3, w->w3, per13 * N * 4);
+        const float *w2 = (const float *)weights(B_T2, w->w2, per2 * N * 4);
+        float *contrib = (float *)buf(B_T0, TK * L * 4);
+        float *gu = (float *)buf(B_T1, (size_t)2 * I * 4);
+        float *a = (float *)buf(B_SGU, (size_t)I * 4);
+        for (int t = 0; t < T; t++)
+            for (int j = 0; j < K; j++) {
+                const int e = hidx[t * K + j];
+                if (e < 0 || e >= N) continue;
+                const float *zt = dz + (size_t)t * L;
+                check(k3k_gemv_f32(gu, zt, w1 + (size_t)e * per13, L, I, 1, I, g_stream), "expert w1");
+                check(k3k_gemv_f32(gu + I, zt, w3 + (size_t)e * per13, L, I, 1, I, g_stream), "expert w3");
+                check(k3k_act(a, gu, I, 1, K3_ACT_SITU, c->situ_b1, c->situ_b2, g_stream), "expert act");
+                check(k3k_gemv_f32(contrib + (size_t)(t * K + j) * L, a, w2 + (size_t)e * per2, I, L, 1,
+                                   L, g_stream),
+                      "expert w2");
+            }
+        check(k3k_combine(dacc, contrib, dwt, di, NULL, N, T, K, L, g_stream), "combine");
+    }
+
+    /* 4. RMSNorm of the aggregate, 5. up-project */
+    if (c->latent_norm) {
+        const float *dn = (const float *)weights(B_T1, w->latent_norm, (size_t)L * 4);
+        check(k3k_rmsnorm(dacc, dacc, dn, L, T, c->rms_eps, g_stream), "latent rmsnorm");
+    }
+    float *dout = (float *)buf(B_OUT, (size_t)T * E * 4);
+    mmw_dev(dout, dacc, T, w->up, w->wdt, L, E, E, B_P);
+
+    /* 6. shared expert on the original input, added unweighted */
+    if (SI > 0 && w->sh1 && w->sh3 && w->sh2) {
+        float *sgu = (float *)buf(B_SGU, (size_t)T * 2 * SI * 4);
+        float *sact = (float *)buf(B_Z, (size_t)T * SI * 4);
+        float *sdn = (float *)buf(B_SDN, (size_t)T * E * 4);
+        mmw_dev(sgu, dx, T, w->sh1, w->wdt, E, SI, 2 * SI, B_P);
+        mmw_dev(sgu + SI, dx, T, w->sh3, w->wdt, E, SI, 2 * SI, B_P);
+        check(k3k_act(sact, sgu, SI, T, K3_ACT_SITU, c->situ_b1, c->situ_b2, g_stream), "shared act");
+        mmw_dev(sdn, sact, T, w->sh2, w->wdt, SI, E, E, B_P);
+        check(k3k_axpy_rows(dout, sdn, (size_t)T * E, g_stream), "shared add");
+    }
+    download(out, dout, (size_t)T * E * 4);
+    if (idx_last) memcpy(idx_last, hidx + (size_t)(T - 1) * K, (size_t)K * sizeof(int));
+    if (wt_last) memcpy(wt_last, hwt + (size_t)(T - 1) * K, (size_t)K * sizeof(float));
+    free(hidx);
+    free(hwt);
+}
+
+void k3_moe(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T, int *idx,
+            float *wt, float *scratch)
+{
+    (void)scratch;
+    moe_latent(out, x, w, c, T, idx, wt, 0);
+}
+
+void k3_moe_prefill(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T, int *idx,
+                    float *wt, float *scratch)
+{
+    (void)scratch;
+    const int batched = w->src && T > 1 && !w->cache_only && !getenv("K3_NO_BATCH_PREFILL");
+    moe_latent(out, x, w, c, T, idx, wt, batched);
+}

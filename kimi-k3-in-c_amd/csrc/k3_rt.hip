@@ -1,0 +1,221 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * k3_rt.hip -- HIP runtime wrappers behind the k3k C ABI: device selection, memory,
+ * copies, the graph-safe zero fill, streams and the last-error string.
+ */
+#include "k3_common.h"
+#include "k3k.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static char g_err[512];
+static int g_ready = 0;
+static int g_cus = 0;
+
+extern "C" int k3k_fail(const char *what, hipError_t e)
+{
+    snprintf(g_err, sizeof g_err, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+    return -1;
+}
+
+extern "C" const char *k3k_error(void) { return g_err; }
+
+extern "C" int k3k_device_count(void)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+extern "C" int k3k_init(void)
+{
+    if (g_ready) return 0;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        snprintf(g_err, sizeof g_err, "no HIP device available (%s)",
+                 e == hipSuccess ? "device count 0" : hipGetErrorString(e));
+        return -1;
+    }
+    int dev = 0;
+    e = hipGetDevice(&dev);
+    if (e != hipSuccess) return k3k_fail("hipGetDevice", e);
+    e = hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return k3k_fail("hipDeviceGetAttribute", e);
+    g_ready = 1;
+    return 0;
+}
+
+extern "C" int k3k_cu_count(void)
+{
+    if (!g_ready && k3k_init() != 0) return 256;
+    return g_cus > 0 ? g_cus : 256;
+}
+
+extern "C" void *k3k_malloc(size_t bytes)
+{
+    void *p = nullptr;
+    if (bytes == 0) bytes = 256;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        k3k_fail("hipMalloc", e);
+        return nullptr;
+    }
+    return p;
+}
+
+extern "C" int k3k_free(void *p)
+{
+    if (!p) return 0;
+    hipError_t e = hipFree(p);
+    return e == hipSuccess ? 0 : k3k_fail("hipFree", e);
+}
+
+extern "C" int k3k_h2d(void *dst, const void *src, size_t bytes, void *stream)
+{
+    if (!bytes) return 0;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : k3k_fail("hipMemcpyAsync H2D", e);
+}
+
+extern "C" int k3k_d2h(void *dst, const void *src, size_t bytes, void *stream)
+{
+    if (!bytes) return 0;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : k3k_fail("hipMemcpyAsync D2H", e);
+}
+
+extern "C" int k3k_d2d(void *dst, const void *src, size_t bytes, void *stream)
+{
+    if (!bytes) return 0;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : k3k_fail("hipMemcpyAsync D2D", e);
+}
+
+namespace {
+__global__ void zero_kernel(uint32_t *p, size_t nwords, uint8_t *tail, size_t ntail)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nwords;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+    if (blockIdx.x == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
+}
+}  // namespace
+
+/* A fill kernel rather than hipMemsetAsync, so that a caller may capture it in a graph. */
+extern "C" int k3k_zero(void *dst, size_t bytes, void *stream)
+{
+    if (!bytes) return 0;
+    const size_t nw = bytes / 4, nt = bytes % 4;
+    size_t blocks = (nw + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (uint32_t *)dst, nw, (uint8_t *)dst + nw * 4, nt);
+    K3K_LAUNCH_CHECK("zero launch");
+    return 0;
+}
+
+extern "C" int k3k_sync(void *stream)
+{
+    hipError_t e = stream ? hipStreamSynchronize((hipStream_t)stream) : hipDeviceSynchronize();
+    return e == hipSuccess ? 0 : k3k_fail("synchronize", e);
+}
+
+extern "C" void *k3k_stream_create(void)
+{
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        k3k_fail("hipStreamCreate", e);
+        return nullptr;
+    }
+    return (void *)s;
+}
+
+extern "C" int k3k_stream_destroy(void *stream)
+{
+    if (!stream) return 0;
+    hipError_t e = hipStreamDestroy((hipStream_t)stream);
+    return e == hipSuccess ? 0 : k3k_fail("hipStreamDestroy", e);
+}
+
+/* ---- stage profiler ------------------------------------------------------------------ */
+namespace {
+hipEvent_t *g_ev = nullptr;
+int *g_ev_stage = nullptr;
+hipStream_t *g_ev_stream = nullptr;
+int g_ev_cap = 0, g_ev_n = 0, g_prof_on = 0;
+}  // namespace
+
+extern "C" int k3k_prof_enable(int max_marks)
+{
+    if (max_marks <= 0) {
+        g_prof_on = 0;
+        return 0;
+    }
+    if (max_marks > g_ev_cap) {
+        for (int i = 0; i < g_ev_cap; i++) hipEventDestroy(g_ev[i]);
+        free(g_ev);
+        free(g_ev_stage);
+        free(g_ev_stream);
+        g_ev = (hipEvent_t *)calloc((size_t)max_marks, sizeof(hipEvent_t));
+        g_ev_stage = (int *)calloc((size_t)max_marks, sizeof(int));
+        g_ev_stream = (hipStream_t *)calloc((size_t)max_marks, sizeof(hipStream_t));
+        if (!g_ev || !g_ev_stage || !g_ev_stream) {
+            g_ev_cap = 0;
+            snprintf(g_err, sizeof g_err, "profiler: out of host memory");
+            return -1;
+        }
+        for (int i = 0; i < max_marks; i++) {
+            hipError_t e = hipEventCreate(&g_ev[i]);
+            if (e != hipSuccess) {
+                g_ev_cap = i;
+                return k3k_fail("hipEventCreate", e);
+            }
+        }
+        g_ev_cap = max_marks;
+    }
+    g_ev_n = 0;
+    g_prof_on = 1;
+    return 0;
+}
+
+extern "C" int k3k_prof_active(void) { return g_prof_on; }
+
+extern "C" int k3k_prof_mark(void *stream, int stage)
+{
+    if (!g_prof_on || g_ev_n >= g_ev_cap) return 0;
+    hipError_t e = hipEventRecord(g_ev[g_ev_n], (hipStream_t)stream);
+    if (e != hipSuccess) return k3k_fail("hipEventRecord", e);
+    g_ev_stage[g_ev_n] = stage;
+    g_ev_stream[g_ev_n] = (hipStream_t)stream;
+    g_ev_n++;
+    return 0;
+}
+
+extern "C" int k3k_prof_collect(double *ms, int *count, int n_stages)
+{
+    for (int s = 0; s < n_stages; s++) { ms[s] = 0.0; count[s] = 0; }
+    for (int i = 0; i < g_ev_n; i++) {
+        hipError_t e = hipEventSynchronize(g_ev[i]);
+        if (e != hipSuccess) return k3k_fail("hipEventSynchronize", e);
+    }
+    for (int i = 1; i < g_ev_n; i++) {
+        int prev = -1;
+        for (int j = i - 1; j >= 0; j--)
+            if (g_ev_stream[j] == g_ev_stream[i]) { prev = j; break; }
+        const int st = g_ev_stage[i];
+        if (prev < 0 || st <= 0 || st >= n_stages) continue;   /* stage 0 opens a sequence */
+        float t = 0.0f;
+        hipError_t e = hipEventElapsedTime(&t, g_ev[prev], g_ev[i]);
+        if (e != hipSuccess) return k3k_fail("hipEventElapsedTime", e);
+        ms[st] += t;
+        count[st]++;
+    }
+    g_prof_on = 0;
+    g_ev_n = 0;
+    return 0;
+}

@@ -1,0 +1,132 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * k3k.h -- the thin C ABI between the C99 host layer and the HIP kernels.
+ *
+ * Every function here launches one kernel (or wraps one HIP runtime call) on the given
+ * stream and returns 0 or a negative code; k3k_error() describes the last failure. All
+ * pointers are DEVICE pointers unless named h_*. Nothing here allocates, except
+ * k3k_malloc itself.
+ */
+#ifndef K3K_H
+#define K3K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime -------------------------------------------------------------------- */
+int k3k_init(void);                 /* select device 0 on first use; 0 = ok */
+const char *k3k_error(void);
+int k3k_device_count(void);
+void *k3k_malloc(size_t bytes);     /* NULL on failure */
+int k3k_free(void *p);
+int k3k_h2d(void *dst, const void *h_src, size_t bytes, void *stream);
+int k3k_d2h(void *h_dst, const void *src, size_t bytes, void *stream);
+int k3k_d2d(void *dst, const void *src, size_t bytes, void *stream);
+int k3k_zero(void *dst, size_t bytes, void *stream);       /* fill kernel, graph-safe */
+int k3k_sync(void *stream);
+void *k3k_stream_create(void);
+int k3k_stream_destroy(void *stream);
+int k3k_cu_count(void);
+
+/* Stage profiler: while enabled, k3k_prof_mark(stream, stage) records a HIP event on the
+ * stream; k3k_prof_collect() waits for the device and sums, per stage, the time from the
+ * previous mark on the same stream to that stage's mark. */
+int k3k_prof_enable(int max_marks);
+int k3k_prof_active(void);
+int k3k_prof_mark(void *stream, int stage);
+int k3k_prof_collect(double *ms, int *count, int n_stages);
+
+/* ---- activations: fp32 -> bf16 split --------------------------------------------- */
+/* hi = bf16_rne(x), lo = bf16_rne(x - hi) (lo may be NULL: one-term rounding). */
+int k3k_split_bf16(uint16_t *hi, uint16_t *lo, const float *x, size_t n, void *stream);
+
+/* ---- MXFP4 grouped matmul on MFMA -------------------------------------------------
+ * A "job" is one weight matrix W [rows][K] in packed MXFP4 (group 32) applied to a list
+ * of activation rows: out[row_of(tok)][r] = sum_k W[r][k] * act[row_of(tok)][k].
+ * Jobs come either from the expert gather (mode GATEUP / DOWN) or from a single matrix
+ * (mode PLAIN). Activations arrive pre-split as bf16 hi (+ lo when nsplit == 2). */
+enum { K3K_MX_PLAIN = 0, K3K_MX_GATEUP = 1, K3K_MX_DOWN = 2 };
+
+typedef struct {
+    /* PLAIN: one job. */
+    const uint8_t *packed, *scales;     /* [rows][K/2], [rows][K/32] */
+    const uint16_t *xhi, *xlo;          /* [ntok][K] */
+    float *y;                           /* [ntok][ldy] */
+    int ntok, ldy;
+    /* GATEUP / DOWN: jobs from the gather. A pass is up to 16 tokens of one job. */
+    const void *bank;                   /* device K3ExpertQ[n_experts] */
+    const int *job_expert, *job_off, *job_cnt;
+    const int *pass_job, *pass_tp, *n_passes;
+    const int *perm;                    /* sorted position -> assignment a = t*topk + j */
+    int topk;
+    float *out;                         /* DOWN: contrib [T*topk][rows]              */
+    uint16_t *ahi, *alo;                /* GATEUP: activation split [T*topk][rows]   */
+    int act;                            /* K3_ACT_* */
+    float b1, b2;
+    /* shape */
+    int rows, K, nsplit;
+    int max_passes;                     /* host-side bound on *n_passes (grid sizing) */
+} K3kMxArgs;
+
+int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
+
+/* Generic fp32-exact MXFP4 GEMV on the vector units for any even K and group <= 64
+ * (y[rows] = W x, one token). Used where the MFMA path's shape assumptions fail. */
+int k3k_mx_gemv_valu(float *y, const float *x, const uint8_t *packed, const uint8_t *scales,
+                     int in, int rows, int group, void *stream);
+int k3k_mx_dequant(float *out, const uint8_t *packed, const uint8_t *scales, int rows,
+                   int pcols, int group, void *stream);
+
+/* ---- dense GEMV (vector units, fp32 accumulation) -------------------------------- */
+/* y[t*ldy + o] = W[o][:] . x[t][:] for t < ntok, o < out. */
+int k3k_gemv_f32(float *y, const float *x, const float *W, int in, int out, int ntok, int ldy,
+                 void *stream);
+int k3k_gemv_bf16(float *y, const float *x, const uint16_t *W, int in, int out, int ntok,
+                  int ldy, void *stream);
+int k3k_gemv_q8(float *y, const float *x, const void *W, int in, int out, int ntok, int ldy,
+                void *stream);
+
+/* ---- router ----------------------------------------------------------------------- */
+/* Logit partials in fp64 over ksplit K-chunks: part[ks][t][e]. */
+int k3k_router_partial(double *part, const float *x, int T, const float *W, int hidden,
+                       int n_experts, int ksplit, void *stream);
+/* Sum partials in fixed order, sigmoid, biased selection, renorm, scale. idx/wt [T][topk].
+ * flags [T] receives the number of logits whose fp32 rounding was not certified (and
+ * were therefore recomputed in the reference's sequential order). */
+int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, int ksplit,
+                     const float *x, const float *W, const float *bias, int T, int hidden,
+                     int n_experts, int topk, int renorm, float routed_scale,
+                     const uint32_t *exc, int n_exc, void *stream);
+
+/* ---- gather / combine -------------------------------------------------------------- */
+/* Stable expert-major gather of the T*topk assignments in idx (one workgroup). Outputs:
+ *   offsets[n_experts+1]; perm[T*topk]: sorted position -> assignment t*topk+j, experts
+ *   ascending and (t, j) ascending inside one expert; jobs = experts with at least one
+ *   assignment and a present bank entry, ascending: job_expert/job_off/job_cnt; passes
+ *   of up to pass_tok tokens of one job: pass_job/pass_tp; counts[0] = n_jobs,
+ *   counts[1] = n_passes, counts[2] = assignments whose bank entry is NULL (dropped). */
+int k3k_gather(int *offsets, int *perm, int *job_expert, int *job_off, int *job_cnt,
+               int *pass_job, int *pass_tp, int *counts, const int *idx, int T, int topk,
+               int n_experts, const void *bank, int pass_tok, void *stream);
+/* out[t][i] = 0 + sum_j wt[t][j] * contrib[t*topk+j][i], j ascending, skipping
+ * assignments whose expert index is outside [0, n_experts) or whose bank entry has a
+ * NULL pointer (bank == NULL: every in-range expert is present). */
+int k3k_combine(float *out, const float *contrib, const float *wt, const int *idx,
+                const void *bank, int n_experts, int T, int topk, int E, void *stream);
+
+/* ---- elementwise -------------------------------------------------------------------- */
+int k3k_act(float *y, const float *gu, int n, int rows, int act, float b1, float b2,
+            void *stream);
+int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int rows, float eps,
+                void *stream);
+int k3k_axpy_rows(float *out, const float *add, size_t n, void *stream); /* out += add */
+int k3k_scale(float *out, const float *in, float s, size_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

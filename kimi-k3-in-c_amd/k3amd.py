@@ -1,0 +1,340 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Python mirror of libk3amd.so's C ABI (include/k3.h, include/k3_dev.h, include/k3_gen.h).
+
+The host-pointer functions keep the reference's names, argument meaning and error
+behaviour (src/core/k3_ops.c of the reference; a precondition violation aborts the
+process there and here). Arrays are numpy; outputs are returned. The device-pointer
+functions take integer device addresses (e.g. torch tensor .data_ptr()) and a stream
+handle, and enqueue without synchronising.
+
+The library is loaded from this directory; nothing here falls back to another
+implementation: if libk3amd.so is missing the import of any entry point raises.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libk3amd.so")
+
+K3_WF32, K3_WBF16, K3_WI8 = 0, 1, 2
+K3_ACT_SITU, K3_ACT_SILU = 0, 1
+K3_MAX_TOPK = 64
+STAGES = ("begin", "router", "gather", "gateup", "down", "combine", "gemv")
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        _lib = C.CDLL(LIB_PATH, mode=C.RTLD_GLOBAL)
+        _declare(_lib)
+    return _lib
+
+
+P = C.c_void_p
+I = C.c_int
+F = C.c_float
+SZ = C.c_size_t
+
+
+class K3ExpertQ(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("p1", "s1", "p3", "s3", "p2", "s2")]
+
+
+class K3ExpertSrc(C.Structure):
+    pass
+
+
+GETFN = C.CFUNCTYPE(C.c_int, C.POINTER(K3ExpertSrc), C.c_int, C.c_int, C.POINTER(K3ExpertQ))
+GETMANYFN = C.CFUNCTYPE(C.c_int, C.POINTER(K3ExpertSrc), C.c_int, C.POINTER(C.c_int), C.c_int)
+K3ExpertSrc._fields_ = [("get", GETFN), ("getmany", GETMANYFN), ("resident", GETFN),
+                        ("ctx", C.c_void_p)]
+
+
+class K3Cfg(C.Structure):
+    _fields_ = [("hidden", I), ("n_layers", I), ("vocab", I), ("rms_eps", F),
+                ("kda_heads", I), ("kda_head_dim", I), ("conv_k", I), ("gate_lb", F),
+                ("n_heads", I), ("q_lora", I), ("kv_lora", I), ("qk_nope", I), ("qk_rope", I),
+                ("v_head", I), ("mla_out_gate", I), ("n_experts", I), ("topk", I),
+                ("n_shared", I), ("latent", I), ("moe_inter", I), ("routed_scale", F),
+                ("moe_renorm", I), ("latent_norm", I), ("first_dense", I), ("dense_inter", I),
+                ("attn_res_block", I), ("situ_b1", F), ("situ_b2", F), ("n_full_attn", I),
+                ("full_attn", C.POINTER(C.c_int))]
+
+
+class K3MoeW(C.Structure):
+    _fields_ = [("gate", P), ("bias", P), ("w1", P), ("w3", P), ("w2", P), ("latent_norm", P),
+                ("down", P), ("up", P), ("sh1", P), ("sh3", P), ("sh2", P), ("wdt", I),
+                ("src", C.POINTER(K3ExpertSrc)), ("layer", I), ("cache_only", I)]
+
+
+def _declare(L):
+    def d(name, res, *args):
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = list(args)
+
+    d("k3_matmul", None, P, P, P, I, I)
+    d("k3_matmul_bf16", None, P, P, P, I, I)
+    d("k3_matmul_q8", None, P, P, P, I, I)
+    d("k3_mxfp4_dequant", None, P, P, P, I, I, I)
+    d("k3_matmul_mxfp4", None, P, P, P, P, I, I, I)
+    d("k3_router", None, P, P, P, P, P, I, I, I, I, F)
+    d("k3_situ_glu", None, P, P, I, F, F)
+    d("k3_rmsnorm", None, P, P, P, I, F)
+    d("k3_moe_scratch", SZ, C.POINTER(K3Cfg))
+    d("k3_moe", None, P, P, C.POINTER(K3MoeW), C.POINTER(K3Cfg), I, P, P, P)
+    d("k3_moe_prefill", None, P, P, C.POINTER(K3MoeW), C.POINTER(K3Cfg), I, P, P, P)
+    d("k3_expert_ffn", None, P, P, C.POINTER(K3ExpertQ), I, I, I, F, F, F)
+    d("k3_moe_routed", None, P, P, P, P, I, P, P, P, I, I, I, I, I, F, I, F, F, I)
+    d("k3_dev_register", I, P, SZ)
+    d("k3_dev_unregister", I, P)
+    d("k3_dev_lookup", P, P)
+    d("k3_dev_last_error", C.c_char_p)
+    # device API
+    d("k3d_init", I)
+    d("k3d_error", C.c_char_p)
+    d("k3d_malloc", P, SZ)
+    d("k3d_free", I, P)
+    d("k3d_h2d", I, P, P, SZ, P)
+    d("k3d_d2h", I, P, P, SZ, P)
+    d("k3d_sync", I, P)
+    d("k3d_prof_begin", I, I)
+    d("k3d_prof_mark", I, P, I)
+    d("k3d_prof_end", I, P, P, I)
+    d("k3d_matmul_mxfp4_ws", SZ, I, I)
+    d("k3d_matmul_mxfp4", I, P, P, I, P, P, I, I, I, P, SZ, P)
+    d("k3d_matmul_f32", I, P, P, I, P, I, I, P)
+    d("k3d_matmul_bf16", I, P, P, I, P, I, I, P)
+    d("k3d_router_ws", SZ, I, I, I)
+    d("k3d_router", I, P, P, P, I, P, P, I, I, I, I, F, P, SZ, P)
+    d("k3d_moe_ws", SZ, I, I, I, I, I, I)
+    d("k3d_moe_routed", I, P, P, P, P, I, P, P, P, I, I, I, I, I, F, I, F, F, I, P, SZ, P, P, P,
+      P)
+    d("k3d_moe_experts", I, P, P, P, P, I, P, I, I, I, I, I, F, F, I, P, SZ, P, P, P, P)
+    # generator
+    d("k3g_u64", C.c_uint64, C.c_uint64, C.c_uint64)
+    d("k3g_bytes", None, P, SZ, C.c_uint64)
+    d("k3g_e8m0", None, P, SZ, C.c_uint64, I, I)
+    d("k3g_normal", None, P, SZ, C.c_uint64, C.c_double, C.c_double)
+    d("k3g_bf16_normal", None, P, SZ, C.c_uint64, C.c_double, C.c_double)
+    d("k3g_expert_seed", C.c_uint64, C.c_uint64, I, I)
+    d("k3g_mxfp4_expert", None, P, P, P, P, P, P, I, I, C.c_uint64, I, I, I)
+
+
+def exported_symbols():
+    """Names this module binds; the C-ABI tests check the library exports each one."""
+    return ["k3_matmul", "k3_matmul_bf16", "k3_matmul_q8", "k3_mxfp4_dequant",
+            "k3_matmul_mxfp4", "k3_router", "k3_situ_glu", "k3_rmsnorm", "k3_moe_scratch",
+            "k3_moe", "k3_moe_prefill", "k3_expert_ffn", "k3_moe_routed", "k3_dev_register",
+            "k3_dev_unregister", "k3_dev_lookup", "k3_dev_last_error", "k3_expert_drops"]
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u8(a):
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+# ------------------------------------------------------------------ host surface ----
+def matmul(x, W):
+    W = _f32(W)
+    out, inn = W.shape
+    y = np.empty(out, np.float32)
+    lib().k3_matmul(_p(y), _p(_f32(x)), _p(W), inn, out)
+    return y
+
+
+def matmul_bf16(x, Wb):
+    Wb = np.ascontiguousarray(Wb, dtype=np.uint16)
+    out, inn = Wb.shape
+    y = np.empty(out, np.float32)
+    lib().k3_matmul_bf16(_p(y), _p(_f32(x)), _p(Wb), inn, out)
+    return y
+
+
+def matmul_q8(x, Wq, inn, out):
+    Wq = _u8(Wq)
+    y = np.empty(out, np.float32)
+    lib().k3_matmul_q8(_p(y), _p(_f32(x)), _p(Wq), inn, out)
+    return y
+
+
+def matmul_mxfp4(x, packed, scales, inn, rows, group=32):
+    y = np.empty(rows, np.float32)
+    lib().k3_matmul_mxfp4(_p(y), _p(_f32(x)), _p(_u8(packed)), _p(_u8(scales)), inn, rows, group)
+    return y
+
+
+def mxfp4_dequant(packed, scales, rows, pcols, group=32):
+    out = np.empty((rows, pcols * 2), np.float32)
+    lib().k3_mxfp4_dequant(_p(out), _p(_u8(packed)), _p(_u8(scales)), rows, pcols, group)
+    return out
+
+
+def router(x, W, bias, topk, renorm=1, routed_scale=1.0):
+    W = _f32(W)
+    n_experts, hidden = W.shape
+    idx = np.empty(topk, np.int32)
+    w = np.empty(topk, np.float32)
+    b = None if bias is None else _f32(bias)
+    lib().k3_router(_p(idx), _p(w), _p(_f32(x)), _p(W), _p(b), hidden, n_experts, topk, renorm,
+                    routed_scale)
+    return idx, w
+
+
+def situ_glu(x, n, b1=4.0, b2=25.0):
+    y = np.empty(n, np.float32)
+    lib().k3_situ_glu(_p(y), _p(_f32(x)), n, b1, b2)
+    return y
+
+
+def rmsnorm(x, w, eps):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().k3_rmsnorm(_p(y), _p(x), _p(_f32(w)), x.size, eps)
+    return y
+
+
+class Expert:
+    """One MXFP4 expert held in host memory (gate/up [inter][hidden], down [hidden][inter])."""
+
+    def __init__(self, p1, s1, p3, s3, p2, s2):
+        self.t = [_u8(a) for a in (p1, s1, p3, s3, p2, s2)]
+
+    def q(self):
+        return K3ExpertQ(*[a.ctypes.data for a in self.t])
+
+
+def gen_expert(hidden, inter, seed, expert, lo=119, hi=127):
+    pk = hidden * inter // 2
+    sc = hidden * inter // 32
+    a = [np.empty(n, np.uint8) for n in (pk, sc, pk, sc, pk, sc)]
+    lib().k3g_mxfp4_expert(*[_p(t) for t in a], hidden, inter, seed, expert, lo, hi)
+    return Expert(*a)
+
+
+def expert_ffn(x, e, hidden, inter, act=K3_ACT_SILU, b1=4.0, b2=25.0, wt=1.0):
+    out = np.empty(hidden, np.float32)
+    q = e.q()
+    lib().k3_expert_ffn(_p(out), _p(_f32(x)), C.byref(q), hidden, inter, act, b1, b2, wt)
+    return out
+
+
+def moe_routed(x, router_w, bias, bank, hidden, inter, topk, renorm=1, routed_scale=1.0,
+               act=K3_ACT_SILU, b1=4.0, b2=25.0, prec=0):
+    """bank: list of Expert (or None for a missing expert), one per expert id."""
+    x = _f32(x).reshape(-1, hidden)
+    T = x.shape[0]
+    n_experts = len(bank)
+    qs = (K3ExpertQ * n_experts)()
+    for e, ex in enumerate(bank):
+        if ex is not None:
+            qs[e] = ex.q()
+    out = np.empty((T, hidden), np.float32)
+    idx = np.empty((T, topk), np.int32)
+    wt = np.empty((T, topk), np.float32)
+    b = None if bias is None else _f32(bias)
+    lib().k3_moe_routed(_p(out), _p(idx), _p(wt), _p(x), T, _p(_f32(router_w)), _p(b), qs, hidden,
+                        inter, n_experts, topk, renorm, routed_scale, act, b1, b2, prec)
+    return out, idx, wt
+
+
+def expert_drops():
+    return C.c_long.in_dll(lib(), "k3_expert_drops").value
+
+
+def dev_register(arr):
+    rc = lib().k3_dev_register(arr.ctypes.data, arr.nbytes)
+    if rc != 0:
+        raise RuntimeError(lib().k3_dev_last_error().decode())
+
+
+def dev_unregister(arr):
+    return lib().k3_dev_unregister(arr.ctypes.data)
+
+
+# --------------------------------------------------------------------- generator ----
+def gen_bytes(n, seed):
+    a = np.empty(n, np.uint8)
+    lib().k3g_bytes(_p(a), n, seed)
+    return a
+
+
+def gen_e8m0(n, seed, lo=119, hi=127):
+    a = np.empty(n, np.uint8)
+    lib().k3g_e8m0(_p(a), n, seed, lo, hi)
+    return a
+
+
+def gen_normal(n, seed, mean=0.0, sigma=1.0):
+    a = np.empty(n, np.float32)
+    lib().k3g_normal(_p(a), n, seed, mean, sigma)
+    return a
+
+
+def gen_bf16_normal(n, seed, mean=0.0, sigma=1.0):
+    a = np.empty(n, np.uint16)
+    lib().k3g_bf16_normal(_p(a), n, seed, mean, sigma)
+    return a
+
+
+def expert_seed(seed, expert, tensor):
+    return lib().k3g_expert_seed(seed, expert, tensor)
+
+
+# ------------------------------------------------------------------ device API ----
+def check(rc, what="k3d"):
+    if rc != 0:
+        raise RuntimeError(f"{what}: {lib().k3d_error().decode()}")
+
+
+class Profile:
+    """HIP-event stage timing of the library's own launches (k3d_prof_*)."""
+
+    def __init__(self, max_marks=65536):
+        check(lib().k3d_prof_begin(max_marks), "k3d_prof_begin")
+
+    def end(self):
+        n = len(STAGES)
+        ms = (C.c_double * n)()
+        cnt = (C.c_int * n)()
+        check(lib().k3d_prof_end(ms, cnt, n), "k3d_prof_end")
+        return {STAGES[i]: (ms[i], cnt[i]) for i in range(n) if cnt[i]}
+
+
+class DevBuf:
+    """A device allocation owned by Python (k3d_malloc / k3d_free)."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = lib().k3d_malloc(self.nbytes)
+        if not self.ptr:
+            raise RuntimeError("k3d_malloc: " + lib().k3d_error().decode())
+
+    def upload(self, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        check(lib().k3d_h2d(self.ptr + offset, arr.ctypes.data, arr.nbytes, None), "h2d")
+        check(lib().k3d_sync(None), "sync")
+        return self
+
+    def download(self, arr, offset=0):
+        check(lib().k3d_d2h(arr.ctypes.data, self.ptr + offset, arr.nbytes, None), "d2h")
+        check(lib().k3d_sync(None), "sync")
+        return arr
+
+    def free(self):
+        if self.ptr:
+            lib().k3d_free(self.ptr)
+            self.ptr = None
