@@ -42,35 +42,32 @@ def log(msg):
 
 
 class Layer:
-    """The 384-expert layer resident on the device."""
+    """The 384-expert layer resident on the device, the bank in the tiled layout."""
 
-    def __init__(self):
+    def __init__(self, layout=k3amd.K3D_LAYOUT_TILED):
         L = k3amd.lib()
         k3amd.check(L.k3d_init(), "k3d_init")
-        slot = (EXPERT_BYTES + 6 * 256 + 4095) // 4096 * 4096
-        self.bank = k3amd.DevBuf(N * slot)
-        table = (k3amd.K3ExpertQ * N)()
         t0 = time.time()
-        for e in range(N):
-            ex = wl.expert(e)
-            off = e * slot
-            ptrs = []
-            for a in ex.t:
-                self.bank.upload(a, off)
-                ptrs.append(self.bank.ptr + off)
-                off += (a.nbytes + 255) // 256 * 256
-            table[e] = k3amd.K3ExpertQ(*ptrs)
-            if e % 64 == 63:
-                log(f"bench: expert bank {e + 1}/{N} resident ({time.time() - t0:.1f} s)")
-        self.table = k3amd.DevBuf(C.sizeof(table))
-        k3amd.check(L.k3d_h2d(self.table.ptr, C.addressof(table), C.sizeof(table), None))
+
+        class Lazy:                     # experts generated one at a time while uploading
+            def __len__(self):
+                return N
+
+            def __iter__(self):
+                for e in range(N):
+                    if e % 64 == 63:
+                        log(f"bench: expert bank {e + 1}/{N} resident ({time.time() - t0:.1f} s)")
+                    yield wl.expert(e)
+
+        self.layout = layout
+        self.bank = k3amd.DevBank(Lazy(), E, I, layout)
         self.router = k3amd.DevBuf(ROUTER_BYTES).upload(wl.router_weights())
 
     def run(self, x, out, idx, wt, T, ws, prec=0):
         k3amd.check(k3amd.lib().k3d_moe_routed(
-            out.ptr, idx.ptr, wt.ptr, x.ptr, T, self.router.ptr, None, self.table.ptr, E, I, N, K,
-            1, 1.0, k3amd.K3_ACT_SILU, 4.0, 25.0, prec, ws.ptr, ws.nbytes, None, None, None, None),
-            "k3d_moe_routed")
+            out.ptr, idx.ptr, wt.ptr, x.ptr, T, self.router.ptr, None, self.bank.table.ptr,
+            self.layout, E, I, N, K, 1, 1.0, k3amd.K3_ACT_SILU, 4.0, 25.0, prec, ws.ptr, ws.nbytes,
+            None, None, None, None), "k3d_moe_routed")
 
 
 def time_layer(layer, T, steps, warmup, nbatch=4):

@@ -60,24 +60,36 @@ int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const
                int hidden, int n_experts, int topk, int renorm, float routed_scale, void *ws,
                size_t ws_bytes, void *stream);
 
+/* Device layouts of an expert bank's MXFP4 matrices.
+ *   K3D_LAYOUT_ROWS:  the reference's, packed [rows][in/2] + scales [rows][in/32] bytes.
+ *   K3D_LAYOUT_TILED: the same bytes regrouped per tile of 16 rows x 512 columns in the
+ *     order the expert kernel reads them (k3d_mxfp4_tile); rows are padded to a multiple
+ *     of 16, in must be a multiple of 512. Same arithmetic, results bit-identical to ROWS;
+ *     the expert kernel streams it at a higher fraction of HBM bandwidth. */
+enum { K3D_LAYOUT_ROWS = 0, K3D_LAYOUT_TILED = 1 };
+int k3d_mxfp4_tiled_size(int rows, int in, size_t *packed_bytes, size_t *scales_bytes);
+int k3d_mxfp4_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
+                   const uint8_t *scales, int rows, int in, void *stream);
+
 /* The routed MoE layer (k3_moe's routed loop, reference k3_ops.c:576-643, with z := x),
  * expert-major. bank is a DEVICE array of n_experts K3ExpertQ (k3.h) whose pointers are
- * device pointers; an entry with a NULL pointer is a dropped expert. perm_out (T*topk) and
+ * device pointers, in the given layout; an entry with a NULL pointer is a dropped expert.
+ * hidden and inter: multiples of 32 (ROWS) or of 512 (TILED). perm_out (T*topk) and
  * offsets_out (n_experts+1), when not NULL, receive the gather permutation. *drops_out,
  * when not NULL, receives (after the stream reaches it) the number of dropped
  * assignments; it must be a device int. */
 size_t k3d_moe_ws(int T, int hidden, int inter, int n_experts, int topk, int prec);
 int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T,
-                   const float *router_w, const float *bias, const void *bank, int hidden,
-                   int inter, int n_experts, int topk, int renorm, float routed_scale, int act,
-                   float b1, float b2, int prec, void *ws, size_t ws_bytes, int *perm_out,
-                   int *offsets_out, int *drops_out, void *stream);
+                   const float *router_w, const float *bias, const void *bank, int layout,
+                   int hidden, int inter, int n_experts, int topk, int renorm, float routed_scale,
+                   int act, float b1, float b2, int prec, void *ws, size_t ws_bytes,
+                   int *perm_out, int *offsets_out, int *drops_out, void *stream);
 
 /* The expert half of the layer for a routing already in idx/wt (device). */
 int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x, int T,
-                    const void *bank, int hidden, int inter, int n_experts, int topk, int act,
-                    float b1, float b2, int prec, void *ws, size_t ws_bytes, int *perm_out,
-                    int *offsets_out, int *drops_out, void *stream);
+                    const void *bank, int layout, int hidden, int inter, int n_experts, int topk,
+                    int act, float b1, float b2, int prec, void *ws, size_t ws_bytes,
+                    int *perm_out, int *offsets_out, int *drops_out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -86,6 +86,54 @@ __device__ __forceinline__ k3_bf16x8 k3_dequant8_bf16(uint32_t codes, float scal
     return r;
 }
 
+/* Loads through explicitly global (address space 1) pointers. Pointers read from memory
+ * (the expert table) or carried in a struct argument are generic to the compiler, which
+ * would otherwise emit flat loads; a flat load also counts against lgkmcnt, so every wait
+ * for an LDS read would drain all outstanding weight loads. */
+typedef __attribute__((address_space(1))) const uint4 k3_g_uint4;
+typedef __attribute__((address_space(1))) const uint8_t k3_g_u8;
+typedef __attribute__((address_space(1))) const uint16_t k3_g_u16;
+typedef __attribute__((address_space(1))) const float k3_g_f32;
+typedef __attribute__((address_space(1))) const int k3_g_int;
+
+__device__ __forceinline__ uint4 k3_ldg16(const void *p)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    k3_g_uint4 *gp = (k3_g_uint4 *)p;
+    return make_uint4(gp->x, gp->y, gp->z, gp->w);
+#else
+    (void)p;
+    return make_uint4(0, 0, 0, 0);
+#endif
+}
+
+/* Buffer loads: a wave-uniform descriptor (base, size in bytes) and a per-lane 32-bit byte
+ * offset. They count against vmcnt only, and a load past `bytes` returns zeros. The third
+ * descriptor word 0x00020000 is the raw-buffer format of the gfx9 family. */
+typedef __amdgpu_buffer_rsrc_t k3_rsrc;
+
+__device__ __forceinline__ k3_rsrc k3_make_rsrc(const void *base, uint32_t bytes)
+{
+    /* The caller guarantees base and bytes are wave-uniform. Pointers read from memory
+     * through a generic pointer (the expert table) are divergent to the compiler, which
+     * would then wrap every load in a readfirstlane loop; reading lane 0 here makes the
+     * descriptor scalar. */
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    void *ub = (void *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(ub, 0, __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ uint4 k3_bload16(k3_rsrc r, uint32_t off)
+{
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t k3_bload4(k3_rsrc r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
 __device__ __forceinline__ k3_bf16x8 k3_as_bf16x8(uint4 v)
 {
     return __builtin_bit_cast(k3_bf16x8, v);

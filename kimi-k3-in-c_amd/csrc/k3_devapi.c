@@ -198,12 +198,19 @@ typedef struct {
     int max_passes;
 } MoeWs;
 
+/* Tokens per expert pass: the LDS-staged expert kernel (8) needs both matrix widths to be
+ * multiples of 512; other shapes run the register-fed kernel (16, row-major bank only). */
+static int moe_pass_tok(int hidden, int inter)
+{
+    return (hidden % 512 == 0 && inter % 512 == 0) ? 8 : 16;
+}
+
 static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n_experts, int topk,
                          int prec)
 {
     const size_t N = (size_t)T * topk;
     const int maxjobs = (int)(N < (size_t)n_experts ? N : (size_t)n_experts);
-    w->max_passes = maxjobs + (int)(N / 16) + 1;
+    w->max_passes = maxjobs + (int)(N / (size_t)moe_pass_tok(hidden, inter)) + 1;
     w->xhi = (uint16_t *)take(c, (size_t)T * hidden * 2);
     w->xlo = prec == 0 ? (uint16_t *)take(c, (size_t)T * hidden * 2) : NULL;
     w->ahi = (uint16_t *)take(c, N * inter * 2);
@@ -230,21 +237,46 @@ size_t k3d_moe_ws(int T, int hidden, int inter, int n_experts, int topk, int pre
     return c.off;
 }
 
+static int moe_check(const char *fn, int hidden, int inter, int topk, int layout)
+{
+    static char msg[160];
+    if ((hidden % 32) || (inter % 32)) {
+        snprintf(msg, sizeof msg, "%s: hidden and inter must be multiples of 32", fn);
+        return bad(msg);
+    }
+    if (topk < 1 || topk > K3_MAX_TOPK) {
+        snprintf(msg, sizeof msg, "%s: topk outside 1..64", fn);
+        return bad(msg);
+    }
+    if (layout != K3D_LAYOUT_ROWS && layout != K3D_LAYOUT_TILED) {
+        snprintf(msg, sizeof msg, "%s: unknown bank layout %d", fn, layout);
+        return bad(msg);
+    }
+    if (layout == K3D_LAYOUT_TILED && moe_pass_tok(hidden, inter) != 8) {
+        snprintf(msg, sizeof msg, "%s: a tiled bank needs hidden and inter multiples of 512", fn);
+        return bad(msg);
+    }
+    return 0;
+}
+
 static int moe_experts_ws(float *out, const int *idx, const float *wt, const float *x, int T,
-                          const void *bank, int hidden, int inter, int n_experts, int topk,
-                          int act, float b1, float b2, int prec, const MoeWs *w, int *perm_out,
-                          int *offsets_out, int *drops_out, void *stream)
+                          const void *bank, int layout, int hidden, int inter, int n_experts,
+                          int topk, int act, float b1, float b2, int prec, const MoeWs *w,
+                          int *perm_out, int *offsets_out, int *drops_out, void *stream)
 {
     int *perm = perm_out ? perm_out : w->perm;
     int *offsets = offsets_out ? offsets_out : w->offsets;
+    const int pass_tok = moe_pass_tok(hidden, inter);
     if (k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
     if (k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
-                   w->counts, idx, T, topk, n_experts, bank, 16, stream))
+                   w->counts, idx, T, topk, n_experts, bank, pass_tok, stream))
         return fail("gather");
     k3k_prof_mark(stream, K3D_STAGE_GATHER);
     K3kMxArgs a;
     memset(&a, 0, sizeof a);
     a.bank = bank;
+    a.pass_tok = pass_tok;
+    a.layout = layout;
     a.job_expert = w->job_expert;
     a.job_off = w->job_off;
     a.job_cnt = w->job_cnt;
@@ -265,6 +297,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     a.alo = w->alo;
     a.rows = inter;
     a.K = hidden;
+    a.n_xrows = T;
     if (k3k_mx_gemm(K3K_MX_GATEUP, &a, stream)) return fail("mx_gemm gateup");
     k3k_prof_mark(stream, K3D_STAGE_GATEUP);
     /* down: K = inter, rows = hidden, activations are the assignments */
@@ -273,6 +306,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     a.out = w->contrib;
     a.rows = hidden;
     a.K = inter;
+    a.n_xrows = T * topk;
     if (k3k_mx_gemm(K3K_MX_DOWN, &a, stream)) return fail("mx_gemm down");
     k3k_prof_mark(stream, K3D_STAGE_DOWN);
     if (k3k_combine(out, w->contrib, wt, idx, bank, n_experts, T, topk, hidden, stream)) return fail("combine");
@@ -282,32 +316,32 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
 }
 
 int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x, int T,
-                    const void *bank, int hidden, int inter, int n_experts, int topk, int act,
-                    float b1, float b2, int prec, void *ws, size_t ws_bytes, int *perm_out,
-                    int *offsets_out, int *drops_out, void *stream)
+                    const void *bank, int layout, int hidden, int inter, int n_experts, int topk,
+                    int act, float b1, float b2, int prec, void *ws, size_t ws_bytes,
+                    int *perm_out, int *offsets_out, int *drops_out, void *stream)
 {
     if (T <= 0) return 0;
-    if ((hidden % 32) || (inter % 32)) return bad("k3d_moe_experts: hidden and inter must be multiples of 32");
-    if (topk < 1 || topk > K3_MAX_TOPK) return bad("k3d_moe_experts: topk outside 1..64");
+    int rc = moe_check("k3d_moe_experts", hidden, inter, topk, layout);
+    if (rc) return rc;
     if (ws_bytes < k3d_moe_ws(T, hidden, inter, n_experts, topk, prec))
         return bad("k3d_moe_experts: workspace too small");
     Carve c = {(char *)ws, 0};
     MoeWs w;
     moe_layout(&c, &w, T, hidden, inter, n_experts, topk, prec);
     k3k_prof_mark(stream, K3D_STAGE_BEGIN);
-    return moe_experts_ws(out, idx, wt, x, T, bank, hidden, inter, n_experts, topk, act, b1, b2,
-                          prec, &w, perm_out, offsets_out, drops_out, stream);
+    return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
+                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, stream);
 }
 
 int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const float *router_w,
-                   const float *bias, const void *bank, int hidden, int inter, int n_experts,
-                   int topk, int renorm, float routed_scale, int act, float b1, float b2, int prec,
-                   void *ws, size_t ws_bytes, int *perm_out, int *offsets_out, int *drops_out,
-                   void *stream)
+                   const float *bias, const void *bank, int layout, int hidden, int inter,
+                   int n_experts, int topk, int renorm, float routed_scale, int act, float b1,
+                   float b2, int prec, void *ws, size_t ws_bytes, int *perm_out, int *offsets_out,
+                   int *drops_out, void *stream)
 {
     if (T <= 0) return 0;
-    if ((hidden % 32) || (inter % 32)) return bad("k3d_moe_routed: hidden and inter must be multiples of 32");
-    if (topk < 1 || topk > K3_MAX_TOPK) return bad("k3d_moe_routed: topk outside 1..64");
+    int rc = moe_check("k3d_moe_routed", hidden, inter, topk, layout);
+    if (rc) return rc;
     if (ws_bytes < k3d_moe_ws(T, hidden, inter, n_experts, topk, prec))
         return bad("k3d_moe_routed: workspace too small");
     Carve c = {(char *)ws, 0};
@@ -326,6 +360,23 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
                          renorm, routed_scale, exc, nexc, stream))
         return fail("router_final");
     k3k_prof_mark(stream, K3D_STAGE_ROUTER);
-    return moe_experts_ws(out, idx, wt, x, T, bank, hidden, inter, n_experts, topk, act, b1, b2,
-                          prec, &w, perm_out, offsets_out, drops_out, stream);
+    return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
+                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, stream);
+}
+
+/* ---- tiled expert layout ---------------------------------------------------------------- */
+int k3d_mxfp4_tiled_size(int rows, int in, size_t *packed_bytes, size_t *scales_bytes)
+{
+    if (rows <= 0 || in <= 0 || in % 512) return bad("k3d_mxfp4_tiled_size: need rows > 0 and in % 512 == 0");
+    const size_t prow = ((size_t)rows + 15) / 16 * 16;
+    if (packed_bytes) *packed_bytes = prow * (size_t)in / 2;
+    if (scales_bytes) *scales_bytes = prow * (size_t)in / 32;
+    return 0;
+}
+
+int k3d_mxfp4_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
+                   const uint8_t *scales, int rows, int in, void *stream)
+{
+    if (rows <= 0 || in <= 0 || in % 512) return bad("k3d_mxfp4_tile: need rows > 0 and in % 512 == 0");
+    return k3k_mx_tile(tpacked, tscales, packed, scales, rows, in, stream) ? fail("mx_tile") : 0;
 }

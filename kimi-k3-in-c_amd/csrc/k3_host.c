@@ -415,8 +415,9 @@ static void run_bank(float *out_d, const int *idx, const int *idx_d, const float
     if ((hidden % 32) == 0 && (inter % 32) == 0) {
         void *bank_d = upload(B_BANK, bank, (size_t)n_experts * sizeof(QPtr));
         const size_t wsb = k3d_moe_ws(T, hidden, inter, n_experts, topk, prec);
-        check(k3d_moe_experts(out_d, idx_d, wt_d, x_d, T, bank_d, hidden, inter, n_experts, topk,
-                              act, b1, b2, prec, buf(B_WS, wsb), wsb, NULL, NULL, NULL, g_stream),
+        check(k3d_moe_experts(out_d, idx_d, wt_d, x_d, T, bank_d, K3D_LAYOUT_ROWS, hidden, inter,
+                              n_experts, topk, act, b1, b2, prec, buf(B_WS, wsb), wsb, NULL, NULL,
+                              NULL, g_stream),
               "moe experts");
     } else {
         experts_generic(out_d, idx, wt_d, idx_d, x_d, T, bank, hidden, inter, n_experts, topk, act,

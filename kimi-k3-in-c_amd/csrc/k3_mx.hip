@@ -53,7 +53,7 @@ struct ExpertQDev {
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p)
 {
-    return *reinterpret_cast<const uint4 *>(p);
+    return k3_ldg16(p);
 }
 
 template <int MODE, int MT, int NT, int NS, int DEPTH, int MAXW>
@@ -147,18 +147,18 @@ __global__ __launch_bounds__(64 * MAXW) void mx_gemm_kernel(K3kMxArgs a, int kw)
 #pragma unroll
                 for (int m = 0; m < MT; m++) {
                     q[d][m] = v ? ld16(pa[m] + (size_t)blk * 16) : make_uint4(0, 0, 0, 0);
-                    sc[d][m] = v ? (uint32_t)sa[m][blk] : 127u;
+                    sc[d][m] = v ? (uint32_t)((k3_g_u8 *)sa[m])[blk] : 127u;
                 }
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
                     const bool ok = v && tv[nt];
-                    const uint4 *ph = reinterpret_cast<const uint4 *>(xh[nt] + (size_t)blk * 32);
 #pragma unroll
-                    for (int p = 0; p < 4; p++) bh[d][nt][p] = ok ? ph[p] : make_uint4(0, 0, 0, 0);
+                    for (int p = 0; p < 4; p++)
+                        bh[d][nt][p] = ok ? k3_ldg16(xh[nt] + (size_t)blk * 32 + 8 * p) : make_uint4(0, 0, 0, 0);
                     if (NS == 2) {
-                        const uint4 *pl = reinterpret_cast<const uint4 *>(xl[nt] + (size_t)blk * 32);
 #pragma unroll
-                        for (int p = 0; p < 4; p++) bl[d][nt][p] = ok ? pl[p] : make_uint4(0, 0, 0, 0);
+                        for (int p = 0; p < 4; p++)
+                            bl[d][nt][p] = ok ? k3_ldg16(xl[nt] + (size_t)blk * 32 + 8 * p) : make_uint4(0, 0, 0, 0);
                     }
                 }
             }
@@ -247,6 +247,251 @@ int launch_mx(const K3kMxArgs *a, int kw, int grid, hipStream_t st)
     return 0;
 }
 
+/* ---- expert jobs, LDS-staged activations ---------------------------------------------
+ * mx_moe_kernel: the GATEUP / DOWN modes in passes of up to PT tokens, K % 512 == 0.
+ *
+ * A workgroup of NW waves takes one item = (pass, row block); the waves own consecutive
+ * row tiles (MT tiles of 16 rows each) and walk K in chunks of 512 elements (16 MX
+ * blocks = 4 steps of 128). K order inside a chunk: at step d, lane group g (lanes
+ * 16g..16g+15) holds MX block 4d+g of its row (the MFMA's K permutation is free as long
+ * as A and B agree). Weights come in one of two layouts:
+ *   LAYOUT 0, row-major (the reference's): per step a lane loads its block's 16 bytes
+ *     (a wave: 16 rows x 64 contiguous bytes), per chunk one 16-byte load of the row's
+ *     16 scale bytes, of which it uses one per step;
+ *   LAYOUT 1, tiled (mx_tile_kernel): the bytes of a 16-row tile's chunk stored in lane
+ *     order, so a wave's load is 1 KB contiguous and a lane's four scale bytes of the
+ *     chunk are one 4-byte load.
+ * The pass's activation rows (hi, lo) for the chunk are staged once in LDS by the whole
+ * workgroup (double buffered), one wave-uniform row-half per wave instruction and only for
+ * the pass's real tokens; B lanes of token columns past the pass read a row of zeros.
+ * While chunk c is multiplied, the weight/scale loads and the activation loads of chunk
+ * c+1 are in flight (activations issued first, so waiting for them leaves the weight
+ * loads outstanding).
+ */
+template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
+void mx_moe_kernel(K3kMxArgs a)
+{
+    constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
+    constexpr int KC = 512, SPC = 4, LDT = KC + 8;           /* LDS row: 16-byte pad */
+    constexpr int NRH = PT * NS;                             /* staged row-halves per chunk */
+    constexpr int PPW = (NRH + NW - 1) / NW;                 /* row-halves per wave */
+    /* row PT of each buffer/half stays zero: the B operand of absent token columns */
+    __shared__ __attribute__((aligned(16))) uint16_t bsh[2][NS][PT + 1][LDT];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int K = a.K, nblk = K >> 5, nchunk = nblk >> 4;
+    const int rows = a.rows;
+    const uint32_t rstride = (uint32_t)K >> 1;
+    const int rpw = 16 * RT, rpg = NW * rpw;
+    const int n_rb = (rows + rpg - 1) / rpg;
+    const int n_items = (*a.n_passes) * n_rb;
+    /* requires K % 512 == 0: the host routes other K to mx_gemm_kernel */
+
+    for (int i = tid; i < 2 * NS * LDT / 8; i += 64 * NW) {
+        const int bh = i / (LDT / 8), o = i % (LDT / 8);
+        *reinterpret_cast<uint4 *>(&bsh[bh / NS][bh % NS][PT][o * 8]) = make_uint4(0, 0, 0, 0);
+    }
+
+    for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+        const int rb = item % n_rb, pass = item / n_rb;
+        const int j = a.pass_job[pass];
+        const int e = a.job_expert[j];
+        const int off = a.job_off[j];
+        const int tok0 = a.pass_tp[pass] * PT;
+        const int ntok = min(PT, a.job_cnt[j] - tok0);
+        const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[e];
+        /* one buffer descriptor per matrix (wave-uniform); per-lane byte offsets */
+        const uint32_t prow = LAYOUT == 0 ? (uint32_t)rows : (uint32_t)((rows + 15) & ~15);
+        const uint32_t pbytes = prow * rstride, sbytes = prow * nblk;
+        k3_rsrc rp0, rp1, rs0, rs1;
+        if (MODE == K3K_MX_GATEUP) {
+            rp0 = k3_make_rsrc(q.p1, pbytes); rs0 = k3_make_rsrc(q.s1, sbytes);
+            rp1 = k3_make_rsrc(q.p3, pbytes); rs1 = k3_make_rsrc(q.s3, sbytes);
+        } else {
+            rp0 = rp1 = k3_make_rsrc(q.p2, pbytes);
+            rs0 = rs1 = k3_make_rsrc(q.s2, sbytes);
+        }
+        uint32_t poff[MT], soff[MT];
+        const int ntile = (rows + 15) >> 4;
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            const int mt = (MODE == K3K_MX_GATEUP) ? (m % RT) : m;
+            if (LAYOUT == 0) {
+                const int r = min(rb * rpg + wv * rpw + 16 * mt + r16, rows - 1);
+                poff[m] = (uint32_t)r * rstride + (uint32_t)g * 16u;
+                soff[m] = (uint32_t)r * (uint32_t)nblk;
+            } else {
+                const int t = min((rb * rpg + wv * rpw) / 16 + mt, ntile - 1);
+                poff[m] = (uint32_t)t * (uint32_t)nchunk * 4096u + (uint32_t)lane * 16u;
+                soff[m] = (uint32_t)t * (uint32_t)nchunk * 256u + (uint32_t)lane * 4u;
+            }
+        }
+        /* staging: wave wv copies row-halves wv, wv+NW, ...; lane = 16-byte piece */
+        const uint32_t xbytes = (uint32_t)a.n_xrows * (uint32_t)K * 2u;
+        const k3_rsrc rxh = k3_make_rsrc(a.xhi, xbytes);
+        const k3_rsrc rxl = k3_make_rsrc(NS == 2 ? a.xlo : a.xhi, xbytes);
+        uint32_t gsrc[PPW];
+#pragma unroll
+        for (int i = 0; i < PPW; i++) {
+            const int rh = wv + NW * i, p = rh / NS;
+            gsrc[i] = 0;
+            if (rh < NRH && p < ntok) {
+                const int ar = a.perm[off + tok0 + p];
+                const int xr = (MODE == K3K_MX_GATEUP) ? ar / a.topk : ar;
+                gsrc[i] = ((uint32_t)xr * (uint32_t)K + (uint32_t)lane * 8u) * 2u;
+            }
+        }
+        const int brow = r16 < ntok ? r16 : PT;
+
+        k3_f32x4 acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; m++) acc[m] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
+
+        /* One register set per step of a chunk: step d's weights for chunk c+1 are loaded
+         * into qa[d] right after step d of chunk c has consumed them. */
+        uint4 qa[SPC][MT];
+        uint32_t sq[MT * (LAYOUT == 0 ? 4 : 1)], sqn[MT * (LAYOUT == 0 ? 4 : 1)];
+        uint4 bst[PPW];
+
+        auto load_b = [&](int c) {
+#pragma unroll
+            for (int i = 0; i < PPW; i++) {
+                const int rh = wv + NW * i;
+                if (rh < NRH && rh / NS < ntok)
+                    bst[i] = k3_bload16(rh % NS ? rxl : rxh, gsrc[i] + (uint32_t)c * KC * 2u);
+            }
+        };
+        auto store_b = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < PPW; i++) {
+                const int rh = wv + NW * i;
+                if (rh < NRH && rh / NS < ntok)
+                    *reinterpret_cast<uint4 *>(&bsh[buf][rh % NS][rh / NS][lane * 8]) = bst[i];
+            }
+        };
+        auto load_step = [&](int c, int d) {
+            const uint32_t bo = LAYOUT == 0 ? (uint32_t)c * 256u + (uint32_t)d * 64u
+                                            : ((uint32_t)c * 4u + (uint32_t)d) * 1024u;
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                qa[d][m] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo);
+        };
+        auto load_scales = [&](int c, uint32_t *ss) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const k3_rsrc rs = m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1;
+                if (LAYOUT == 0) {
+                    const uint4 v = k3_bload16(rs, soff[m] + (uint32_t)c * 16u);
+                    ss[4 * m] = v.x; ss[4 * m + 1] = v.y; ss[4 * m + 2] = v.z; ss[4 * m + 3] = v.w;
+                } else {
+                    ss[m] = k3_bload4(rs, soff[m] + (uint32_t)c * 256u);
+                }
+            }
+        };
+
+        load_b(0);
+        load_scales(0, sq);
+#pragma unroll
+        for (int d = 0; d < SPC; d++) load_step(0, d);
+        store_b(0);
+        __syncthreads();
+        for (int c = 0; c < nchunk; c++) {
+            const int buf = c & 1;
+            const bool more = c + 1 < nchunk;
+            if (more) {
+                load_b(c + 1);
+                load_scales(c + 1, sqn);
+            }
+#pragma unroll
+            for (int d = 0; d < SPC; d++) {
+                /* B operand: token column r16 (or the zero row), block 4g+d of the chunk */
+                uint4 bh[4], bl[4];
+                const uint4 *bp = reinterpret_cast<const uint4 *>(&bsh[buf][0][brow][(4 * d + g) * 32]);
+                const uint4 *bq = reinterpret_cast<const uint4 *>(&bsh[buf][NS - 1][brow][(4 * d + g) * 32]);
+#pragma unroll
+                for (int pp = 0; pp < 4; pp++) {
+                    bh[pp] = bp[pp];
+                    if (NS == 2) bl[pp] = bq[pp];
+                }
+                uint4 qq[MT];
+                float so[MT];
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    const uint32_t sraw = LAYOUT == 0 ? (sq[4 * m + d] >> (8 * g)) & 0xFFu
+                                                      : (sq[m] >> (8 * d)) & 0xFFu;
+                    const bool nanb = sraw == 255u;          /* NaN byte: the block is 0 */
+                    qq[m] = qa[d][m];
+                    qq[m].x = nanb ? 0u : qq[m].x;
+                    qq[m].y = nanb ? 0u : qq[m].y;
+                    qq[m].z = nanb ? 0u : qq[m].z;
+                    qq[m].w = nanb ? 0u : qq[m].w;
+                    so[m] = k3_e8m0_operand(nanb ? 127u : sraw);
+                }
+#pragma unroll
+                for (int m = 0; m < MT; m++)
+#pragma unroll
+                    for (int pp = 0; pp < 4; pp++) {
+                        const uint32_t codes = pp == 0 ? qq[m].x : pp == 1 ? qq[m].y : pp == 2 ? qq[m].z : qq[m].w;
+                        const k3_bf16x8 av = k3_dequant8_bf16(codes, so[m]);
+                        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh[pp]), acc[m], 0, 0, 0);
+                        if (NS == 2)
+                            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl[pp]), acc[m], 0, 0, 0);
+                    }
+                if (more) load_step(c + 1, d);
+            }
+            if (more) {
+                store_b(buf ^ 1);
+#pragma unroll
+                for (int m = 0; m < MT * (LAYOUT == 0 ? 4 : 1); m++) sq[m] = sqn[m];
+            }
+            __syncthreads();
+        }
+
+        /* epilogue: lane holds token column r16, rows 4g..4g+3 of each tile */
+        if (r16 < ntok) {
+            const int orow = a.perm[off + tok0 + r16];
+            for (int m = 0; m < RT; m++) {
+                const int base = rb * rpg + wv * rpw + 16 * m + 4 * g;
+                if (MODE == K3K_MX_GATEUP) {
+                    uint16_t hi[4], lo[4];
+                    for (int jj = 0; jj < 4; jj++) {
+                        const float v = k3_act_pair(acc[m][jj], acc[m + RT][jj], a.act, a.b1, a.b2);
+                        k3_split2(v, hi[jj], lo[jj]);
+                    }
+                    uint16_t *oh = a.ahi + (size_t)orow * rows;
+                    uint16_t *ol = a.alo ? a.alo + (size_t)orow * rows : nullptr;
+                    for (int jj = 0; jj < 4; jj++)
+                        if (base + jj < rows) {
+                            oh[base + jj] = hi[jj];
+                            if (ol) ol[base + jj] = lo[jj];
+                        }
+                } else {
+                    float *o = a.out + (size_t)orow * rows;
+                    if (base + 3 < rows && (rows & 3) == 0) {
+                        *reinterpret_cast<float4 *>(o + base) =
+                            make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+                    } else {
+                        for (int jj = 0; jj < 4; jj++)
+                            if (base + jj < rows) o[base + jj] = acc[m][jj];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT>
+int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
+{
+    hipLaunchKernelGGL((mx_moe_kernel<MODE, MT, NS, PT, NW, WPE, LAYOUT>), dim3(grid), dim3(64 * NW),
+                       0, st, *a);
+    K3K_LAUNCH_CHECK("mx_moe launch");
+    return 0;
+}
+
 /* ---- generic vector-unit GEMV: any even K, group <= 64, fp32 arithmetic ---------- */
 /* One wave per row; lane-strided elements, weight = E2M1 * 2^(s-127) in fp32 (exact),
  * fp32 fma accumulation, butterfly reduction. */
@@ -287,6 +532,38 @@ __global__ void mx_dequant_kernel(float *out, const uint8_t *packed, const uint8
     }
 }
 
+/* Row-major MXFP4 -> the tiled layout read by mx_moe_kernel<..., LAYOUT=1>. For row tile t
+ * (16 rows), K chunk c (16 blocks of 32) and lane l = 16g + r (r = row in tile):
+ *   codes:  tpacked[((t*nchunk + c)*4 + d)*1024 + 16l ..+16] = block 4d+g of row 16t+r
+ *   scales: tscales[(t*nchunk + c)*256 + 4l + d]             = scale of that block
+ * Rows past `rows` (padding of the last tile) are zero codes with scale byte 0. */
+__global__ void mx_tile_kernel(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
+                               const uint8_t *scales, int rows, int K)
+{
+    const int nchunk = K / 512, nblk = K / 32, ntile = (rows + 15) / 16;
+    const size_t n = (size_t)ntile * nchunk * 64;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int l = (int)(i & 63);
+        const size_t tc = i >> 6;                          /* t*nchunk + c */
+        const int c = (int)(tc % nchunk), t = (int)(tc / nchunk);
+        const int r = l & 15, g = l >> 4, row = 16 * t + r;
+        uint32_t sw = 0;
+        for (int d = 0; d < 4; d++) {
+            const int blk = c * 16 + 4 * d + g;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            uint32_t sb = 0;
+            if (row < rows) {
+                v = *reinterpret_cast<const uint4 *>(packed + (size_t)row * (K / 2) + (size_t)blk * 16);
+                sb = scales[(size_t)row * nblk + blk];
+            }
+            *reinterpret_cast<uint4 *>(tpacked + ((tc * 4 + d) * 1024) + (size_t)l * 16) = v;
+            sw |= sb << (8 * d);
+        }
+        *reinterpret_cast<uint32_t *>(tscales + tc * 256 + (size_t)l * 4) = sw;
+    }
+}
+
 }  // namespace
 
 extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
@@ -306,6 +583,29 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
         if (a->nsplit == 2) return launch_mx<K3K_MX_PLAIN, 1, 1, 2, 2, 16>(a, kw, grid, st);
         return launch_mx<K3K_MX_PLAIN, 1, 1, 1, 2, 16>(a, kw, grid, st);
     }
+    if (a->pass_tok == 8) {
+        /* LDS-staged expert kernel: K % 512 == 0; 4 waves x 4 tiles of 16 rows per item */
+        if (a->K % 512) return k3k_fail("mx_moe: K % 512 != 0", hipErrorInvalidValue);
+        const int rpg = mode == K3K_MX_GATEUP ? 128 : 256;
+        const long items = (long)a->max_passes * ((a->rows + rpg - 1) / rpg);
+        const int grid = (int)(items < (long)cus * 4 ? (items > 0 ? items : 1) : (long)cus * 4);
+        const bool tiled = a->layout == 1;
+        if (mode == K3K_MX_GATEUP) {
+            if (a->nsplit == 2)
+                return tiled ? launch_moe<K3K_MX_GATEUP, 4, 2, 8, 4, 2, 1>(a, grid, st)
+                             : launch_moe<K3K_MX_GATEUP, 4, 2, 8, 4, 2, 0>(a, grid, st);
+            return tiled ? launch_moe<K3K_MX_GATEUP, 4, 1, 8, 4, 2, 1>(a, grid, st)
+                         : launch_moe<K3K_MX_GATEUP, 4, 1, 8, 4, 2, 0>(a, grid, st);
+        }
+        if (a->nsplit == 2)
+            return tiled ? launch_moe<K3K_MX_DOWN, 4, 2, 8, 4, 2, 1>(a, grid, st)
+                         : launch_moe<K3K_MX_DOWN, 4, 2, 8, 4, 2, 0>(a, grid, st);
+        return tiled ? launch_moe<K3K_MX_DOWN, 4, 1, 8, 4, 2, 1>(a, grid, st)
+                     : launch_moe<K3K_MX_DOWN, 4, 1, 8, 4, 2, 0>(a, grid, st);
+    }
+    if (a->pass_tok != 16 || a->layout != 0)
+        return k3k_fail("mx_gemm: expert passes of 16 tokens need the row-major layout",
+                        hipErrorInvalidValue);
     /* Expert jobs: 16 output rows per item (GATEUP: 16 gate + the same 16 up rows). */
     const int n_rb = mode == K3K_MX_GATEUP ? (a->rows + 15) / 16 : (a->rows + 31) / 32;
     const long items = (long)a->max_passes * n_rb;
@@ -319,6 +619,19 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
     }
     if (a->nsplit == 2) return launch_mx<K3K_MX_DOWN, 2, 1, 2, 2, 8>(a, kw, (int)grid, st);
     return launch_mx<K3K_MX_DOWN, 2, 1, 1, 2, 8>(a, kw, (int)grid, st);
+}
+
+extern "C" int k3k_mx_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
+                           const uint8_t *scales, int rows, int K, void *stream)
+{
+    if (rows <= 0) return 0;
+    if (K <= 0 || K % 512) return k3k_fail("mx_tile: K % 512 != 0", hipErrorInvalidValue);
+    const size_t n = (size_t)((rows + 15) / 16) * (K / 512) * 64;
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(mx_tile_kernel, dim3(blocks < 16384 ? (unsigned)blocks : 16384u), dim3(256),
+                       0, (hipStream_t)stream, tpacked, tscales, packed, scales, rows, K);
+    K3K_LAUNCH_CHECK("mx_tile launch");
+    return 0;
 }
 
 extern "C" int k3k_mx_gemv_valu(float *y, const float *x, const uint8_t *packed,

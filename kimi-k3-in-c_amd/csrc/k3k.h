@@ -57,8 +57,11 @@ typedef struct {
     const uint16_t *xhi, *xlo;          /* [ntok][K] */
     float *y;                           /* [ntok][ldy] */
     int ntok, ldy;
-    /* GATEUP / DOWN: jobs from the gather. A pass is up to 16 tokens of one job. */
+    /* GATEUP / DOWN: jobs from the gather. A pass is up to pass_tok tokens of one job:
+     * 16 (any K % 32 == 0, row-major bank) or 8 (K % 512 == 0, either bank layout). */
     const void *bank;                   /* device K3ExpertQ[n_experts] */
+    int pass_tok;
+    int layout;                         /* 0: row-major bank, 1: tiled (k3k_mx_tile) */
     const int *job_expert, *job_off, *job_cnt;
     const int *pass_job, *pass_tp, *n_passes;
     const int *perm;                    /* sorted position -> assignment a = t*topk + j */
@@ -69,10 +72,16 @@ typedef struct {
     float b1, b2;
     /* shape */
     int rows, K, nsplit;
+    int n_xrows;                        /* rows of the activation arrays (xhi/xlo) */
     int max_passes;                     /* host-side bound on *n_passes (grid sizing) */
 } K3kMxArgs;
 
 int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
+
+/* Row-major MXFP4 matrix [rows][K] (K % 512 == 0) -> the tiled layout of the expert kernel:
+ * tpacked [ceil(rows/16)*16][K/2] bytes, tscales [ceil(rows/16)*16][K/32] bytes. */
+int k3k_mx_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed, const uint8_t *scales,
+                int rows, int K, void *stream);
 
 /* Generic fp32-exact MXFP4 GEMV on the vector units for any even K and group <= 64
  * (y[rows] = W x, one token). Used where the MFMA path's shape assumptions fail. */

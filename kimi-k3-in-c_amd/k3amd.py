@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(HERE, "libk3amd.so")
 K3_WF32, K3_WBF16, K3_WI8 = 0, 1, 2
 K3_ACT_SITU, K3_ACT_SILU = 0, 1
 K3_MAX_TOPK = 64
+K3D_LAYOUT_ROWS, K3D_LAYOUT_TILED = 0, 1
 STAGES = ("begin", "router", "gather", "gateup", "down", "combine", "gemv")
 
 _lib = None
@@ -114,9 +115,11 @@ def _declare(L):
     d("k3d_router_ws", SZ, I, I, I)
     d("k3d_router", I, P, P, P, I, P, P, I, I, I, I, F, P, SZ, P)
     d("k3d_moe_ws", SZ, I, I, I, I, I, I)
-    d("k3d_moe_routed", I, P, P, P, P, I, P, P, P, I, I, I, I, I, F, I, F, F, I, P, SZ, P, P, P,
-      P)
-    d("k3d_moe_experts", I, P, P, P, P, I, P, I, I, I, I, I, F, F, I, P, SZ, P, P, P, P)
+    d("k3d_moe_routed", I, P, P, P, P, I, P, P, P, I, I, I, I, I, I, F, I, F, F, I, P, SZ, P, P,
+      P, P)
+    d("k3d_moe_experts", I, P, P, P, P, I, P, I, I, I, I, I, I, F, F, I, P, SZ, P, P, P, P)
+    d("k3d_mxfp4_tiled_size", I, I, I, P, P)
+    d("k3d_mxfp4_tile", I, P, P, P, P, I, I, P)
     # generator
     d("k3g_u64", C.c_uint64, C.c_uint64, C.c_uint64)
     d("k3g_bytes", None, P, SZ, C.c_uint64)
@@ -338,3 +341,101 @@ class DevBuf:
         if self.ptr:
             lib().k3d_free(self.ptr)
             self.ptr = None
+
+
+class DevBank:
+    """An expert bank resident on the device: the n experts' six MXFP4 arrays in HBM and a
+    device table of K3ExpertQ with device pointers (None in `experts` = a dropped expert,
+    NULL pointers in the table). layout K3D_LAYOUT_TILED stores each matrix regrouped by
+    k3d_mxfp4_tile (the arrays are uploaded row-major into a staging buffer and tiled on the
+    device); K3D_LAYOUT_ROWS stores them as they are."""
+
+    def __init__(self, experts, hidden, inter, layout=K3D_LAYOUT_ROWS):
+        L = lib()
+        check(L.k3d_init(), "k3d_init")
+        self.layout, self.n = layout, len(experts)
+        shapes = [(inter, hidden), (inter, hidden), (hidden, inter)]   # (rows, in) of p1, p3, p2
+        sizes = []
+        for rows, inn in shapes:
+            if layout == K3D_LAYOUT_TILED:
+                pk, sc = C.c_size_t(), C.c_size_t()
+                check(L.k3d_mxfp4_tiled_size(rows, inn, C.byref(pk), C.byref(sc)),
+                      "k3d_mxfp4_tiled_size")
+                sizes += [pk.value, sc.value]
+            else:
+                sizes += [rows * inn // 2, rows * inn // 32]
+        rnd = [(b + 255) // 256 * 256 for b in sizes]
+        slot = sum(rnd)
+        self.mem = DevBuf(max(1, slot * self.n))
+        stage = DevBuf(max(rnd)) if layout == K3D_LAYOUT_TILED else None
+        stage2 = DevBuf(max(rnd)) if layout == K3D_LAYOUT_TILED else None
+        table = (K3ExpertQ * max(1, self.n))()
+        for e, ex in enumerate(experts):
+            if ex is None:
+                continue
+            base = self.mem.ptr + e * slot
+            offs = [base + sum(rnd[:i]) for i in range(6)]
+            if layout == K3D_LAYOUT_TILED:
+                for m, (rows, inn) in enumerate(shapes):
+                    stage.upload(ex.t[2 * m])
+                    stage2.upload(ex.t[2 * m + 1])
+                    check(L.k3d_mxfp4_tile(offs[2 * m], offs[2 * m + 1], stage.ptr, stage2.ptr,
+                                           rows, inn, None), "k3d_mxfp4_tile")
+                    check(L.k3d_sync(None), "sync")
+            else:
+                for i in range(6):
+                    self.mem.upload(ex.t[i], offs[i] - self.mem.ptr)
+            table[e] = K3ExpertQ(*offs)
+        for b in (stage, stage2):
+            if b is not None:
+                b.free()
+        self.table = DevBuf(C.sizeof(table))
+        check(L.k3d_h2d(self.table.ptr, C.addressof(table), C.sizeof(table), None), "h2d")
+        check(L.k3d_sync(None), "sync")
+
+    def free(self):
+        self.mem.free()
+        self.table.free()
+
+
+def moe_routed_device(bank, x, router_w, bias, topk, renorm=1, routed_scale=1.0,
+                      act=K3_ACT_SILU, b1=4.0, b2=25.0, prec=0, hidden=None, inter=None):
+    """The routed layer through k3d_moe_routed on a DevBank: host arrays in, host arrays
+    out (out [T][hidden], idx, wt [T][topk], perm [T*topk], offsets [n+1], drops)."""
+    L = lib()
+    router_w = _f32(router_w)
+    n_experts, hid = router_w.shape
+    hidden = hidden or hid
+    x = _f32(x).reshape(-1, hidden)
+    T = x.shape[0]
+    bufs = {}
+    try:
+        bufs["x"] = DevBuf(x.nbytes).upload(x)
+        bufs["w"] = DevBuf(router_w.nbytes).upload(router_w)
+        bufs["b"] = DevBuf(n_experts * 4).upload(_f32(bias)) if bias is not None else None
+        bufs["out"] = DevBuf(T * hidden * 4)
+        bufs["idx"] = DevBuf(T * topk * 4)
+        bufs["wt"] = DevBuf(T * topk * 4)
+        bufs["perm"] = DevBuf(T * topk * 4)
+        bufs["off"] = DevBuf((n_experts + 1) * 4)
+        bufs["drops"] = DevBuf(4)
+        wsb = L.k3d_moe_ws(T, hidden, inter, n_experts, topk, prec)
+        bufs["ws"] = DevBuf(wsb)
+        b = bufs["b"].ptr if bufs["b"] is not None else None
+        check(L.k3d_moe_routed(bufs["out"].ptr, bufs["idx"].ptr, bufs["wt"].ptr, bufs["x"].ptr, T,
+                               bufs["w"].ptr, b, bank.table.ptr, bank.layout, hidden, inter,
+                               n_experts, topk, renorm, routed_scale, act, b1, b2, prec,
+                               bufs["ws"].ptr, wsb, bufs["perm"].ptr, bufs["off"].ptr,
+                               bufs["drops"].ptr, None), "k3d_moe_routed")
+        check(L.k3d_sync(None), "sync")
+        out = bufs["out"].download(np.empty((T, hidden), np.float32))
+        idx = bufs["idx"].download(np.empty((T, topk), np.int32))
+        wt = bufs["wt"].download(np.empty((T, topk), np.float32))
+        perm = bufs["perm"].download(np.empty(T * topk, np.int32))
+        off = bufs["off"].download(np.empty(n_experts + 1, np.int32))
+        drops = int(bufs["drops"].download(np.empty(1, np.int32))[0])
+        return out, idx, wt, perm, off, drops
+    finally:
+        for v in bufs.values():
+            if v is not None:
+                v.free()

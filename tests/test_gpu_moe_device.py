@@ -1,0 +1,149 @@
+# SPDX-License-Identifier: Apache-2.0
+"""The device-resident MoE path (k3d_moe_routed) on both bank layouts: the tiled layout's
+bytes, row-major vs tiled results bit-identical, parity with the oracle (routing and the
+gather permutation bit-exact, outputs within 1e-4 * ||ref||inf; bf16 activations within
+2e-2 relative), and the full decode shape against the reference's golden outputs."""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import max_err_rel_inf
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+TOL_BF16 = 2e-2
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def tile_layout(packed, scales, rows, K):
+    """The tiled layout, restated with numpy: tile t (16 rows), chunk c (16 blocks), step d,
+    lane l = 16g + r holds block 4d+g of row 16t+r; its four scale bytes (d = 0..3) are
+    contiguous at [(t*nchunk + c)*256 + 4l]."""
+    ntile, nchunk, nblk = (rows + 15) // 16, K // 512, K // 32
+    P = np.zeros((ntile * 16, K // 2), np.uint8)
+    S = np.zeros((ntile * 16, nblk), np.uint8)
+    P[:rows] = packed.reshape(rows, K // 2)
+    S[:rows] = scales.reshape(rows, nblk)
+    Pb = P.reshape(ntile, 16, nchunk, 4, 4, 16)          # t, r, c, d, g, byte
+    tp = Pb.transpose(0, 2, 3, 4, 1, 5).reshape(-1)      # t, c, d, (g, r), byte
+    Sb = S.reshape(ntile, 16, nchunk, 4, 4)              # t, r, c, d, g
+    ts = Sb.transpose(0, 2, 4, 1, 3).reshape(-1)         # t, c, (g, r), d
+    return tp, ts
+
+
+@pytest.mark.parametrize("rows,K", [(40, 1024), (16, 512), (2048, 7168)])
+def test_tile_layout_bytes(gpu, rows, K):
+    say(f"case: tile layout rows={rows} K={K}")
+    L = gpu.lib()
+    rng = np.random.default_rng(rows + K)
+    packed = rng.integers(0, 256, rows * K // 2, dtype=np.uint8)
+    scales = rng.integers(0, 256, rows * K // 32, dtype=np.uint8)
+    import ctypes as C
+    pk, sc = C.c_size_t(), C.c_size_t()
+    gpu.check(L.k3d_mxfp4_tiled_size(rows, K, C.byref(pk), C.byref(sc)), "size")
+    src_p = gpu.DevBuf(packed.nbytes).upload(packed)
+    src_s = gpu.DevBuf(scales.nbytes).upload(scales)
+    dst_p, dst_s = gpu.DevBuf(pk.value), gpu.DevBuf(sc.value)
+    gpu.check(L.k3d_mxfp4_tile(dst_p.ptr, dst_s.ptr, src_p.ptr, src_s.ptr, rows, K, None), "tile")
+    gpu.check(L.k3d_sync(None), "sync")
+    got_p = dst_p.download(np.empty(pk.value, np.uint8))
+    got_s = dst_s.download(np.empty(sc.value, np.uint8))
+    for b in (src_p, src_s, dst_p, dst_s):
+        b.free()
+    tp, ts = tile_layout(packed, scales, rows, K)
+    assert np.array_equal(got_p, tp)
+    assert np.array_equal(got_s, ts)
+
+
+def test_tile_rejects_bad_width(gpu):
+    L = gpu.lib()
+    assert L.k3d_mxfp4_tile(None, None, None, None, 16, 480, None) != 0
+    assert b"512" in L.k3d_error()
+
+
+def nan_scaled(k3, E, I, seed, e):
+    """An expert whose gate and down matrices carry NaN (255) scale bytes: those blocks
+    contribute zero (reference k3_ops.c mxfp4 paths)."""
+    ex = k3.gen_expert(E, I, seed, e)
+    t = [a.copy() for a in ex.t]
+    t[1][5::37] = 255
+    t[5][3::41] = 255
+    return k3.Expert(*t)
+
+
+@pytest.fixture(scope="module")
+def small_layer(k3):
+    E, I, N, K, T = 1024, 512, 16, 4, 29
+    rng = np.random.default_rng(31)
+    bank = [k3.gen_expert(E, I, 41, e) for e in range(N)]
+    bank[3] = nan_scaled(k3, E, I, 41, 3)
+    W = (rng.standard_normal((N, E)) * 0.05).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.02).astype(np.float32)
+    X = rng.standard_normal((T, E)).astype(np.float32)
+    return dict(E=E, I=I, N=N, K=K, T=T, bank=bank, W=W, bias=bias, X=X)
+
+
+def stable_gather(idx, n_experts):
+    a = idx.reshape(-1)
+    perm = np.argsort(a, kind="stable").astype(np.int32)
+    off = np.zeros(n_experts + 1, np.int32)
+    np.cumsum(np.bincount(a, minlength=n_experts), out=off[1:])
+    return perm, off
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_moe_device_layouts_vs_oracle(gpu, orc, small_layer, prec):
+    s = small_layer
+    say(f"case: device moe layouts prec={prec} E={s['E']} I={s['I']} T={s['T']}")
+    res = {}
+    for layout in (gpu.K3D_LAYOUT_ROWS, gpu.K3D_LAYOUT_TILED):
+        bank = gpu.DevBank(s["bank"], s["E"], s["I"], layout)
+        try:
+            res[layout] = gpu.moe_routed_device(bank, s["X"], s["W"], s["bias"], s["K"], prec=prec,
+                                                inter=s["I"])
+        finally:
+            bank.free()
+    r, t = res[gpu.K3D_LAYOUT_ROWS], res[gpu.K3D_LAYOUT_TILED]
+    for a, b in zip(r, t):
+        assert np.array_equal(np.asarray(a), np.asarray(b))       # layouts: identical bits
+    out, idx, wt, perm, off, drops = r
+    o2, i2, w2 = orc.moe_routed(s["X"], s["W"], s["bias"], s["bank"], s["E"], s["I"], s["K"])
+    assert np.array_equal(idx, i2)
+    assert np.array_equal(bits(wt), bits(w2))
+    p2, off2 = stable_gather(i2, s["N"])
+    assert np.array_equal(perm, p2) and np.array_equal(off, off2)
+    assert np.bincount(idx.ravel(), minlength=s["N"]).max() > 8     # some expert needs 2 passes
+    assert drops == 0
+    if prec == 0:
+        for tk in range(s["T"]):
+            assert max_err_rel_inf(out[tk], o2[tk]) <= TOL, tk
+    else:
+        assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
+
+
+def test_moe_device_tiled_decode_golden(gpu, wl, gold):
+    """Full decode shape (7168 x 2048, 384 experts, top-8) from a tiled bank: the reference's
+    golden routing and outputs for 8 tokens."""
+    say("case: device moe tiled, decode shape, 8 tokens vs golden")
+    W = wl.router_weights()
+    X = wl.tokens(64)[:8]
+    bank = gpu.DevBank(wl.lazy_bank(gold["router_idx"][:8]), wl.HIDDEN, wl.INTER,
+                       gpu.K3D_LAYOUT_TILED)
+    try:
+        out, idx, wt, _, _, drops = gpu.moe_routed_device(bank, X, W, None, wl.TOPK, inter=wl.INTER)
+    finally:
+        bank.free()
+    assert np.array_equal(idx, gold["router_idx"][:8])
+    assert np.array_equal(bits(wt), bits(gold["router_wt"][:8]))
+    assert drops == 0
+    for t in range(8):
+        assert max_err_rel_inf(out[t], gold["moe8_out"][t]) <= TOL, t
