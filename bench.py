@@ -170,13 +170,40 @@ def cpu_baseline(T_sample=8, budget_s=10.0):
             "ms_per_token": round(med / T_sample * 1e3, 2)}
 
 
+def measured_traffic():
+    """HBM bytes per GATEUP dispatch at batch 64 from the profiler's byte counters (two
+    counter passes over this bench, scaled by a copy of known size), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
+            return int(json.load(f)["traffic_bytes_per_dispatch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_probe(nbytes=256 << 20, reps=10):
+    """A plain device-to-device copy kernel of known size: reads and writes nbytes each."""
+    import torch
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"bench: copy probe {reps} x {nbytes} B read + {nbytes} B written")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 256 MiB device copy 10 times (calibrates the HBM "
+                         "byte counters of a profiler run) and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build does not shard the layer across GPUs)", file=sys.stderr)
@@ -220,9 +247,10 @@ def main():
         "config": {"workload": "moe_decode_batch64", "tokens": T, "hidden": E, "inter": I,
                    "experts": N, "topk": K, "activation": "silu", "bank_GB": round(N * EXPERT_BYTES / 1e9, 3),
                    "unique_experts_per_step": round(u_mean, 1)},
-        "roofline": {"bound": "hbm", "kernel": "mx_gemm GATEUP (fused gate/up + SiLU)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "mx_moe_kernel GATEUP (fused gate/up + SiLU, tiled bank)",
                      "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
                      "kernel_ms": round(gu_ms, 4), "algorithmic_bytes": int(gu_bytes)},
         "layer_GBps": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
         "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in stages.items()},
