@@ -71,6 +71,12 @@ int k3d_mxfp4_tiled_size(int rows, int in, size_t *packed_bytes, size_t *scales_
 int k3d_mxfp4_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
                    const uint8_t *scales, int rows, int in, void *stream);
 
+/* Diagnostics of the last k3d_router call that used workspace `ws` (after the device has
+ * finished it; synchronises): h_counts[t] = number of token t's logits whose fp32 rounding
+ * the split fp64 sum could not certify and that were recomputed with the reference's
+ * sequential chain. */
+int k3d_router_recomputed(int *h_counts, const void *ws, int T, int hidden, int n_experts);
+
 /* The routed MoE layer (k3_moe's routed loop, reference k3_ops.c:576-643, with z := x),
  * expert-major. bank is a DEVICE array of n_experts K3ExpertQ (k3.h) whose pointers are
  * device pointers, in the given layout; an entry with a NULL pointer is a dropped expert.

@@ -9,6 +9,7 @@
 #include "k3k.h"
 
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 extern const int k3_expf_exc_n;
@@ -50,19 +51,65 @@ int k3d_prof_end(double *ms, int *count, int n_stages)
 }
 int k3d_prof_mark(void *stream, int stage) { return k3k_prof_mark(stream, stage) ? fail("prof_mark") : 0; }
 
-/* The libm exception table of the router score, uploaded once per process. */
-static const uint32_t *g_exc_dev = NULL;
-static int exc_table(const uint32_t **tab, int *n)
+/* The libm exception table of the router score and its bucket index, uploaded once per
+ * process. */
+static K3kExc g_exc;
+static int g_exc_ready = 0;
+
+static int exc_table(const K3kExc **out)
 {
-    if (!g_exc_dev) {
-        uint32_t *d = (uint32_t *)k3k_malloc((size_t)(2 * k3_expf_exc_n + 2) * 4);
-        if (!d) return -1;
-        if (k3k_h2d(d, k3_expf_exc, (size_t)(2 * k3_expf_exc_n + 2) * 4, NULL) || k3k_sync(NULL))
-            return -1;
-        g_exc_dev = d;
+    if (!g_exc_ready) {
+        const int n = k3_expf_exc_n;
+        memset(&g_exc, 0, sizeof g_exc);
+        if (n > 0) {
+            const uint32_t kmin = k3_expf_exc[0], kmax = k3_expf_exc[2 * (n - 1)];
+            const uint32_t base = kmin >> 12, nb = (kmax >> 12) - base + 1;
+            uint32_t *index = (uint32_t *)malloc((size_t)(nb + 1) * 4);
+            if (!index) return bad("router exception index: out of host memory");
+            uint32_t i = 0;
+            for (uint32_t bk = 0; bk <= nb; bk++) {
+                while (i < (uint32_t)n && (k3_expf_exc[2 * i] >> 12) - base < bk) i++;
+                index[bk] = i;
+            }
+            /* membership bitmap over |key| in [mmin, mmax], one word array per sign */
+            uint32_t mmin = 0xffffffffu, mmax = 0;
+            for (int j = 0; j < n; j++) {
+                const uint32_t m = k3_expf_exc[2 * j] & 0x7fffffffu;
+                if (m < mmin) mmin = m;
+                if (m > mmax) mmax = m;
+            }
+            const uint32_t mwords = ((mmax - mmin) >> 5) + 1;
+            uint32_t *bits = (uint32_t *)calloc((size_t)2 * mwords, 4);
+            if (!bits) {
+                free(index);
+                return bad("router exception bitmap: out of host memory");
+            }
+            for (int j = 0; j < n; j++) {
+                const uint32_t key = k3_expf_exc[2 * j], bi = (key & 0x7fffffffu) - mmin;
+                bits[(size_t)(key >> 31) * mwords + (bi >> 5)] |= 1u << (bi & 31);
+            }
+            uint32_t *dp = (uint32_t *)k3k_malloc((size_t)2 * n * 4);
+            uint32_t *di = (uint32_t *)k3k_malloc((size_t)(nb + 1) * 4);
+            uint32_t *db = (uint32_t *)k3k_malloc((size_t)2 * mwords * 4);
+            int rc = !dp || !di || !db || k3k_h2d(dp, k3_expf_exc, (size_t)2 * n * 4, NULL) ||
+                     k3k_h2d(di, index, (size_t)(nb + 1) * 4, NULL) ||
+                     k3k_h2d(db, bits, (size_t)2 * mwords * 4, NULL) || k3k_sync(NULL);
+            free(index);
+            free(bits);
+            if (rc) return fail("router exception table upload");
+            g_exc.bits = db;
+            g_exc.mmin = mmin;
+            g_exc.mwords = mwords;
+            g_exc.pairs = dp;
+            g_exc.index = di;
+            g_exc.kmin = kmin;
+            g_exc.kmax = kmax;
+            g_exc.base = base;
+            g_exc.n = n;
+        }
+        g_exc_ready = 1;
     }
-    *tab = g_exc_dev;
-    *n = k3_expf_exc_n;
+    *out = &g_exc;
     return 0;
 }
 
@@ -140,25 +187,20 @@ int k3d_matmul_bf16(float *y, const float *x, int ntok, const uint16_t *W, int i
 }
 
 /* ---- router -------------------------------------------------------------------------- */
-static int router_ksplit(int T, int hidden, int n_experts)
-{
-    const int tiles = ((n_experts + 63) / 64) * ((T + 15) / 16);
-    int ks = (512 + tiles - 1) / tiles;
-    int kmax = hidden / 512;
-    if (kmax < 1) kmax = 1;
-    if (ks > kmax) ks = kmax;
-    if (ks < 1) ks = 1;
-    return ks;
-}
-
 typedef struct {
     double *part;
+    float *rbound;
+    int *nrecomp;
+    int chunk;
 } RtWs;
 
 static size_t router_layout(Carve *c, RtWs *w, int T, int hidden, int n_experts)
 {
-    const int ks = router_ksplit(T, hidden, n_experts);
-    w->part = (double *)take(c, (size_t)ks * T * n_experts * 8);
+    w->chunk = k3k_router_chunk(T, hidden, n_experts);
+    const size_t ks = (size_t)((hidden + w->chunk - 1) / w->chunk);
+    w->part = (double *)take(c, ks * T * n_experts * 8);
+    w->rbound = (float *)take(c, ks * T * n_experts * 4);
+    w->nrecomp = (int *)take(c, (size_t)T * 4);
     return c->off;
 }
 
@@ -169,25 +211,44 @@ size_t k3d_router_ws(int T, int hidden, int n_experts)
     return router_layout(&c, &w, T, hidden, n_experts);
 }
 
+static int router_run(int *idx, float *wt, const float *x, int T, const float *W,
+                      const float *bias, int hidden, int n_experts, int topk, int renorm,
+                      float routed_scale, const RtWs *w, void *stream)
+{
+    const K3kExc *exc;
+    int rc = exc_table(&exc);
+    if (rc) return rc;
+    if (k3k_router_partial(w->part, w->rbound, x, T, W, hidden, n_experts, w->chunk, stream))
+        return fail("router_partial");
+    if (k3k_router_final(idx, wt, w->nrecomp, w->part, w->rbound, w->chunk, x, W, bias, T, hidden,
+                         n_experts, topk, renorm, routed_scale, exc, stream))
+        return fail("router_final");
+    return 0;
+}
+
+int k3d_router_recomputed(int *h_counts, const void *ws, int T, int hidden, int n_experts)
+{
+    if (T <= 0) return 0;
+    Carve c = {(char *)ws, 0};
+    RtWs w;
+    router_layout(&c, &w, T, hidden, n_experts);
+    if (k3k_d2h(h_counts, w.nrecomp, (size_t)T * 4, NULL) || k3k_sync(NULL)) return fail("router_recomputed");
+    return 0;
+}
+
 int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const float *bias,
                int hidden, int n_experts, int topk, int renorm, float routed_scale, void *ws,
                size_t ws_bytes, void *stream)
 {
     if (T <= 0) return 0;
     if (topk < 1 || topk > K3_MAX_TOPK) return bad("k3d_router: topk outside 1..64");
+    if (n_experts < 1 || n_experts > 2048) return bad("k3d_router: n_experts outside 1..2048");
     if (ws_bytes < k3d_router_ws(T, hidden, n_experts)) return bad("k3d_router: workspace too small");
     Carve c = {(char *)ws, 0};
     RtWs w;
     router_layout(&c, &w, T, hidden, n_experts);
-    const int ks = router_ksplit(T, hidden, n_experts);
-    const uint32_t *exc;
-    int nexc;
-    if (exc_table(&exc, &nexc)) return fail("router exception table");
-    if (k3k_router_partial(w.part, x, T, W, hidden, n_experts, ks, stream)) return fail("router_partial");
-    if (k3k_router_final(idx, wt, NULL, w.part, ks, x, W, bias, T, hidden, n_experts, topk, renorm,
-                         routed_scale, exc, nexc, stream))
-        return fail("router_final");
-    return 0;
+    return router_run(idx, wt, x, T, W, bias, hidden, n_experts, topk, renorm, routed_scale, &w,
+                      stream);
 }
 
 /* ---- MoE experts ----------------------------------------------------------------------- */
@@ -237,9 +298,13 @@ size_t k3d_moe_ws(int T, int hidden, int inter, int n_experts, int topk, int pre
     return c.off;
 }
 
-static int moe_check(const char *fn, int hidden, int inter, int topk, int layout)
+static int moe_check(const char *fn, int hidden, int inter, int n_experts, int topk, int layout)
 {
     static char msg[160];
+    if (n_experts < 1 || n_experts > 2048) {
+        snprintf(msg, sizeof msg, "%s: n_experts outside 1..2048", fn);
+        return bad(msg);
+    }
     if ((hidden % 32) || (inter % 32)) {
         snprintf(msg, sizeof msg, "%s: hidden and inter must be multiples of 32", fn);
         return bad(msg);
@@ -321,7 +386,7 @@ int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x,
                     int *perm_out, int *offsets_out, int *drops_out, void *stream)
 {
     if (T <= 0) return 0;
-    int rc = moe_check("k3d_moe_experts", hidden, inter, topk, layout);
+    int rc = moe_check("k3d_moe_experts", hidden, inter, n_experts, topk, layout);
     if (rc) return rc;
     if (ws_bytes < k3d_moe_ws(T, hidden, inter, n_experts, topk, prec))
         return bad("k3d_moe_experts: workspace too small");
@@ -340,7 +405,7 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
                    int *drops_out, void *stream)
 {
     if (T <= 0) return 0;
-    int rc = moe_check("k3d_moe_routed", hidden, inter, topk, layout);
+    int rc = moe_check("k3d_moe_routed", hidden, inter, n_experts, topk, layout);
     if (rc) return rc;
     if (ws_bytes < k3d_moe_ws(T, hidden, inter, n_experts, topk, prec))
         return bad("k3d_moe_routed: workspace too small");
@@ -349,16 +414,10 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
     RtWs r;
     moe_layout(&c, &w, T, hidden, inter, n_experts, topk, prec);
     router_layout(&c, &r, T, hidden, n_experts);
-    const int ks = router_ksplit(T, hidden, n_experts);
-    const uint32_t *exc;
-    int nexc;
-    if (exc_table(&exc, &nexc)) return fail("router exception table");
     k3k_prof_mark(stream, K3D_STAGE_BEGIN);
-    if (k3k_router_partial(r.part, x, T, router_w, hidden, n_experts, ks, stream))
-        return fail("router_partial");
-    if (k3k_router_final(idx, wt, NULL, r.part, ks, x, router_w, bias, T, hidden, n_experts, topk,
-                         renorm, routed_scale, exc, nexc, stream))
-        return fail("router_final");
+    rc = router_run(idx, wt, x, T, router_w, bias, hidden, n_experts, topk, renorm, routed_scale,
+                    &r, stream);
+    if (rc) return rc;
     k3k_prof_mark(stream, K3D_STAGE_ROUTER);
     return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
                           b1, b2, prec, &w, perm_out, offsets_out, drops_out, stream);

@@ -8,6 +8,8 @@
 #include "k3_expf.h"
 #include "k3k.h"
 
+#include <string.h>
+
 namespace {
 
 struct ExpertQDev {
@@ -32,146 +34,386 @@ __global__ void split_kernel(uint16_t *hi, uint16_t *lo, const float *x, size_t 
     }
 }
 
-/* ---- router logits ------------------------------------------------------------------
- * part[ks][t][e] = sum over the ks-th K chunk of (double)W[e][k] * (double)x[t][k],
- * accumulated with fp64 fma in ascending k. A product of two floats is exact in fp64, so
- * each fma equals the reference's separate multiply and add (k3_ops.c:449-450); only the
- * grouping of the 7168-term sum differs from the reference's single ascending chain.
- * Workgroup tile: 64 experts x 16 tokens; each thread one expert x 4 tokens. */
-constexpr int RT_E = 64, RT_T = 16, RT_K = 64;
+/* ---- router scores ------------------------------------------------------------------
+ * logit[t][e] = the reference's own fp64 chain: acc = 0; for k ascending: acc += (double)
+ * W[e][k] * (double)x[t][k] (k3_ops.c:446-450). A product of two floats is exact in fp64,
+ * so fma(w, x, acc) rounds exactly like the separate multiply and add; one lane runs one
+ * (token, expert) chain in the reference's order, so the logit is bit-identical to the
+ * reference's by construction. Then score = 1/(1+expf(-(float)acc)) with the host libm's
+ * expf (k3_ops.c:451) and choice = score + bias (k3_ops.c:452).
+ *
+ * A workgroup covers EB experts x TB tokens (EB*TB = 256 lanes): EB = 4, TB = 64 (a wave
+ * is 64 tokens of one expert) when there are many tokens, EB = 64, TB = 4 (a wave is 64
+ * experts of one token) when there are few. K walks in chunks of RC columns; W and x of the
+ * chunk are staged in LDS (double buffered) and each lane reads its W row and x row 4
+ * columns at a time. */
 
-__global__ __launch_bounds__(256) void router_partial_kernel(double *part, const float *x, int T,
-                                                             const float *W, int hidden,
-                                                             int n_experts, int ksplit)
-{
-    __shared__ float ws[RT_E][RT_K + 1];
-    __shared__ float xs[RT_T][RT_K];
-    const int e0 = blockIdx.x * RT_E, t0 = blockIdx.y * RT_T, ks = blockIdx.z;
-    const int kc = (hidden + ksplit - 1) / ksplit;
-    const int k0 = ks * kc, k1 = min(hidden, k0 + kc);
-    const int tid = threadIdx.x, el = tid & 63, tg = tid >> 6;
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int kb = k0; kb < k1; kb += RT_K) {
-        for (int i = tid; i < RT_E * RT_K; i += 256) {
-            const int r = i / RT_K, c = i % RT_K;
-            const int e = e0 + r, k = kb + c;
-            ws[r][c] = (e < n_experts && k < k1) ? W[(size_t)e * hidden + k] : 0.0f;
-        }
-        for (int i = tid; i < RT_T * RT_K; i += 256) {
-            const int r = i / RT_K, c = i % RT_K;
-            const int t = t0 + r, k = kb + c;
-            xs[r][c] = (t < T && k < k1) ? x[(size_t)t * hidden + k] : 0.0f;
-        }
-        __syncthreads();
-        const int kn = min(RT_K, k1 - kb);
-        for (int k = 0; k < kn; k++) {
-            const double w = (double)ws[el][k];
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] = fma(w, (double)xs[tg * 4 + i][k], acc[i]);
-        }
-        __syncthreads();
-    }
-    const int e = e0 + el;
-    if (e < n_experts)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = t0 + tg * 4 + i;
-            if (t < T) part[((size_t)ks * T + t) * n_experts + e] = acc[i];
-        }
-}
+struct ExcTable {
+    const uint32_t *pairs;      /* sorted (key bits of v, libm expf(v) bits) */
+    const uint32_t *index;      /* index[b] = first pair with (key >> 12) - base >= b */
+    const uint32_t *bits;       /* membership bitmap over |key| in [mmin, mmax], per sign */
+    uint32_t kmin, kmax, base, mmin, mwords;
+    int n;
+};
 
-/* libm-exact router score 1/(1+expf(v)) for v = -logit: the deterministic candidate,
- * overridden where host libm's expf gives a different score (table built at build time:
- * sorted (key bits, libm expf bits) pairs, binary searched). */
-__device__ __forceinline__ float router_score(float logit, const uint32_t *exc, int n_exc)
+/* libm-exact score 1/(1+expf(v)), v = -logit: the deterministic correctly rounded
+ * candidate, replaced where the host libm's expf differs (exception table built at build
+ * time from that libm). One bitmap load decides membership; only members search their
+ * bucket (key >> 12, at most 17 pairs). */
+__device__ __forceinline__ float router_score(float logit, const ExcTable &x)
 {
     const float v = -logit;
     float E = k3_expf_det(v);
-    if (n_exc > 0) {
-        const uint32_t key = __float_as_uint(v);
-        int lo = 0, hi = n_exc;
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            const uint32_t k = exc[2 * mid];
-            if (k < key) lo = mid + 1;
-            else hi = mid;
+    const uint32_t key = __float_as_uint(v);
+    const uint32_t mag = key & 0x7fffffffu;
+    if (x.n > 0 && mag >= x.mmin) {
+        const uint32_t bi = mag - x.mmin, w = bi >> 5;
+        if (w < x.mwords && ((x.bits[(key >> 31) * x.mwords + w] >> (bi & 31)) & 1u)) {
+            const uint32_t bkt = (key >> 12) - x.base;
+            int lo = (int)x.index[bkt], hi = (int)x.index[bkt + 1];
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (x.pairs[2 * mid] < key) lo = mid + 1;
+                else hi = mid;
+            }
+            if (lo < x.n && x.pairs[2 * lo] == key) E = __uint_as_float(x.pairs[2 * lo + 1]);
         }
-        if (lo < n_exc && exc[2 * lo] == key) E = __uint_as_float(exc[2 * lo + 1]);
     }
     return 1.0f / (1.0f + E);
 }
 
-/* One workgroup per token: logits (partials summed in ascending chunk order, rounded to
- * fp32), score, biased choice, then topk rounds of "largest choice, lowest index among
- * equals, strictly above -inf" exactly as the reference's first-strict-max scan
- * (k3_ops.c:459-467), then renormalisation and scaling (k3_ops.c:469-475). */
-constexpr int RF_MAXE = 2048;
+/* ---- router logits, certified ---------------------------------------------------------
+ * The reference's logit is one sequential fp64 chain per (token, expert):
+ *   a_0 = 0, a_{i+1} = fl(a_i + w_i x_i), i ascending, logit = (float)a_n
+ * (k3_ops.c:446-451; the product of two floats is exact in fp64, so fma(w, x, a) rounds
+ * like the separate multiply and add). Run literally, that is a 7168-step dependent chain
+ * per logit. Instead:
+ *
+ * 1. router_partial_kernel computes, per K chunk k of C_k columns, the chunk's own chain
+ *    P_k (from 0, ascending) and R_k, an upper bound on the sum of |r_i| over the chunk's
+ *    intermediate values r_i: per 32-column sub-block, 32 * (|r at its start| + ||w||_1 *
+ *    ||x||_inf of the sub-block).
+ * 2. router_final_kernel sums S = P_0 + P_1 + ... in k order and bounds |S - a_n|: with
+ *    u = 2^-53 and Q_k the prefix before chunk k, the reference's chain errs from the
+ *    exact sum by at most u * sum_i |a_i| <= u * sum_k (C_k |Q_k| + R_k), this
+ *    computation by at most u * sum_k (R_k + |Q_{k+1}|); B = 1.01 u sum_k (C_k |Q_k| +
+ *    2 R_k + |Q_{k+1}|) + 4u|S| covers both and the second-order terms. If every value in
+ *    [S - B, S + B] rounds to the same float, that float is the reference's logit.
+ * 3. Logits that are not certified and could matter -- the expert is selected (its weight
+ *    must be exact) or its choice could reach the selection -- are recomputed with the
+ *    reference's chain itself, and the selection is redone until no such logit is left.
+ *
+ * The partial kernel: a workgroup computes 32 experts x 64 tokens over one chunk, a thread
+ * 2 experts x 4 tokens. W and x are staged in LDS 32 columns at a time (double buffered),
+ * widened to fp64 once while staging (the conversion costs four times an fp64 fma), with
+ * the sub-block norms; the threads' LDS reads are mostly broadcasts. */
+constexpr int RP_E = 32, RP_T = 64, RP_KS = 32, RP_SUB = 32, RP_LD = RP_KS + 2;
 
-__global__ __launch_bounds__(256) void router_final_kernel(int *idx, float *wt, int *nrecomp,
-                                                           const double *part, int ksplit,
-                                                           const float *bias, int T,
-                                                           int n_experts, int topk, int renorm,
-                                                           float routed_scale,
-                                                           const uint32_t *exc, int n_exc)
+__global__ __launch_bounds__(256) void router_partial_kernel(double *part, float *rbound,
+                                                             const float *x, int T, const float *W,
+                                                             int hidden, int n_experts, int chunk,
+                                                             int vec)
 {
-    __shared__ float score[RF_MAXE];
-    __shared__ float choice[RF_MAXE];
-    __shared__ float rv[256];
-    __shared__ int ri[256];
-    __shared__ float wsel[K3_MAX_TOPK_DEV];
-    const int t = blockIdx.x, tid = threadIdx.x;
-    for (int e = tid; e < n_experts; e += 256) {
-        double s = 0.0;
-        for (int ks = 0; ks < ksplit; ks++) s += part[((size_t)ks * T + t) * n_experts + e];
-        const float sc = router_score((float)s, exc, n_exc);
-        score[e] = sc;
-        choice[e] = sc + (bias ? bias[e] : 0.0f);
-    }
-    __syncthreads();
-    for (int j = 0; j < topk; j++) {
-        float bv = -INFINITY;
-        int bi = -1;
-        for (int e = tid; e < n_experts; e += 256) {
-            const float c = choice[e];
-            if (c > bv) { bv = c; bi = e; }           /* ascending e: first strict max */
+    __shared__ __attribute__((aligned(16))) double ws[2][RP_E][RP_LD];
+    __shared__ __attribute__((aligned(16))) double xs[2][RP_T][RP_LD];
+    __shared__ float wn[2][RP_E];                    /* sum |w| over the sub-block */
+    __shared__ float xn[2][RP_T];                    /* max |x| over the sub-block */
+    const int tid = threadIdx.x;
+    const int eg = tid & 15, tg = tid >> 4;          /* experts 2eg, 2eg+1; tokens 4tg.. */
+    const int e0 = blockIdx.x * RP_E, t0 = blockIdx.y * RP_T, ks = blockIdx.z;
+    const int kb0 = ks * chunk, kb1 = min(hidden, kb0 + chunk);
+    const int nsub = (kb1 - kb0 + RP_KS - 1) / RP_KS;
+    const float *Wt = W + (size_t)e0 * hidden, *xt = x + (size_t)t0 * hidden;
+    /* staging: W 32 rows x 8 float4 = 256 pieces (1 per thread), x 64 x 8 = 512 (2) */
+    float4 wst, xst[2];
+    auto fetch = [&](const float *base, int rows_valid, int r, int k) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < rows_valid) {
+            const float *src = base + (size_t)r * hidden + k;
+            if (vec && k + 3 < kb1) v = *reinterpret_cast<const float4 *>(src);
+            else {
+                v.x = k < kb1 ? src[0] : 0.f;
+                v.y = k + 1 < kb1 ? src[1] : 0.f;
+                v.z = k + 2 < kb1 ? src[2] : 0.f;
+                v.w = k + 3 < kb1 ? src[3] : 0.f;
+            }
         }
-        rv[tid] = bv;
-        ri[tid] = bi;
+        return v;
+    };
+    auto load = [&](int sc) {
+        const int k0 = kb0 + sc * RP_KS;
+        wst = fetch(Wt, n_experts - e0, tid >> 3, k0 + (tid & 7) * 4);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int pc = tid + 256 * i;
+            xst[i] = fetch(xt, T - t0, pc >> 3, k0 + (pc & 7) * 4);
+        }
+    };
+    auto put = [&](double *dst, float4 v) {
+        reinterpret_cast<double2 *>(dst)[0] = make_double2((double)v.x, (double)v.y);
+        reinterpret_cast<double2 *>(dst)[1] = make_double2((double)v.z, (double)v.w);
+    };
+    auto store = [&](int buf) {
+        /* 8 consecutive threads hold one row's 32 columns */
+        {
+            const int r = tid >> 3, c = (tid & 7) * 4;
+            put(&ws[buf][r][c], wst);
+            float a = fabsf(wst.x) + fabsf(wst.y) + fabsf(wst.z) + fabsf(wst.w);
+            a += __shfl_xor(a, 1, 64);
+            a += __shfl_xor(a, 2, 64);
+            a += __shfl_xor(a, 4, 64);
+            if ((tid & 7) == 0) wn[buf][r] = a;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int pc = tid + 256 * i, r = pc >> 3, c = (pc & 7) * 4;
+            put(&xs[buf][r][c], xst[i]);
+            float m = fmaxf(fmaxf(fabsf(xst[i].x), fabsf(xst[i].y)), fmaxf(fabsf(xst[i].z), fabsf(xst[i].w)));
+            m = fmaxf(m, __shfl_xor(m, 1, 64));
+            m = fmaxf(m, __shfl_xor(m, 2, 64));
+            m = fmaxf(m, __shfl_xor(m, 4, 64));
+            if ((pc & 7) == 0) xn[buf][r] = m;
+        }
+    };
+
+    double acc[2][4], rb[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) { acc[a][b] = 0.0; rb[a][b] = 0.0; }
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int sc = 0; sc < nsub; sc++) {
+        const int buf = sc & 1;
+        if (sc + 1 < nsub) load(sc + 1);
+        /* bound term of this sub-block, from the chains' values at its start */
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const double an = (double)wn[buf][2 * eg + a] * (double)xn[buf][4 * tg + b];
+                rb[a][b] = fma((double)RP_SUB, fabs(acc[a][b]) + an, rb[a][b]);
+            }
+#pragma unroll 4
+        for (int k = 0; k < RP_KS; k += 2) {
+            const double2 w0 = *reinterpret_cast<const double2 *>(&ws[buf][2 * eg][k]);
+            const double2 w1 = *reinterpret_cast<const double2 *>(&ws[buf][2 * eg + 1][k]);
+            double2 xv[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) xv[b] = *reinterpret_cast<const double2 *>(&xs[buf][4 * tg + b][k]);
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                acc[0][b] = fma(w0.x, xv[b].x, acc[0][b]);
+                acc[1][b] = fma(w1.x, xv[b].x, acc[1][b]);
+            }
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                acc[0][b] = fma(w0.y, xv[b].y, acc[0][b]);
+                acc[1][b] = fma(w1.y, xv[b].y, acc[1][b]);
+            }
+        }
+        if (sc + 1 < nsub) store(buf ^ 1);
         __syncthreads();
-        for (int s = 128; s > 0; s >>= 1) {
-            if (tid < s) {
-                const float ov = rv[tid + s];
-                const int oi = ri[tid + s];
-                /* keep the larger value; among equal values the lower index */
-                if (oi >= 0 && (ri[tid] < 0 || ov > rv[tid] || (ov == rv[tid] && oi < ri[tid]))) {
-                    rv[tid] = ov;
-                    ri[tid] = oi;
+    }
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int e = e0 + 2 * eg + a, t = t0 + 4 * tg + b;
+            if (e < n_experts && t < T) {
+                const size_t o = ((size_t)ks * T + t) * n_experts + e;
+                part[o] = acc[a][b];
+                /* rounded up: the float sums of |w| carry at most a 2^-18 relative error */
+                rbound[o] = (float)(rb[a][b] * (1.0 + 0x1p-17)) * (1.0f + 0x1p-20f);
+            }
+        }
+}
+
+/* The reference's own chain for one logit (the fallback of the certification). */
+__device__ __forceinline__ double router_chain(const float *w, const float *x, int hidden)
+{
+    double acc = 0.0;
+    int k = 0;
+    for (; k + 8 <= hidden; k += 8) {
+        float wv[8], xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) { wv[j] = w[k + j]; xv[j] = x[k + j]; }
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc = fma((double)wv[j], (double)xv[j], acc);
+    }
+    for (; k < hidden; k++) acc = fma((double)w[k], (double)x[k], acc);
+    return acc;
+}
+
+/* The float next to finite f towards +inf (up) or -inf (down). */
+__device__ __forceinline__ float next_float(float f, bool up)
+{
+    if (f == 0.0f) return up ? 0x1p-149f : -0x1p-149f;
+    const uint32_t b = __float_as_uint(f);
+    const bool away = (f > 0.0f) == up;                       /* magnitude grows */
+    return __uint_as_float(away ? b + 1u : b - 1u);
+}
+
+/* Midpoints between f and its float neighbours; a double in (lo, hi) rounds to f. */
+__device__ __forceinline__ void round_interval(float f, double &lo, double &hi)
+{
+    const float dn = next_float(f, false), up = next_float(f, true);
+    lo = isinf(dn) ? -0x1.ffffffp+127 : 0.5 * ((double)f + (double)dn);
+    hi = isinf(up) ? 0x1.ffffffp+127 : 0.5 * ((double)f + (double)up);
+}
+
+/* One workgroup per token, one lane per expert (SL experts per lane past 1024): certify
+ * the logit, score, then topk rounds of the reference's rule -- largest choice, lowest
+ * index among equals, strictly above -inf, none left: idx 0, weight 0 (k3_ops.c:459-467)
+ * -- with a wave argmax and one barrier per round; recompute what matters and repeat;
+ * renormalise and scale (k3_ops.c:469-475). nrecomp[t] (optional) counts recomputes. */
+constexpr int RF_MAXE = 2048, RF_MAXW = 16;
+
+template <int SL>
+__global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt, int *nrecomp,
+                                                            const double *part,
+                                                            const float *rbound, int ksplit,
+                                                            int chunk, const float *x,
+                                                            const float *W, const float *bias,
+                                                            int T, int hidden, int n_experts,
+                                                            int topk, int renorm,
+                                                            float routed_scale, ExcTable exc)
+{
+    __shared__ float rbv[2][RF_MAXW];
+    __shared__ int rbi[2][RF_MAXW];
+    __shared__ float selw[64];
+    __shared__ int selid[64];
+    __shared__ int nre_sh;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+    const int nthr = blockDim.x;
+    const int t = blockIdx.x;
+    if (tid == 0) nre_sh = 0;
+    float c[SL], cmax[SL], sc[SL];
+    bool unc[SL];
+#pragma unroll
+    for (int i = 0; i < SL; i++) {
+        const int e = tid + nthr * i;
+        c[i] = -INFINITY;
+        cmax[i] = -INFINITY;
+        sc[i] = 0.0f;
+        unc[i] = false;
+        if (e < n_experts) {
+            double Q = 0.0, bs = 0.0;
+#pragma unroll 8
+            for (int k = 0; k < ksplit; k++) {
+                const size_t o = ((size_t)k * T + t) * n_experts + e;
+                const int ck = min(chunk, hidden - k * chunk);
+                bs += (double)ck * fabs(Q) + 2.0 * (double)rbound[o];
+                Q += part[o];
+                bs += fabs(Q);
+            }
+            const float f = (float)Q;
+            /* non-finite sums come from inf/NaN inputs and propagate alike in any order */
+            bool ok = true;
+            float fhi = f;
+            if (fabs(Q) <= 0x1.fffffffffffffp+1023) {
+                const double B = 1.01 * 0x1p-53 * bs + 4.0 * 0x1p-53 * fabs(Q) + 0x1p-1060;
+                double mlo, mhi;
+                round_interval(f, mlo, mhi);
+                ok = (Q - B > mlo) && (Q + B < mhi);
+                if (!ok) {
+                    const float hb = (float)(Q + B);
+                    fhi = fabsf(hb) <= 0x1.fffffep+127f ? next_float(hb, true) : hb;
                 }
             }
-            __syncthreads();
-        }
-        if (tid == 0) {
-            const int best = ri[0];
-            if (best < 0) {
-                idx[(size_t)t * topk + j] = 0;
-                wsel[j] = 0.0f;
-            } else {
-                idx[(size_t)t * topk + j] = best;
-                wsel[j] = score[best];
-                choice[best] = -INFINITY;
+            sc[i] = router_score(f, exc);
+            const float bb = bias ? bias[e] : 0.0f;
+            c[i] = sc[i] + bb;
+            cmax[i] = c[i];
+            if (!ok) {
+                unc[i] = true;
+                cmax[i] = router_score(fhi, exc) + bb;      /* choice is monotone in logit */
             }
         }
+    }
+    __syncthreads();
+    for (int round = 0; round <= n_experts; round++) {
+        float cc[SL];
+        bool sel[SL];
+#pragma unroll
+        for (int i = 0; i < SL; i++) { cc[i] = c[i]; sel[i] = false; }
+        float ckth = -INFINITY;
+        int nsel = 0;
+        for (int j = 0; j < topk; j++) {
+            float bv = -INFINITY;
+            int bi = -1;
+#pragma unroll
+            for (int i = 0; i < SL; i++)
+                if (cc[i] > bv) { bv = cc[i]; bi = tid + nthr * i; }
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const float ov = __shfl_xor(bv, o, 64);
+                const int oi = __shfl_xor(bi, o, 64);
+                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+            }
+            if (lane == 0) { rbv[j & 1][wv] = bv; rbi[j & 1][wv] = bi; }
+            __syncthreads();
+            bv = -INFINITY;
+            bi = -1;
+            for (int w = 0; w < nw; w++) {
+                const float ov = rbv[j & 1][w];
+                const int oi = rbi[j & 1][w];
+                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+            }
+            if (bi >= 0) {
+                nsel++;
+                ckth = bv;
+#pragma unroll
+                for (int i = 0; i < SL; i++)
+                    if (bi == tid + nthr * i) {
+                        cc[i] = -INFINITY;
+                        sel[i] = true;
+                        selw[j] = sc[i];
+                        selid[j] = bi;
+                    }
+            } else if (tid == 0) {
+                selw[j] = 0.0f;
+                selid[j] = 0;
+            }
+        }
+        /* uncertified logits that matter: selected, or able to reach the selection */
+        bool need_any = false;
+        bool need[SL];
+#pragma unroll
+        for (int i = 0; i < SL; i++) {
+            need[i] = unc[i] && (sel[i] || nsel < topk || cmax[i] >= ckth);
+            need_any |= need[i];
+        }
+        if (!__syncthreads_or(need_any)) break;
+#pragma unroll
+        for (int i = 0; i < SL; i++)
+            if (need[i]) {
+                const int e = tid + nthr * i;
+                const double a = router_chain(W + (size_t)e * hidden, x + (size_t)t * hidden, hidden);
+                sc[i] = router_score((float)a, exc);
+                c[i] = sc[i] + (bias ? bias[e] : 0.0f);
+                cmax[i] = c[i];
+                unc[i] = false;
+                atomicAdd(&nre_sh, 1);
+            }
         __syncthreads();
     }
-    if (tid == 0) {
+    __syncthreads();
+    if (wv == 0) {
+        float w = lane < topk ? selw[lane] : 0.0f;
         if (renorm && topk > 1) {
             double s = 0.0;
-            for (int j = 0; j < topk; j++) s += (double)wsel[j];
+            for (int j = 0; j < topk; j++) s += (double)__shfl(w, j, 64);   /* j ascending */
             const float inv = (float)(1.0 / (s + 1e-20));
-            for (int j = 0; j < topk; j++) wsel[j] = wsel[j] * inv;
+            w = w * inv;
         }
-        for (int j = 0; j < topk; j++) wt[(size_t)t * topk + j] = wsel[j] * routed_scale;
-        if (nrecomp) nrecomp[t] = 0;
+        if (lane < topk) {
+            idx[(size_t)t * topk + lane] = selid[lane];
+            wt[(size_t)t * topk + lane] = w * routed_scale;
+        }
+        if (nrecomp && lane == 0) nrecomp[t] = nre_sh;
     }
 }
 
@@ -382,31 +624,67 @@ extern "C" int k3k_split_bf16(uint16_t *hi, uint16_t *lo, const float *x, size_t
     return 0;
 }
 
-extern "C" int k3k_router_partial(double *part, const float *x, int T, const float *W, int hidden,
-                                  int n_experts, int ksplit, void *stream)
+extern "C" int k3k_router_chunk(int T, int hidden, int n_experts)
 {
-    if (T <= 0) return 0;
-    dim3 grid((n_experts + RT_E - 1) / RT_E, (T + RT_T - 1) / RT_T, ksplit);
-    hipLaunchKernelGGL(router_partial_kernel, grid, dim3(256), 0, (hipStream_t)stream, part, x, T,
-                       W, hidden, n_experts, ksplit);
+    /* enough workgroups to fill the chip, chunks a multiple of 64 columns */
+    const long tiles = (long)((n_experts + RP_E - 1) / RP_E) * ((T + RP_T - 1) / RP_T);
+    long ks = (2L * k3k_cu_count() + tiles - 1) / tiles;
+    const long kmax = (hidden + 255) / 256;
+    if (ks > kmax) ks = kmax;
+    if (ks < 1) ks = 1;
+    int chunk = (int)((hidden + ks - 1) / ks);
+    chunk = (chunk + RP_KS - 1) / RP_KS * RP_KS;
+    return chunk;
+}
+
+extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, int T,
+                                  const float *W, int hidden, int n_experts, int chunk,
+                                  void *stream)
+{
+    if (T <= 0 || n_experts <= 0) return 0;
+    if (chunk <= 0 || chunk % RP_KS) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
+    const int ks = (hidden + chunk - 1) / chunk;
+    const int vec = (hidden % 4 == 0) && ((((uintptr_t)x) | ((uintptr_t)W)) % 16 == 0);
+    dim3 grid((n_experts + RP_E - 1) / RP_E, (T + RP_T - 1) / RP_T, ks);
+    hipLaunchKernelGGL(router_partial_kernel, grid, dim3(256), 0, (hipStream_t)stream, part,
+                       rbound, x, T, W, hidden, n_experts, chunk, vec);
     K3K_LAUNCH_CHECK("router_partial launch");
     return 0;
 }
 
-extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, int ksplit,
-                                const float *x, const float *W, const float *bias, int T,
-                                int hidden, int n_experts, int topk, int renorm,
-                                float routed_scale, const uint32_t *exc, int n_exc, void *stream)
+extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part,
+                                const float *rbound, int chunk, const float *x, const float *W,
+                                const float *bias, int T, int hidden, int n_experts, int topk,
+                                int renorm, float routed_scale, const K3kExc *exc, void *stream)
 {
-    (void)x;
-    (void)W;
-    (void)hidden;
     if (T <= 0) return 0;
-    if (n_experts > RF_MAXE || topk > K3_MAX_TOPK_DEV)
+    if (n_experts > RF_MAXE || topk > 64)
         return k3k_fail("router_final: n_experts or topk too large", hipErrorInvalidValue);
-    hipLaunchKernelGGL(router_final_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, idx, wt,
-                       nrecomp, part, ksplit, bias, T, n_experts, topk, renorm, routed_scale, exc,
-                       n_exc);
+    ExcTable e;
+    memset(&e, 0, sizeof e);
+    if (exc) {
+        e.pairs = exc->pairs;
+        e.index = exc->index;
+        e.bits = exc->bits;
+        e.kmin = exc->kmin;
+        e.kmax = exc->kmax;
+        e.base = exc->base;
+        e.mmin = exc->mmin;
+        e.mwords = exc->mwords;
+        e.n = exc->n;
+    }
+    const int ks = (hidden + chunk - 1) / chunk;
+    int nw = (n_experts + 63) / 64;
+    if (nw > RF_MAXW) nw = RF_MAXW;
+    hipStream_t st = (hipStream_t)stream;
+    if (n_experts <= 64 * RF_MAXW)
+        hipLaunchKernelGGL(router_final_kernel<1>, dim3(T), dim3(64 * nw), 0, st, idx, wt, nrecomp,
+                           part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm,
+                           routed_scale, e);
+    else
+        hipLaunchKernelGGL(router_final_kernel<2>, dim3(T), dim3(64 * nw), 0, st, idx, wt, nrecomp,
+                           part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm,
+                           routed_scale, e);
     K3K_LAUNCH_CHECK("router_final launch");
     return 0;
 }

@@ -157,7 +157,7 @@ extern "C" int k3k_prof_enable(int max_marks)
         return 0;
     }
     if (max_marks > g_ev_cap) {
-        for (int i = 0; i < g_ev_cap; i++) hipEventDestroy(g_ev[i]);
+        for (int i = 0; i < g_ev_cap; i++) (void)hipEventDestroy(g_ev[i]);
         free(g_ev);
         free(g_ev_stage);
         free(g_ev_stream);

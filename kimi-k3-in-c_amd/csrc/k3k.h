@@ -100,16 +100,30 @@ int k3k_gemv_q8(float *y, const float *x, const void *W, int in, int out, int nt
                 void *stream);
 
 /* ---- router ----------------------------------------------------------------------- */
-/* Logit partials in fp64 over ksplit K-chunks: part[ks][t][e]. */
-int k3k_router_partial(double *part, const float *x, int T, const float *W, int hidden,
-                       int n_experts, int ksplit, void *stream);
-/* Sum partials in fixed order, sigmoid, biased selection, renorm, scale. idx/wt [T][topk].
- * flags [T] receives the number of logits whose fp32 rounding was not certified (and
- * were therefore recomputed in the reference's sequential order). */
-int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, int ksplit,
-                     const float *x, const float *W, const float *bias, int T, int hidden,
-                     int n_experts, int topk, int renorm, float routed_scale,
-                     const uint32_t *exc, int n_exc, void *stream);
+/* The libm expf exception table on the device: sorted (key, value) bit pairs and a bucket
+ * index by key >> 12 over [kmin, kmax] (index[b] = first pair whose (key >> 12) - base >= b),
+ * and a membership bitmap so that a miss costs one load. */
+typedef struct {
+    const uint32_t *pairs, *index;
+    const uint32_t *bits;      /* membership bits of |key| - mmin: [2 signs][mwords] words */
+    uint32_t kmin, kmax, base, mmin, mwords;
+    int n;
+} K3kExc;
+
+/* Router in two launches. k3k_router_partial: per K chunk of `chunk` columns (a multiple
+ * of 64, from k3k_router_chunk), the chunk's fp64 chain part[k][t][e] and a bound
+ * rbound[k][t][e] on its intermediate magnitudes. k3k_router_final: the certified logit
+ * (the reference's sequential fp64 chain recomputed where the bound cannot decide the
+ * fp32 rounding and the logit matters), sigmoid with the host libm's expf, biased
+ * first-strict-max top-k, renorm, scale -> idx/wt [T][topk]; nrecomp [T] (may be NULL)
+ * receives the number of recomputed logits per token. */
+int k3k_router_chunk(int T, int hidden, int n_experts);
+int k3k_router_partial(double *part, float *rbound, const float *x, int T, const float *W,
+                       int hidden, int n_experts, int chunk, void *stream);
+int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, const float *rbound,
+                     int chunk, const float *x, const float *W, const float *bias, int T,
+                     int hidden, int n_experts, int topk, int renorm, float routed_scale,
+                     const K3kExc *exc, void *stream);
 
 /* ---- gather / combine -------------------------------------------------------------- */
 /* Stable expert-major gather of the T*topk assignments in idx (one workgroup). Outputs:

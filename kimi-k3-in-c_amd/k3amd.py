@@ -114,6 +114,7 @@ def _declare(L):
     d("k3d_matmul_bf16", I, P, P, I, P, I, I, P)
     d("k3d_router_ws", SZ, I, I, I)
     d("k3d_router", I, P, P, P, I, P, P, I, I, I, I, F, P, SZ, P)
+    d("k3d_router_recomputed", I, P, P, I, I, I)
     d("k3d_moe_ws", SZ, I, I, I, I, I, I)
     d("k3d_moe_routed", I, P, P, P, P, I, P, P, P, I, I, I, I, I, I, F, I, F, F, I, P, SZ, P, P,
       P, P)
@@ -439,3 +440,32 @@ def moe_routed_device(bank, x, router_w, bias, topk, renorm=1, routed_scale=1.0,
         for v in bufs.values():
             if v is not None:
                 v.free()
+
+
+def router_device(x, W, bias, topk, renorm=1, routed_scale=1.0):
+    """k3d_router over T tokens on the device: host arrays in, idx/wt [T][topk] out."""
+    L = lib()
+    W = _f32(W)
+    n_experts, hidden = W.shape
+    x = _f32(x).reshape(-1, hidden)
+    T = x.shape[0]
+    bufs = [DevBuf(x.nbytes).upload(x), DevBuf(W.nbytes).upload(W),
+            DevBuf(n_experts * 4).upload(_f32(bias)) if bias is not None else None,
+            DevBuf(T * topk * 4), DevBuf(T * topk * 4)]
+    wsb = L.k3d_router_ws(T, hidden, n_experts)
+    bufs.append(DevBuf(wsb))
+    try:
+        dx, dW, db, di, dw, dws = bufs
+        check(L.k3d_router(di.ptr, dw.ptr, dx.ptr, T, dW.ptr, db.ptr if db else None, hidden,
+                           n_experts, topk, renorm, routed_scale, dws.ptr, wsb, None), "k3d_router")
+        check(L.k3d_sync(None), "sync")
+        rec = np.empty(T, np.int32)
+        check(L.k3d_router_recomputed(rec.ctypes.data, dws.ptr, T, hidden, n_experts),
+              "k3d_router_recomputed")
+        router_device.recomputed = rec
+        return (di.download(np.empty((T, topk), np.int32)),
+                dw.download(np.empty((T, topk), np.float32)))
+    finally:
+        for b in bufs:
+            if b is not None:
+                b.free()

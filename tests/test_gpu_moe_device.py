@@ -147,3 +147,83 @@ def test_moe_device_tiled_decode_golden(gpu, wl, gold):
     assert drops == 0
     for t in range(8):
         assert max_err_rel_inf(out[t], gold["moe8_out"][t]) <= TOL, t
+
+
+@pytest.mark.parametrize("T,hidden,N,K,biased", [
+    (1, 7168, 384, 8, False), (7, 7168, 384, 8, True), (31, 1001, 70, 5, True),
+    (33, 1000, 70, 5, False), (64, 7168, 384, 8, False), (100, 520, 131, 16, True)])
+def test_router_device_bit_exact(gpu, orc, T, hidden, N, K, biased):
+    """Both tile shapes of the chain kernel (few / many tokens), widths that are not a
+    multiple of the staging chunk (and an odd one: scalar staging), expert counts that are
+    not a multiple of 64: idx and weight bits equal to the oracle's per-token router."""
+    say(f"case: router T={T} hidden={hidden} N={N} K={K} bias={biased}")
+    rng = np.random.default_rng(T * 1000 + hidden)
+    W = (rng.standard_normal((N, hidden)) * 0.02).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32) if biased else None
+    X = rng.standard_normal((T, hidden)).astype(np.float32)
+    idx, wt = gpu.router_device(X, W, bias, K)
+    say(f"  recomputed logits: {int(gpu.router_device.recomputed.sum())} over {T} tokens")
+    assert gpu.router_device.recomputed.sum() <= max(2, T // 8)   # the fallback stays rare
+    for t in range(T):
+        i2, w2 = orc.router(X[t], W, bias, K)
+        assert np.array_equal(idx[t], i2), t
+        assert np.array_equal(bits(wt[t]), bits(w2)), t
+
+
+def test_router_device_ties_and_nonfinite(gpu, orc):
+    """Duplicate expert rows give equal choices (lowest index wins); a NaN and a -inf bias
+    keep an expert from ever being chosen; fewer finite candidates than topk give idx 0,
+    weight 0 (reference first-strict-max rule)."""
+    say("case: router ties and non-finite choices")
+    rng = np.random.default_rng(5)
+    N, hidden, K = 12, 256, 6
+    W = (rng.standard_normal((N, hidden)) * 0.05).astype(np.float32)
+    W[7] = W[2]
+    W[9] = W[2]
+    X = rng.standard_normal((3, hidden)).astype(np.float32)
+    bias = np.zeros(N, np.float32)
+    bias[4] = np.nan
+    bias[5] = -np.inf
+    for b in (None, bias):
+        idx, wt = gpu.router_device(X, W, b, K)
+        for t in range(3):
+            i2, w2 = orc.router(X[t], W, b, K)
+            assert np.array_equal(idx[t], i2), (t, idx[t], i2)
+            assert np.array_equal(bits(wt[t]), bits(w2)), t
+    allbad = np.full(N, -np.inf, np.float32)
+    allbad[:3] = 0.0
+    idx, wt = gpu.router_device(X, W, allbad, K)
+    for t in range(3):
+        i2, w2 = orc.router(X[t], W, allbad, K)
+        assert np.array_equal(idx[t], i2) and np.array_equal(bits(wt[t]), bits(w2))
+        assert list(idx[t][3:]) == [0, 0, 0] and not wt[t][3:].any()
+
+
+@pytest.mark.parametrize("hidden", [1024, 7168])
+def test_router_device_uncertified_logits(gpu, orc, hidden):
+    """Rows built so that a chunked fp64 sum and the reference's sequential chain round to
+    different floats (1 + 2^-24 - 2^-52 then 2^-53 terms: the chain ties to even at every
+    step, a chunked sum does not): the router must detect the ambiguous rounding and use
+    the reference's chain. Expert 2's logit is exactly 1.0, a tie with the crafted experts
+    under the reference (lowest index first), and the crafted experts carry the largest
+    weights, so both the order of idx and the weight bits would expose a wrong logit."""
+    say(f"case: router uncertified logits hidden={hidden}")
+    N, K = 16, 4
+    rng = np.random.default_rng(hidden)
+    W = (rng.standard_normal((N, hidden)) * 1e-3).astype(np.float32)
+    crafted = np.full(hidden, 2.0 ** -53, np.float32)
+    crafted[:3] = [1.0, 2.0 ** -24, -2.0 ** -52]
+    for e in (5, 11):
+        W[e] = crafted
+    W[2] = 0.0
+    W[2, 0] = 1.0
+    X = np.stack([np.ones(hidden, np.float32),
+                  rng.standard_normal(hidden).astype(np.float32)])
+    idx, wt = gpu.router_device(X, W, None, K)
+    rec = gpu.router_device.recomputed
+    for t in range(2):
+        i2, w2 = orc.router(X[t], W, None, K)
+        assert np.array_equal(idx[t], i2), (t, idx[t], i2)
+        assert np.array_equal(bits(wt[t]), bits(w2)), t
+    assert list(idx[0][:3]) == [2, 5, 11]
+    assert rec[0] >= 2          # both crafted logits went through the reference's chain
