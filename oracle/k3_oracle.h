@@ -2,7 +2,7 @@
 /*
  * k3_oracle.h -- CPU restatement of the kimi-k3-in-c routed-MoE hot path.
  *
- * TEST INFRASTRUCTURE ONLY. This is the checker that the HIP library is compared
+ * TEST INFRASTRUCTURE ONLY. This is the oracle that the HIP library is compared
  * against. Only tests/, the smoke entry point and the CPU-baseline leg of bench.py load
  * it; the product library never links or calls it.
  *
@@ -11,7 +11,7 @@
  * with AVX2 + FMA and -ffp-contract=off, which is the path the reference's own build
  * selects on this class of host). "Restates" means the same operations in the same order
  * with the same rounding, so the outputs are bit-identical to the reference build; the
- * tests in tests/test_oracle_*.py check exactly that against the compiled reference and
+ * tests in tests/test_oracle.py check exactly that against the compiled reference and
  * the reference's fixtures.
  */
 #ifndef K3_ORACLE_H
