@@ -63,11 +63,11 @@ class Layer:
         self.bank = k3amd.DevBank(Lazy(), E, I, layout)
         self.router = k3amd.DevBuf(ROUTER_BYTES).upload(wl.router_weights())
 
-    def run(self, x, out, idx, wt, T, ws, prec=0):
+    def run(self, x, out, idx, wt, T, ws, prec=0, stream=None):
         k3amd.check(k3amd.lib().k3d_moe_routed(
             out.ptr, idx.ptr, wt.ptr, x.ptr, T, self.router.ptr, None, self.bank.table.ptr,
             self.layout, E, I, N, K, 1, 1.0, k3amd.K3_ACT_SILU, 4.0, 25.0, prec, ws.ptr, ws.nbytes,
-            None, None, None, None), "k3d_moe_routed")
+            None, None, None, stream), "k3d_moe_routed")
 
 
 def time_layer(layer, T, steps, warmup, nbatch=4):
@@ -82,15 +82,33 @@ def time_layer(layer, T, steps, warmup, nbatch=4):
         layer.run(xs[b], out, idx, wt, T, ws)
         h = idx.download(np.empty((T, K), np.int32))
         uniq.append(len(np.unique(h)))
+    # one HIP graph per token batch: the whole layer replayed with one launch per step
+    stream = L.k3d_stream_create()
+    if not stream:
+        raise RuntimeError("k3d_stream_create: " + L.k3d_error().decode())
+    graphs = []
+    for b in range(nbatch):
+        k3amd.check(L.k3d_graph_begin(stream), "k3d_graph_begin")
+        layer.run(xs[b], out, idx, wt, T, ws, stream=stream)
+        ex = C.c_void_p()
+        k3amd.check(L.k3d_graph_end(stream, C.byref(ex)), "k3d_graph_end")
+        graphs.append(ex)
     for s in range(warmup):
-        layer.run(xs[s % nbatch], out, idx, wt, T, ws)
-    k3amd.check(L.k3d_sync(None))
-    prof = k3amd.Profile(max_marks=16 * steps + 64)
-    t0 = time.perf_counter()
+        k3amd.check(L.k3d_graph_launch(graphs[s % nbatch], stream), "k3d_graph_launch")
+    k3amd.check(L.k3d_sync(stream))
+    t0 = time.perf_counter()                      # timed steps: graph replays, no profiler
     for s in range(steps):
+        k3amd.check(L.k3d_graph_launch(graphs[s % nbatch], stream), "k3d_graph_launch")
+    k3amd.check(L.k3d_sync(stream))
+    t1 = time.perf_counter()
+    for g in graphs:
+        L.k3d_graph_destroy(g)
+    L.k3d_stream_destroy(stream)
+    nprof = min(steps, 20)                        # stage breakdown: a separate profiled run
+    prof = k3amd.Profile(max_marks=16 * nprof + 64)
+    for s in range(nprof):
         layer.run(xs[s % nbatch], out, idx, wt, T, ws)
     k3amd.check(L.k3d_sync(None))
-    t1 = time.perf_counter()
     stages = prof.end()
     for b in xs + [out, idx, wt, ws]:
         b.free()

@@ -22,6 +22,8 @@
 extern "C" {
 #endif
 
+/* Selects the device and uploads the router's tables once; after it, no entry point below
+ * allocates or synchronises (except k3d_malloc/free/sync and the copies). */
 int k3d_init(void);
 const char *k3d_error(void);
 void *k3d_malloc(size_t bytes);
@@ -29,6 +31,17 @@ int k3d_free(void *p);
 int k3d_h2d(void *dst, const void *src, size_t bytes, void *stream);
 int k3d_d2h(void *dst, const void *src, size_t bytes, void *stream);
 int k3d_sync(void *stream);
+
+/* Streams (default priority) and HIP graphs: k3d_graph_begin/end capture everything the
+ * k3d_* calls enqueue on a created stream between them (no allocation or synchronisation
+ * happens inside those calls); k3d_graph_launch replays it with one launch. The captured
+ * pointers are baked in: replay with the same buffers, new contents. */
+void *k3d_stream_create(void);
+int k3d_stream_destroy(void *stream);
+int k3d_graph_begin(void *stream);
+int k3d_graph_end(void *stream, void **exec);
+int k3d_graph_launch(void *exec, void *stream);
+int k3d_graph_destroy(void *exec);
 
 /* Stage profiler (HIP events). Between k3d_prof_begin and k3d_prof_end, the MoE and GEMV
  * entry points record an event at each stage boundary; k3d_prof_end synchronises and

@@ -31,7 +31,28 @@ static int bad(const char *what)
 
 const char *k3d_error(void) { return g_msg; }
 
-int k3d_init(void) { return k3k_init() ? fail("init") : 0; }
+static int exc_table(const K3kExc **out);
+
+/* Device selection and the one-time uploads (router tables), so that no later entry point
+ * allocates or synchronises and the layer can be captured in a graph. */
+int k3d_init(void)
+{
+    if (k3k_init()) return fail("init");
+    const K3kExc *e;
+    return exc_table(&e);
+}
+void *k3d_stream_create(void)
+{
+    if (k3d_init()) return NULL;
+    void *s = k3k_stream_create();
+    if (!s) fail("k3d_stream_create");
+    return s;
+}
+int k3d_stream_destroy(void *s) { return k3k_stream_destroy(s) ? fail("k3d_stream_destroy") : 0; }
+int k3d_graph_begin(void *s) { return k3k_graph_begin(s) ? fail("k3d_graph_begin") : 0; }
+int k3d_graph_end(void *s, void **exec) { return k3k_graph_end(s, exec) ? fail("k3d_graph_end") : 0; }
+int k3d_graph_launch(void *exec, void *s) { return k3k_graph_launch(exec, s) ? fail("k3d_graph_launch") : 0; }
+int k3d_graph_destroy(void *exec) { return k3k_graph_destroy(exec) ? fail("k3d_graph_destroy") : 0; }
 void *k3d_malloc(size_t bytes)
 {
     if (k3d_init()) return NULL;

@@ -43,6 +43,8 @@
  *   DOWN   expert jobs; activation rows are assignments; contrib[assignment][hidden].
  */
 #include "k3_common.h"
+
+#include <type_traits>
 #include "k3k.h"
 
 namespace {
@@ -268,7 +270,7 @@ int launch_mx(const K3kMxArgs *a, int kw, int grid, hipStream_t st)
  * c+1 are in flight (activations issued first, so waiting for them leaves the weight
  * loads outstanding).
  */
-template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT>
+template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT, int DEPTH>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
 void mx_moe_kernel(K3kMxArgs a)
 {
@@ -350,10 +352,14 @@ void mx_moe_kernel(K3kMxArgs a)
 #pragma unroll
         for (int m = 0; m < MT; m++) acc[m] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
 
-        /* One register set per step of a chunk: step d's weights for chunk c+1 are loaded
-         * into qa[d] right after step d of chunk c has consumed them. */
-        uint4 qa[SPC][MT];
-        uint32_t sq[MT * (LAYOUT == 0 ? 4 : 1)], sqn[MT * (LAYOUT == 0 ? 4 : 1)];
+        /* Weights in registers, DEPTH chunks ahead: qa[slot][d] holds step d of a chunk.
+         * DEPTH 1: step d of chunk c+1 is loaded into qa[0][d] right after step d of chunk
+         * c has consumed it. DEPTH 2: chunks alternate between two slots and step d of
+         * chunk c+2 is loaded into chunk c's slot. Scales follow one chunk behind. */
+        constexpr int NSLOT = DEPTH == 2 ? 2 : 1;
+        constexpr int SQN = MT * (LAYOUT == 0 ? 4 : 1);
+        uint4 qa[NSLOT][SPC][MT];
+        uint32_t sq[SQN], sqn[SQN], sqnn[SQN];
         uint4 bst[PPW];
 
         auto load_b = [&](int c) {
@@ -372,12 +378,13 @@ void mx_moe_kernel(K3kMxArgs a)
                     *reinterpret_cast<uint4 *>(&bsh[buf][rh % NS][rh / NS][lane * 8]) = bst[i];
             }
         };
-        auto load_step = [&](int c, int d) {
+        auto load_step = [&](int c, int d, auto slot) {
+            constexpr int S = decltype(slot)::value;
             const uint32_t bo = LAYOUT == 0 ? (uint32_t)c * 256u + (uint32_t)d * 64u
                                             : ((uint32_t)c * 4u + (uint32_t)d) * 1024u;
 #pragma unroll
             for (int m = 0; m < MT; m++)
-                qa[d][m] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo);
+                qa[S][d][m] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo);
         };
         auto load_scales = [&](int c, uint32_t *ss) {
 #pragma unroll
@@ -392,22 +399,29 @@ void mx_moe_kernel(K3kMxArgs a)
             }
         };
 
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, NSLOT - 1>;
         load_b(0);
         load_scales(0, sq);
 #pragma unroll
-        for (int d = 0; d < SPC; d++) load_step(0, d);
+        for (int d = 0; d < SPC; d++) load_step(0, d, I0{});
+        if (DEPTH == 2 && nchunk > 1) {
+            load_scales(1, sqn);
+#pragma unroll
+            for (int d = 0; d < SPC; d++) load_step(1, d, I1{});
+        }
         store_b(0);
         __syncthreads();
-        for (int c = 0; c < nchunk; c++) {
+        auto chunk = [&](int c, auto slot) {
+            constexpr int S = decltype(slot)::value;
             const int buf = c & 1;
             const bool more = c + 1 < nchunk;
-            if (more) {
-                load_b(c + 1);
-                load_scales(c + 1, sqn);
-            }
+            const bool more2 = c + DEPTH < nchunk;
+            if (more) load_b(c + 1);
+            if (more2) load_scales(c + DEPTH, DEPTH == 2 ? sqnn : sqn);
 #pragma unroll
             for (int d = 0; d < SPC; d++) {
-                /* B operand: token column r16 (or the zero row), block 4g+d of the chunk */
+                /* B operand: token column r16 (or the zero row), block 4d+g of the chunk */
                 uint4 bh[4], bl[4];
                 const uint4 *bp = reinterpret_cast<const uint4 *>(&bsh[buf][0][brow][(4 * d + g) * 32]);
                 const uint4 *bq = reinterpret_cast<const uint4 *>(&bsh[buf][NS - 1][brow][(4 * d + g) * 32]);
@@ -423,7 +437,7 @@ void mx_moe_kernel(K3kMxArgs a)
                     const uint32_t sraw = LAYOUT == 0 ? (sq[4 * m + d] >> (8 * g)) & 0xFFu
                                                       : (sq[m] >> (8 * d)) & 0xFFu;
                     const bool nanb = sraw == 255u;          /* NaN byte: the block is 0 */
-                    qq[m] = qa[d][m];
+                    qq[m] = qa[S][d][m];
                     qq[m].x = nanb ? 0u : qq[m].x;
                     qq[m].y = nanb ? 0u : qq[m].y;
                     qq[m].z = nanb ? 0u : qq[m].z;
@@ -440,14 +454,19 @@ void mx_moe_kernel(K3kMxArgs a)
                         if (NS == 2)
                             acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl[pp]), acc[m], 0, 0, 0);
                     }
-                if (more) load_step(c + 1, d);
+                if (more2) load_step(c + DEPTH, d, slot);
             }
-            if (more) {
-                store_b(buf ^ 1);
+            if (more) store_b(buf ^ 1);
 #pragma unroll
-                for (int m = 0; m < MT * (LAYOUT == 0 ? 4 : 1); m++) sq[m] = sqn[m];
+            for (int m = 0; m < SQN; m++) {
+                sq[m] = sqn[m];
+                if (DEPTH == 2) sqn[m] = sqnn[m];
             }
             __syncthreads();
+        };
+        for (int c = 0; c < nchunk; c += NSLOT) {
+            chunk(c, I0{});
+            if (NSLOT == 2 && c + 1 < nchunk) chunk(c + 1, I1{});
         }
 
         /* epilogue: lane holds token column r16, rows 4g..4g+3 of each tile */
@@ -483,10 +502,10 @@ void mx_moe_kernel(K3kMxArgs a)
     }
 }
 
-template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT>
+template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT, int DEPTH = 1>
 int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((mx_moe_kernel<MODE, MT, NS, PT, NW, WPE, LAYOUT>), dim3(grid), dim3(64 * NW),
+    hipLaunchKernelGGL((mx_moe_kernel<MODE, MT, NS, PT, NW, WPE, LAYOUT, DEPTH>), dim3(grid), dim3(64 * NW),
                        0, st, *a);
     K3K_LAUNCH_CHECK("mx_moe launch");
     return 0;
@@ -584,24 +603,30 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
         return launch_mx<K3K_MX_PLAIN, 1, 1, 1, 2, 16>(a, kw, grid, st);
     }
     if (a->pass_tok == 8) {
-        /* LDS-staged expert kernel: K % 512 == 0; 4 waves x 4 tiles of 16 rows per item */
+        /* LDS-staged expert kernel: K % 512 == 0. Items are 4 waves x MT tiles of 16 rows;
+         * when there are too few of them to fill the chip (decode at batch 1-4), halve the
+         * tiles per wave so that twice as many workgroups stream weights. */
         if (a->K % 512) return k3k_fail("mx_moe: K % 512 != 0", hipErrorInvalidValue);
-        const int rpg = mode == K3K_MX_GATEUP ? 128 : 256;
+        const bool gu = mode == K3K_MX_GATEUP;
+        const long items4 = (long)a->max_passes * ((a->rows + (gu ? 127 : 255)) / (gu ? 128 : 256));
+        const bool small = items4 < 2L * cus;
+        const int rpg = gu ? (small ? 64 : 128) : (small ? 128 : 256);
         const long items = (long)a->max_passes * ((a->rows + rpg - 1) / rpg);
         const int grid = (int)(items < (long)cus * 4 ? (items > 0 ? items : 1) : (long)cus * 4);
         const bool tiled = a->layout == 1;
-        if (mode == K3K_MX_GATEUP) {
-            if (a->nsplit == 2)
-                return tiled ? launch_moe<K3K_MX_GATEUP, 4, 2, 8, 4, 2, 1>(a, grid, st)
-                             : launch_moe<K3K_MX_GATEUP, 4, 2, 8, 4, 2, 0>(a, grid, st);
-            return tiled ? launch_moe<K3K_MX_GATEUP, 4, 1, 8, 4, 2, 1>(a, grid, st)
-                         : launch_moe<K3K_MX_GATEUP, 4, 1, 8, 4, 2, 0>(a, grid, st);
+        const bool ns2 = a->nsplit == 2;
+#define K3_MOE_LAUNCH(MODE, MT)                                                              \
+    return tiled ? (ns2 ? launch_moe<MODE, MT, 2, 8, 4, 2, 1>(a, grid, st)                   \
+                        : launch_moe<MODE, MT, 1, 8, 4, 2, 1>(a, grid, st))                  \
+                 : (ns2 ? launch_moe<MODE, MT, 2, 8, 4, 2, 0>(a, grid, st)                   \
+                        : launch_moe<MODE, MT, 1, 8, 4, 2, 0>(a, grid, st))
+        if (gu) {
+            if (small) K3_MOE_LAUNCH(K3K_MX_GATEUP, 2);
+            K3_MOE_LAUNCH(K3K_MX_GATEUP, 4);
         }
-        if (a->nsplit == 2)
-            return tiled ? launch_moe<K3K_MX_DOWN, 4, 2, 8, 4, 2, 1>(a, grid, st)
-                         : launch_moe<K3K_MX_DOWN, 4, 2, 8, 4, 2, 0>(a, grid, st);
-        return tiled ? launch_moe<K3K_MX_DOWN, 4, 1, 8, 4, 2, 1>(a, grid, st)
-                     : launch_moe<K3K_MX_DOWN, 4, 1, 8, 4, 2, 0>(a, grid, st);
+        if (small) K3_MOE_LAUNCH(K3K_MX_DOWN, 2);
+        K3_MOE_LAUNCH(K3K_MX_DOWN, 4);
+#undef K3_MOE_LAUNCH
     }
     if (a->pass_tok != 16 || a->layout != 0)
         return k3k_fail("mx_gemm: expert passes of 16 tokens need the row-major layout",

@@ -231,6 +231,75 @@ __global__ __launch_bounds__(256) void router_partial_kernel(double *part, float
         }
 }
 
+/* The same partials for a few tokens (T <= RS_T): one lane per (expert, chunk) runs the
+ * chunk's chain for every token; the lane streams its W row segment itself (float4), the
+ * tokens' chunk is staged in LDS as fp64 and read as broadcasts. The bound R_k per chain
+ * uses the lane's own running sum of |w| over each 32-column sub-block. */
+constexpr int RS_T = 4;
+
+template <int NT>
+__global__ __launch_bounds__(256) void router_partial_small_kernel(double *part, float *rbound,
+                                                                   const float *x, int T,
+                                                                   const float *W, int hidden,
+                                                                   int n_experts, int chunk,
+                                                                   int vec)
+{
+    extern __shared__ double xsh[];                  /* [NT][chunk] */
+    const int ks = blockIdx.y;
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    const int kb0 = ks * chunk, kb1 = min(hidden, kb0 + chunk);
+    const int len = kb1 - kb0;
+    for (int i = threadIdx.x; i < NT * chunk; i += 256) {
+        const int t = i / chunk, k = i % chunk;
+        xsh[i] = (t < T && k < len) ? (double)x[(size_t)t * hidden + kb0 + k] : 0.0;
+    }
+    __syncthreads();
+    if (e >= n_experts) return;
+    /* sub-block maxima of |x| per token */
+    const float *wr = W + (size_t)e * hidden + kb0;
+    double acc[NT], rb[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) { acc[t] = 0.0; rb[t] = 0.0; }
+    for (int s0 = 0; s0 < len; s0 += 32) {
+        const int sl = min(32, len - s0);
+        float wv[32];
+        if (vec && sl == 32) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float4 v = *reinterpret_cast<const float4 *>(wr + s0 + 4 * q);
+                wv[4 * q] = v.x; wv[4 * q + 1] = v.y; wv[4 * q + 2] = v.z; wv[4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 32; q++) wv[q] = q < sl ? wr[s0 + q] : 0.0f;
+        }
+        float wn = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 32; q++) wn += fabsf(wv[q]);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            double xm = 0.0;
+#pragma unroll
+            for (int q = 0; q < 32; q++) xm = fmax(xm, fabs(xsh[t * chunk + s0 + min(q, sl - 1)]));
+            rb[t] = fma(32.0, fabs(acc[t]) + (double)wn * xm, rb[t]);
+        }
+#pragma unroll
+        for (int q = 0; q < 32; q++) {
+            const double wd = (double)wv[q];
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+                if (q < sl) acc[t] = fma(wd, xsh[t * chunk + s0 + q], acc[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+        if (t < T) {
+            const size_t o = ((size_t)ks * T + t) * n_experts + e;
+            part[o] = acc[t];
+            rbound[o] = (float)(rb[t] * (1.0 + 0x1p-17)) * (1.0f + 0x1p-20f);
+        }
+}
+
 /* The reference's own chain for one logit (the fallback of the certification). */
 __device__ __forceinline__ double router_chain(const float *w, const float *x, int hidden)
 {
@@ -269,7 +338,7 @@ __device__ __forceinline__ void round_interval(float f, double &lo, double &hi)
  * index among equals, strictly above -inf, none left: idx 0, weight 0 (k3_ops.c:459-467)
  * -- with a wave argmax and one barrier per round; recompute what matters and repeat;
  * renormalise and scale (k3_ops.c:469-475). nrecomp[t] (optional) counts recomputes. */
-constexpr int RF_MAXE = 2048, RF_MAXW = 16;
+constexpr int RF_MAXE = 2048, RF_MAXW = 16, RF_KB = 32;
 
 template <int SL>
 __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt, int *nrecomp,
@@ -301,13 +370,27 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
         unc[i] = false;
         if (e < n_experts) {
             double Q = 0.0, bs = 0.0;
-#pragma unroll 8
-            for (int k = 0; k < ksplit; k++) {
-                const size_t o = ((size_t)k * T + t) * n_experts + e;
-                const int ck = min(chunk, hidden - k * chunk);
-                bs += (double)ck * fabs(Q) + 2.0 * (double)rbound[o];
-                Q += part[o];
-                bs += fabs(Q);
+            for (int k0 = 0; k0 < ksplit; k0 += RF_KB) {
+                /* one batch of chunk loads in flight together */
+                double pv[RF_KB];
+                float rv[RF_KB];
+#pragma unroll
+                for (int kk = 0; kk < RF_KB; kk++) {
+                    const int k = min(k0 + kk, ksplit - 1);
+                    const size_t o = ((size_t)k * T + t) * n_experts + e;
+                    pv[kk] = part[o];
+                    rv[kk] = rbound[o];
+                }
+#pragma unroll
+                for (int kk = 0; kk < RF_KB; kk++) {
+                    const int k = k0 + kk;
+                    if (k < ksplit) {
+                        const int ck = min(chunk, hidden - k * chunk);
+                        bs += (double)ck * fabs(Q) + 2.0 * (double)rv[kk];
+                        Q += pv[kk];
+                        bs += fabs(Q);
+                    }
+                }
             }
             const float f = (float)Q;
             /* non-finite sums come from inf/NaN inputs and propagate alike in any order */
@@ -626,7 +709,13 @@ extern "C" int k3k_split_bf16(uint16_t *hi, uint16_t *lo, const float *x, size_t
 
 extern "C" int k3k_router_chunk(int T, int hidden, int n_experts)
 {
-    /* enough workgroups to fill the chip, chunks a multiple of 64 columns */
+    if (T <= RS_T) {
+        /* one lane per (expert, chunk): 256-column chunks, at most 32 of them */
+        int chunk = 256;
+        while ((hidden + chunk - 1) / chunk > RF_KB) chunk += 256;
+        return chunk;
+    }
+    /* enough workgroups to fill the chip, chunks a multiple of 32 columns */
     const long tiles = (long)((n_experts + RP_E - 1) / RP_E) * ((T + RP_T - 1) / RP_T);
     long ks = (2L * k3k_cu_count() + tiles - 1) / tiles;
     const long kmax = (hidden + 255) / 256;
@@ -645,9 +734,21 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
     if (chunk <= 0 || chunk % RP_KS) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
     const int ks = (hidden + chunk - 1) / chunk;
     const int vec = (hidden % 4 == 0) && ((((uintptr_t)x) | ((uintptr_t)W)) % 16 == 0);
-    dim3 grid((n_experts + RP_E - 1) / RP_E, (T + RP_T - 1) / RP_T, ks);
-    hipLaunchKernelGGL(router_partial_kernel, grid, dim3(256), 0, (hipStream_t)stream, part,
-                       rbound, x, T, W, hidden, n_experts, chunk, vec);
+    hipStream_t st = (hipStream_t)stream;
+    if (T <= RS_T) {
+        dim3 grid((n_experts + 255) / 256, ks);
+        const size_t lds = (size_t)RS_T * chunk * sizeof(double);
+        if (T == 1)
+            hipLaunchKernelGGL(router_partial_small_kernel<1>, grid, dim3(256), (size_t)chunk * 8, st,
+                               part, rbound, x, T, W, hidden, n_experts, chunk, vec);
+        else
+            hipLaunchKernelGGL(router_partial_small_kernel<RS_T>, grid, dim3(256), lds, st, part,
+                               rbound, x, T, W, hidden, n_experts, chunk, vec);
+    } else {
+        dim3 grid((n_experts + RP_E - 1) / RP_E, (T + RP_T - 1) / RP_T, ks);
+        hipLaunchKernelGGL(router_partial_kernel, grid, dim3(256), 0, st, part, rbound, x, T, W,
+                           hidden, n_experts, chunk, vec);
+    }
     K3K_LAUNCH_CHECK("router_partial launch");
     return 0;
 }

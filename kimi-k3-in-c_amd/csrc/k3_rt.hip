@@ -142,6 +142,40 @@ extern "C" int k3k_stream_destroy(void *stream)
     return e == hipSuccess ? 0 : k3k_fail("hipStreamDestroy", e);
 }
 
+/* ---- HIP graphs: capture the work enqueued on a stream once, replay it with one launch */
+extern "C" int k3k_graph_begin(void *stream)
+{
+    if (!stream) return k3k_fail("graph capture needs a created stream", hipErrorInvalidValue);
+    hipError_t e = hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal);
+    return e == hipSuccess ? 0 : k3k_fail("hipStreamBeginCapture", e);
+}
+
+extern "C" int k3k_graph_end(void *stream, void **exec)
+{
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture((hipStream_t)stream, &g);
+    if (e != hipSuccess) return k3k_fail("hipStreamEndCapture", e);
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return k3k_fail("hipGraphInstantiate", e);
+    *exec = (void *)x;
+    return 0;
+}
+
+extern "C" int k3k_graph_launch(void *exec, void *stream)
+{
+    hipError_t e = hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : k3k_fail("hipGraphLaunch", e);
+}
+
+extern "C" int k3k_graph_destroy(void *exec)
+{
+    if (!exec) return 0;
+    hipError_t e = hipGraphExecDestroy((hipGraphExec_t)exec);
+    return e == hipSuccess ? 0 : k3k_fail("hipGraphExecDestroy", e);
+}
+
 /* ---- stage profiler ------------------------------------------------------------------ */
 namespace {
 hipEvent_t *g_ev = nullptr;

@@ -31,6 +31,11 @@ int k3k_sync(void *stream);
 void *k3k_stream_create(void);
 int k3k_stream_destroy(void *stream);
 int k3k_cu_count(void);
+/* Graph capture of the work enqueued on `stream` (a created stream, not NULL). */
+int k3k_graph_begin(void *stream);
+int k3k_graph_end(void *stream, void **exec);
+int k3k_graph_launch(void *exec, void *stream);
+int k3k_graph_destroy(void *exec);
 
 /* Stage profiler: while enabled, k3k_prof_mark(stream, stage) records a HIP event on the
  * stream; k3k_prof_collect() waits for the device and sums, per stage, the time from the

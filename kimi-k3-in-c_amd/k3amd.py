@@ -105,6 +105,12 @@ def _declare(L):
     d("k3d_h2d", I, P, P, SZ, P)
     d("k3d_d2h", I, P, P, SZ, P)
     d("k3d_sync", I, P)
+    d("k3d_stream_create", P)
+    d("k3d_stream_destroy", I, P)
+    d("k3d_graph_begin", I, P)
+    d("k3d_graph_end", I, P, P)
+    d("k3d_graph_launch", I, P, P)
+    d("k3d_graph_destroy", I, P)
     d("k3d_prof_begin", I, I)
     d("k3d_prof_mark", I, P, I)
     d("k3d_prof_end", I, P, P, I)

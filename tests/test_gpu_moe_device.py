@@ -150,7 +150,8 @@ def test_moe_device_tiled_decode_golden(gpu, wl, gold):
 
 
 @pytest.mark.parametrize("T,hidden,N,K,biased", [
-    (1, 7168, 384, 8, False), (7, 7168, 384, 8, True), (31, 1001, 70, 5, True),
+    (1, 7168, 384, 8, False), (2, 1001, 70, 5, True), (3, 7168, 384, 8, True),
+    (7, 7168, 384, 8, True), (31, 1001, 70, 5, True),
     (33, 1000, 70, 5, False), (64, 7168, 384, 8, False), (100, 520, 131, 16, True)])
 def test_router_device_bit_exact(gpu, orc, T, hidden, N, K, biased):
     """Both tile shapes of the chain kernel (few / many tokens), widths that are not a
@@ -200,7 +201,8 @@ def test_router_device_ties_and_nonfinite(gpu, orc):
 
 
 @pytest.mark.parametrize("hidden", [1024, 7168])
-def test_router_device_uncertified_logits(gpu, orc, hidden):
+@pytest.mark.parametrize("ntok", [2, 40])
+def test_router_device_uncertified_logits(gpu, orc, hidden, ntok):
     """Rows built so that a chunked fp64 sum and the reference's sequential chain round to
     different floats (1 + 2^-24 - 2^-52 then 2^-53 terms: the chain ties to even at every
     step, a chunked sum does not): the router must detect the ambiguous rounding and use
@@ -217,13 +219,73 @@ def test_router_device_uncertified_logits(gpu, orc, hidden):
         W[e] = crafted
     W[2] = 0.0
     W[2, 0] = 1.0
-    X = np.stack([np.ones(hidden, np.float32),
-                  rng.standard_normal(hidden).astype(np.float32)])
+    X = np.stack([np.ones(hidden, np.float32)] +
+                 [rng.standard_normal(hidden).astype(np.float32) for _ in range(ntok - 1)])
     idx, wt = gpu.router_device(X, W, None, K)
     rec = gpu.router_device.recomputed
-    for t in range(2):
+    for t in range(ntok):
         i2, w2 = orc.router(X[t], W, None, K)
         assert np.array_equal(idx[t], i2), (t, idx[t], i2)
         assert np.array_equal(bits(wt[t]), bits(w2)), t
     assert list(idx[0][:3]) == [2, 5, 11]
     assert rec[0] >= 2          # both crafted logits went through the reference's chain
+
+
+def test_moe_graph_replay_matches_eager(gpu, small_layer):
+    """The layer captured once in a HIP graph (k3d_graph_*) and replayed with new input
+    contents, with eager work and synchronisation between replays: every replay equals
+    the eager call on the same input, bit for bit."""
+    import ctypes as C
+    s = small_layer
+    say("case: graph replay vs eager")
+    L = gpu.lib()
+    E, I, N, K, T = s["E"], s["I"], s["N"], s["K"], s["T"]
+    bank = gpu.DevBank(s["bank"], E, I, gpu.K3D_LAYOUT_TILED)
+    rng = np.random.default_rng(77)
+    xs = [rng.standard_normal((T, E)).astype(np.float32) for _ in range(3)]
+    dx = gpu.DevBuf(T * E * 4)
+    dw = gpu.DevBuf(s["W"].nbytes).upload(s["W"])
+    db = gpu.DevBuf(N * 4).upload(s["bias"])
+    out, idx, wt = gpu.DevBuf(T * E * 4), gpu.DevBuf(T * K * 4), gpu.DevBuf(T * K * 4)
+    wsb = L.k3d_moe_ws(T, E, I, N, K, 0)
+    ws = gpu.DevBuf(wsb)
+    stream = L.k3d_stream_create()
+    assert stream
+
+    def call(st):
+        gpu.check(L.k3d_moe_routed(out.ptr, idx.ptr, wt.ptr, dx.ptr, T, dw.ptr, db.ptr, bank.table.ptr,
+                                   bank.layout, E, I, N, K, 1, 1.0, gpu.K3_ACT_SILU, 4.0, 25.0, 0,
+                                   ws.ptr, wsb, None, None, None, st), "k3d_moe_routed")
+
+    def results():
+        return (out.download(np.empty((T, E), np.float32)), idx.download(np.empty((T, K), np.int32)),
+                wt.download(np.empty((T, K), np.float32)))
+    try:
+        eager = []
+        for x in xs:
+            dx.upload(x)
+            call(None)
+            gpu.check(L.k3d_sync(None), "sync")
+            eager.append(results())
+        dx.upload(xs[0])
+        gpu.check(L.k3d_graph_begin(stream), "graph_begin")
+        call(stream)
+        ex = C.c_void_p()
+        gpu.check(L.k3d_graph_end(stream, C.byref(ex)), "graph_end")
+        for rep in range(6):
+            i = rep % 3
+            dx.upload(xs[i])
+            call(None)                                   # eager work between replays
+            gpu.check(L.k3d_sync(None), "sync")
+            gpu.check(L.k3d_graph_launch(ex, stream), "graph_launch")
+            gpu.check(L.k3d_sync(stream), "sync")
+            got = results()
+            for a, b in zip(got, eager[i]):
+                assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                                      b.view(np.uint32) if b.dtype == np.float32 else b), rep
+        L.k3d_graph_destroy(ex)
+    finally:
+        L.k3d_stream_destroy(stream)
+        for b in (dx, dw, db, out, idx, wt, ws):
+            b.free()
+        bank.free()
