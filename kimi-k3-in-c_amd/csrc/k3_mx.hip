@@ -605,7 +605,8 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
     if (a->pass_tok == 8) {
         /* LDS-staged expert kernel: K % 512 == 0. Items are 4 waves x MT tiles of 16 rows;
          * when there are too few of them to fill the chip (decode at batch 1-4), halve the
-         * tiles per wave so that twice as many workgroups stream weights. */
+         * tiles per wave so that twice as many workgroups stream weights, and (gate/up, 14
+         * chunks of K) keep two chunks of weights in flight per wave. */
         if (a->K % 512) return k3k_fail("mx_moe: K % 512 != 0", hipErrorInvalidValue);
         const bool gu = mode == K3K_MX_GATEUP;
         const long items4 = (long)a->max_passes * ((a->rows + (gu ? 127 : 255)) / (gu ? 128 : 256));
@@ -615,17 +616,17 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
         const int grid = (int)(items < (long)cus * 4 ? (items > 0 ? items : 1) : (long)cus * 4);
         const bool tiled = a->layout == 1;
         const bool ns2 = a->nsplit == 2;
-#define K3_MOE_LAUNCH(MODE, MT)                                                              \
-    return tiled ? (ns2 ? launch_moe<MODE, MT, 2, 8, 4, 2, 1>(a, grid, st)                   \
-                        : launch_moe<MODE, MT, 1, 8, 4, 2, 1>(a, grid, st))                  \
-                 : (ns2 ? launch_moe<MODE, MT, 2, 8, 4, 2, 0>(a, grid, st)                   \
-                        : launch_moe<MODE, MT, 1, 8, 4, 2, 0>(a, grid, st))
+#define K3_MOE_LAUNCH(MODE, MT, D)                                                           \
+    return tiled ? (ns2 ? launch_moe<MODE, MT, 2, 8, 4, 2, 1, D>(a, grid, st)                \
+                        : launch_moe<MODE, MT, 1, 8, 4, 2, 1, D>(a, grid, st))               \
+                 : (ns2 ? launch_moe<MODE, MT, 2, 8, 4, 2, 0, D>(a, grid, st)                \
+                        : launch_moe<MODE, MT, 1, 8, 4, 2, 0, D>(a, grid, st))
         if (gu) {
-            if (small) K3_MOE_LAUNCH(K3K_MX_GATEUP, 2);
-            K3_MOE_LAUNCH(K3K_MX_GATEUP, 4);
+            if (small) K3_MOE_LAUNCH(K3K_MX_GATEUP, 2, 2);
+            K3_MOE_LAUNCH(K3K_MX_GATEUP, 4, 1);
         }
-        if (small) K3_MOE_LAUNCH(K3K_MX_DOWN, 2);
-        K3_MOE_LAUNCH(K3K_MX_DOWN, 4);
+        if (small) K3_MOE_LAUNCH(K3K_MX_DOWN, 2, 1);
+        K3_MOE_LAUNCH(K3K_MX_DOWN, 4, 1);
 #undef K3_MOE_LAUNCH
     }
     if (a->pass_tok != 16 || a->layout != 0)

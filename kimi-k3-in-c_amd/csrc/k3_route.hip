@@ -231,64 +231,91 @@ __global__ __launch_bounds__(256) void router_partial_kernel(double *part, float
         }
 }
 
-/* The same partials for a few tokens (T <= RS_T): one lane per (expert, chunk) runs the
- * chunk's chain for every token; the lane streams its W row segment itself (float4), the
- * tokens' chunk is staged in LDS as fp64 and read as broadcasts. The bound R_k per chain
- * uses the lane's own running sum of |w| over each 32-column sub-block. */
-constexpr int RS_T = 4;
+/* The same partials for a few tokens (T <= RS_T): one lane per (expert, chunk of RS_CH
+ * columns) runs the chunk's chain for every token. The lane issues all of its W row
+ * segment's loads at once (32 x 16 bytes) so that one memory latency covers the chunk;
+ * the tokens' chunk is staged in LDS as fp64 (read as broadcasts) with the per-sub-block
+ * maxima of |x|. The bound R_k per chain uses the lane's own sums of |w| over each
+ * 32-column sub-block. */
+constexpr int RS_T = 4, RS_CH = 128;
 
 template <int NT>
 __global__ __launch_bounds__(256) void router_partial_small_kernel(double *part, float *rbound,
                                                                    const float *x, int T,
                                                                    const float *W, int hidden,
-                                                                   int n_experts, int chunk,
-                                                                   int vec)
+                                                                   int n_experts, int vec)
 {
-    extern __shared__ double xsh[];                  /* [NT][chunk] */
+    __shared__ double xsh[NT][RS_CH];
+    __shared__ double xmx[NT][RS_CH / 32];
     const int ks = blockIdx.y;
     const int e = blockIdx.x * 256 + threadIdx.x;
-    const int kb0 = ks * chunk, kb1 = min(hidden, kb0 + chunk);
-    const int len = kb1 - kb0;
-    for (int i = threadIdx.x; i < NT * chunk; i += 256) {
-        const int t = i / chunk, k = i % chunk;
-        xsh[i] = (t < T && k < len) ? (double)x[(size_t)t * hidden + kb0 + k] : 0.0;
+    const int kb0 = ks * RS_CH, len = min(RS_CH, hidden - kb0);
+    const float *wr = W + (size_t)min(e, n_experts - 1) * hidden + kb0;
+    /* one token: the whole segment in registers, issued before the staging so that the
+     * two latencies overlap; more tokens: one sub-block at a time */
+    constexpr int WQ = NT == 1 ? RS_CH / 4 : 8;
+    float4 wv[WQ];
+    auto fetch = [&](int q0) {
+#pragma unroll
+        for (int q = 0; q < WQ; q++) {
+            const int k = 4 * (q0 + q);
+            if (vec && len == RS_CH) wv[q] = *reinterpret_cast<const float4 *>(wr + k);
+            else
+                wv[q] = make_float4(k < len ? wr[k] : 0.f, k + 1 < len ? wr[k + 1] : 0.f,
+                                    k + 2 < len ? wr[k + 2] : 0.f, k + 3 < len ? wr[k + 3] : 0.f);
+        }
+    };
+    if (NT == 1) fetch(0);
+    /* stage the tokens' chunk; 32 consecutive threads reduce one sub-block's max |x| */
+    for (int i0 = 0; i0 < NT * RS_CH; i0 += 256) {
+        const int i = i0 + threadIdx.x;
+        const int t = i / RS_CH, k = i % RS_CH;
+        double v = 0.0;
+        if (i < NT * RS_CH) {
+            v = (t < T && k < len) ? (double)x[(size_t)t * hidden + kb0 + k] : 0.0;
+            xsh[t][k] = v;
+        }
+        double m = fabs(v);
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) m = fmax(m, __shfl_xor(m, o, 64));
+        if (i < NT * RS_CH && (k & 31) == 0) xmx[t][k >> 5] = m;
     }
     __syncthreads();
     if (e >= n_experts) return;
-    /* sub-block maxima of |x| per token */
-    const float *wr = W + (size_t)e * hidden + kb0;
     double acc[NT], rb[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) { acc[t] = 0.0; rb[t] = 0.0; }
-    for (int s0 = 0; s0 < len; s0 += 32) {
-        const int sl = min(32, len - s0);
-        float wv[32];
-        if (vec && sl == 32) {
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const float4 v = *reinterpret_cast<const float4 *>(wr + s0 + 4 * q);
-                wv[4 * q] = v.x; wv[4 * q + 1] = v.y; wv[4 * q + 2] = v.z; wv[4 * q + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 32; q++) wv[q] = q < sl ? wr[s0 + q] : 0.0f;
-        }
+    auto subblock = [&](int sb, int qb) {
         float wn = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 32; q++) wn += fabsf(wv[q]);
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            double xm = 0.0;
-#pragma unroll
-            for (int q = 0; q < 32; q++) xm = fmax(xm, fabs(xsh[t * chunk + s0 + min(q, sl - 1)]));
-            rb[t] = fma(32.0, fabs(acc[t]) + (double)wn * xm, rb[t]);
+        for (int q = 0; q < 8; q++) {
+            const float4 v = wv[qb + q];
+            wn += fabsf(v.x) + fabsf(v.y) + fabsf(v.z) + fabsf(v.w);
         }
 #pragma unroll
-        for (int q = 0; q < 32; q++) {
-            const double wd = (double)wv[q];
+        for (int t = 0; t < NT; t++)
+            rb[t] = fma(32.0, fabs(acc[t]) + (double)wn * xmx[t][sb], rb[t]);
 #pragma unroll
-            for (int t = 0; t < NT; t++)
-                if (q < sl) acc[t] = fma(wd, xsh[t * chunk + s0 + q], acc[t]);
+        for (int q = 0; q < 8; q++) {
+            const float4 v = wv[qb + q];
+            const int k = sb * 32 + 4 * q;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                acc[t] = fma((double)v.x, xsh[t][k], acc[t]);
+                acc[t] = fma((double)v.y, xsh[t][k + 1], acc[t]);
+                acc[t] = fma((double)v.z, xsh[t][k + 2], acc[t]);
+                acc[t] = fma((double)v.w, xsh[t][k + 3], acc[t]);
+            }
+        }
+    };
+    if (NT == 1) {
+#pragma unroll
+        for (int sb = 0; sb < RS_CH / 32; sb++) subblock(sb, sb * 8);
+    } else {
+#pragma unroll 1
+        for (int sb = 0; sb < RS_CH / 32; sb++) {
+            fetch(sb * 8);
+            subblock(sb, 0);
         }
     }
 #pragma unroll
@@ -340,6 +367,51 @@ __device__ __forceinline__ void round_interval(float f, double &lo, double &hi)
  * renormalise and scale (k3_ops.c:469-475). nrecomp[t] (optional) counts recomputes. */
 constexpr int RF_MAXE = 2048, RF_MAXW = 16, RF_KB = 32;
 
+/* unsigned order of a non-NaN float that matches its numeric order (-0 as +0) */
+__device__ __forceinline__ uint32_t choice_order(float v)
+{
+    const uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o)
+{
+    const uint32_t lo = __shfl_xor((uint32_t)v, o, 64), hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+/* bitonic sort of one key per lane across the wave, descending (lane 0 the largest) */
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane)
+{
+#pragma unroll
+    for (int sz = 2; sz <= 64; sz <<= 1)
+#pragma unroll
+        for (int j = sz >> 1; j > 0; j >>= 1) {
+            const uint64_t o = shfl_xor64(k, j);
+            const bool first = (lane & j) == 0;          /* lower lane of the pair */
+            const bool desc = (lane & sz) == 0;          /* this block sorts descending */
+            const bool take_max = first == desc;
+            k = take_max ? (k > o ? k : o) : (k < o ? k : o);
+        }
+    return k;
+}
+
+/* two descending lists a, b across the wave -> the 64 largest of their union, descending */
+__device__ __forceinline__ uint64_t wave_merge_desc(uint64_t a, uint64_t b, int lane)
+{
+    /* reverse b and keep the pairwise max: a bitonic sequence holding the top 64 */
+    const uint64_t br = ((uint64_t)__shfl((uint32_t)(b >> 32), 63 - lane, 64) << 32) |
+                        (uint64_t)__shfl((uint32_t)b, 63 - lane, 64);
+    uint64_t k = a > br ? a : br;
+#pragma unroll
+    for (int j = 32; j > 0; j >>= 1) {
+        const uint64_t o = shfl_xor64(k, j);
+        const bool first = (lane & j) == 0;
+        k = first ? (k > o ? k : o) : (k < o ? k : o);
+    }
+    return k;
+}
+
 template <int SL>
 __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt, int *nrecomp,
                                                             const double *part,
@@ -350,10 +422,9 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
                                                             int topk, int renorm,
                                                             float routed_scale, ExcTable exc)
 {
-    __shared__ float rbv[2][RF_MAXW];
-    __shared__ int rbi[2][RF_MAXW];
-    __shared__ float selw[64];
-    __shared__ int selid[64];
+    __shared__ uint64_t candk[RF_MAXW][64];
+    __shared__ uint64_t selk[64];
+    __shared__ float csh[RF_MAXE], ssh[RF_MAXE];
     __shared__ int nre_sh;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
     const int nthr = blockDim.x;
@@ -418,47 +489,82 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
     }
     __syncthreads();
     for (int round = 0; round <= n_experts; round++) {
-        float cc[SL];
+        /* Selection keys: (order-preserving bits of the choice, ~expert) as one 64-bit
+         * integer, so that "larger choice, then lower index" is a plain unsigned max; a
+         * choice that is not > -inf (NaN, -inf) is the key 0 and is never selected. */
+        uint64_t key[SL];
+#pragma unroll
+        for (int i = 0; i < SL; i++) {
+            const int e = tid + nthr * i;
+            csh[min(e, RF_MAXE - 1)] = e < n_experts ? c[i] : 0.0f;
+            ssh[min(e, RF_MAXE - 1)] = e < n_experts ? sc[i] : 0.0f;
+            key[i] = (e < n_experts && c[i] > -INFINITY)
+                         ? ((uint64_t)choice_order(c[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e)
+                         : 0ull;
+        }
+        /* 1. each wave sorts its keys (descending, across lanes; SL > 1: lane-local first) */
+        uint64_t kw = key[0];
+#pragma unroll
+        for (int i = 1; i < SL; i++) kw = kw > key[i] ? kw : key[i];
+        /* SL == 2 (past 1024 experts): the second key of each lane joins by a second sort */
+        kw = wave_sort_desc(kw, lane);
+        if (SL == 2) {
+            uint64_t k2 = key[0] < key[1] ? key[0] : key[1];
+            k2 = wave_sort_desc(k2, lane);
+            /* merge two descending lists: lane l keeps the l-th largest of their union */
+            kw = wave_merge_desc(kw, k2, lane);
+        }
+        if (lane < topk) candk[wv][lane] = kw;
+        __syncthreads();
+        /* 2. wave 0 merges the waves' top-k lists */
+        if (wv == 0) {
+            const int ncand = nw * topk;
+            if (ncand <= 64) {
+                uint64_t m = lane < ncand ? candk[lane / topk][lane % topk] : 0ull;
+                m = wave_sort_desc(m, lane);
+                if (lane < topk) selk[lane] = m;
+            } else {
+                /* up to 16 candidates per lane; topk rounds of a wave max */
+                uint64_t mk[RF_MAXW];
+#pragma unroll
+                for (int q = 0; q < RF_MAXW; q++) {
+                    const int ci = lane + 64 * q;
+                    mk[q] = ci < ncand ? candk[ci / topk][ci % topk] : 0ull;
+                }
+                for (int j = 0; j < topk; j++) {
+                    uint64_t b = 0ull;
+#pragma unroll
+                    for (int q = 0; q < RF_MAXW; q++) b = b > mk[q] ? b : mk[q];
+                    const uint64_t mine = b;
+#pragma unroll
+                    for (int o = 1; o < 64; o <<= 1) {
+                        const uint64_t ob = shfl_xor64(b, o);
+                        b = b > ob ? b : ob;
+                    }
+                    if (b != 0ull && mine == b) {
+#pragma unroll
+                        for (int q = 0; q < RF_MAXW; q++)
+                            if (mk[q] == b) mk[q] = 0ull;
+                    }
+                    if (lane == 0) selk[j] = b;
+                }
+            }
+        }
+        __syncthreads();
         bool sel[SL];
 #pragma unroll
-        for (int i = 0; i < SL; i++) { cc[i] = c[i]; sel[i] = false; }
-        float ckth = -INFINITY;
+        for (int i = 0; i < SL; i++) sel[i] = false;
         int nsel = 0;
+        float ckth = -INFINITY;
         for (int j = 0; j < topk; j++) {
-            float bv = -INFINITY;
-            int bi = -1;
-#pragma unroll
-            for (int i = 0; i < SL; i++)
-                if (cc[i] > bv) { bv = cc[i]; bi = tid + nthr * i; }
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const float ov = __shfl_xor(bv, o, 64);
-                const int oi = __shfl_xor(bi, o, 64);
-                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-            }
-            if (lane == 0) { rbv[j & 1][wv] = bv; rbi[j & 1][wv] = bi; }
-            __syncthreads();
-            bv = -INFINITY;
-            bi = -1;
-            for (int w = 0; w < nw; w++) {
-                const float ov = rbv[j & 1][w];
-                const int oi = rbi[j & 1][w];
-                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-            }
-            if (bi >= 0) {
+            const uint64_t kj = selk[j];
+            if (kj != 0ull) {
+                const int id = (int)(0xffffffffu - (uint32_t)kj);
                 nsel++;
-                ckth = bv;
+                ckth = csh[id];
 #pragma unroll
                 for (int i = 0; i < SL; i++)
-                    if (bi == tid + nthr * i) {
-                        cc[i] = -INFINITY;
-                        sel[i] = true;
-                        selw[j] = sc[i];
-                        selid[j] = bi;
-                    }
-            } else if (tid == 0) {
-                selw[j] = 0.0f;
-                selid[j] = 0;
+                    if (id == tid + nthr * i) sel[i] = true;
             }
         }
         /* uncertified logits that matter: selected, or able to reach the selection */
@@ -485,7 +591,9 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
     }
     __syncthreads();
     if (wv == 0) {
-        float w = lane < topk ? selw[lane] : 0.0f;
+        const uint64_t kj = lane < topk ? selk[lane] : 0ull;
+        const int id = kj != 0ull ? (int)(0xffffffffu - (uint32_t)kj) : -1;
+        float w = id >= 0 ? ssh[id] : 0.0f;
         if (renorm && topk > 1) {
             double s = 0.0;
             for (int j = 0; j < topk; j++) s += (double)__shfl(w, j, 64);   /* j ascending */
@@ -493,7 +601,7 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
             w = w * inv;
         }
         if (lane < topk) {
-            idx[(size_t)t * topk + lane] = selid[lane];
+            idx[(size_t)t * topk + lane] = id >= 0 ? id : 0;
             wt[(size_t)t * topk + lane] = w * routed_scale;
         }
         if (nrecomp && lane == 0) nrecomp[t] = nre_sh;
@@ -501,10 +609,36 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
 }
 
 /* ---- expert-major gather -----------------------------------------------------------
- * One workgroup of 1024 threads. Counting sort by expert, stable in assignment order:
- * chunks of 1024 assignments are placed in order; inside a chunk each wave ranks its
- * lanes among equal experts with ballots, and waves commit one after another. */
-constexpr int G_MAXE = 4096;
+ * One workgroup of 1024 threads. Counting sort by expert, stable in assignment order.
+ * Counts by LDS atomics; the scans of (count, jobs, passes) over experts by wave shuffles
+ * plus one pass over the 16 wave totals. Placement in chunks of 1024 assignments: each
+ * wave ranks its lanes among equal experts with ballots; up to 1024 experts, per-wave
+ * expert counts (16-bit, in LDS) give every lane the count of its expert in earlier
+ * waves, so a chunk costs three barriers; past 1024 experts the waves commit one after
+ * another. */
+constexpr int G_MAXE = 4096, G_WCNT_E = 1024;
+
+/* inclusive scan over a wave, then over the workgroup's 16 wave totals */
+__device__ __forceinline__ int block_scan_excl(int v, int *wtot, int lane, int wv, int &total)
+{
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) wtot[wv] = x;
+    __syncthreads();
+    int base = 0;
+    total = 0;
+    for (int w = 0; w < 16; w++) {
+        const int tw = wtot[w];
+        if (w < wv) base += tw;
+        total += tw;
+    }
+    __syncthreads();
+    return base + x - v;
+}
 
 __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, int *job_expert,
                                                       int *job_off, int *job_cnt, int *pass_job,
@@ -514,7 +648,8 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
 {
     __shared__ int cnt[G_MAXE];
     __shared__ int fill[G_MAXE];
-    __shared__ int wsum[32];
+    __shared__ int wtot[16];
+    __shared__ unsigned short wcnt[16][G_WCNT_E];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     for (int e = tid; e < n_experts; e += 1024) cnt[e] = 0;
     __syncthreads();
@@ -524,7 +659,7 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
     }
     __syncthreads();
 
-    /* Exclusive scan of counts -> offsets; per-thread serial over a contiguous range. */
+    /* per-thread sums over a contiguous expert range, then workgroup scans */
     const int per = (n_experts + 1023) / 1024;
     const int ea = tid * per, eb = min(n_experts, ea + per);
     int local = 0, ljobs = 0, lpass = 0, ldrop = 0;
@@ -539,23 +674,11 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
             }
         }
     }
-    /* block scans of (local, ljobs, lpass) via shared memory, 3 passes */
-    __shared__ int sc_a[1024], sc_b[1024], sc_c[1024];
-    sc_a[tid] = local;
-    sc_b[tid] = ljobs;
-    sc_c[tid] = lpass;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-        const int va = tid >= o ? sc_a[tid - o] : 0;
-        const int vb = tid >= o ? sc_b[tid - o] : 0;
-        const int vc = tid >= o ? sc_c[tid - o] : 0;
-        __syncthreads();
-        sc_a[tid] += va;
-        sc_b[tid] += vb;
-        sc_c[tid] += vc;
-        __syncthreads();
-    }
-    int run = sc_a[tid] - local, jrun = sc_b[tid] - ljobs, prun = sc_c[tid] - lpass;
+    int tot_a, tot_b, tot_c, tot_d;
+    int run = block_scan_excl(local, wtot, lane, wv, tot_a);
+    int jrun = block_scan_excl(ljobs, wtot, lane, wv, tot_b);
+    int prun = block_scan_excl(lpass, wtot, lane, wv, tot_c);
+    (void)block_scan_excl(ldrop, wtot, lane, wv, tot_d);
     for (int e = ea; e < eb; e++) {
         offsets[e] = run;
         fill[e] = run;
@@ -573,24 +696,16 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
         }
         run += cnt[e];
     }
-    if (tid == 1023) {
-        offsets[n_experts] = sc_a[1023];
-        counts[0] = sc_b[1023];
-        counts[1] = sc_c[1023];
-    }
-    /* dropped assignment total */
-    if (lane == 0) wsum[wv] = 0;
-    __syncthreads();
-    atomicAdd(&wsum[wv], ldrop);
-    __syncthreads();
     if (tid == 0) {
-        int d = 0;
-        for (int w = 0; w < 16; w++) d += wsum[w];
-        counts[2] = d;
+        offsets[n_experts] = tot_a;
+        counts[0] = tot_b;
+        counts[1] = tot_c;
+        counts[2] = tot_d;
     }
     __syncthreads();
 
-    /* Stable placement. */
+    /* stable placement */
+    const bool wide = n_experts > G_WCNT_E;
     for (int c0 = 0; c0 < N; c0 += 1024) {
         const int a = c0 + tid;
         const int e = a < N ? idx[a] : -1;
@@ -609,37 +724,89 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
             }
             pending &= ~m;
         }
-        for (int w = 0; w < 16; w++) {
-            if (wv == w && ok) {
-                perm[fill[e] + rank] = a;
+        const int m = __popcll(mine);
+        if (!wide) {
+            for (int i = tid; i < 16 * n_experts; i += 1024) wcnt[i / n_experts][i % n_experts] = 0;
+            __syncthreads();
+            if (ok && rank == 0) wcnt[wv][e] = (unsigned short)m;
+            __syncthreads();
+            if (ok) {
+                int base = fill[e];
+                for (int w = 0; w < wv; w++) base += wcnt[w][e];
+                perm[base + rank] = a;
             }
             __syncthreads();
-            if (wv == w && ok && rank == __popcll(mine) - 1) fill[e] += __popcll(mine);
+            for (int x = tid; x < n_experts; x += 1024) {
+                int add = 0;
+                for (int w = 0; w < 16; w++) add += wcnt[w][x];
+                fill[x] += add;
+            }
             __syncthreads();
+        } else {
+            for (int w = 0; w < 16; w++) {
+                if (wv == w && ok) perm[fill[e] + rank] = a;
+                __syncthreads();
+                if (wv == w && ok && rank == m - 1) fill[e] += m;
+                __syncthreads();
+            }
         }
     }
 }
 
-/* ---- combine: out[t] = 0 + sum_j wt[t][j] * contrib[t*topk + j], j ascending ------- */
-__global__ void combine_kernel(float *out, const float *contrib, const float *wt, const int *idx,
-                               const void *bank, int n_experts, int T, int topk, int E)
+/* ---- combine: out[t] = 0 + sum_j wt[t][j] * contrib[t*topk + j], j ascending -------
+ * A slot contributes nothing when its expert index is out of range or its bank entry is
+ * absent. Every slot's row is loaded (it is valid memory either way) and the sum selects,
+ * so that all topk loads are in flight together. */
+__global__ __launch_bounds__(256) void combine_kernel(float *out, const float *contrib,
+                                                     const float *wt, const int *idx,
+                                                     const void *bank, int n_experts, int T,
+                                                     int topk, int E, int vec)
 {
+    __shared__ float wsl[K3_MAX_TOPK_DEV];
+    __shared__ int vsl[K3_MAX_TOPK_DEV];
     const int t = blockIdx.y;
-    const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
-    if (t >= T || i >= E) return;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = 0; j < topk; j++) {
-        const int a = t * topk + j;
+    if (threadIdx.x < topk) {
+        const int a = t * topk + threadIdx.x;
         const int e = idx[a];
-        if (e < 0 || e >= n_experts) continue;          /* filtered: contributes nothing */
-        if (bank && !expert_present(bank, e)) continue; /* dropped: contributes nothing */
-        const float w = wt[a];
-        const float *c = contrib + (size_t)a * E + i;
-        for (int q = 0; q < 4; q++)
-            if (i + q < E) acc[q] = __fadd_rn(acc[q], __fmul_rn(w, c[q]));
+        const bool ok = e >= 0 && e < n_experts && (!bank || expert_present(bank, e));
+        vsl[threadIdx.x] = ok;
+        wsl[threadIdx.x] = wt[a];
     }
-    for (int q = 0; q < 4; q++)
-        if (i + q < E) out[(size_t)t * E + i + q] = acc[q];
+    __syncthreads();
+    const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= E) return;
+    const float *c0 = contrib + (size_t)t * topk * E + i;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int JB = 8;
+    for (int j0 = 0; j0 < topk; j0 += JB) {
+        float cv[JB][4];
+#pragma unroll
+        for (int jj = 0; jj < JB; jj++) {
+            const int j = min(j0 + jj, topk - 1);
+            const float *c = c0 + (size_t)j * E;
+            if (vec) {
+                const float4 v = *reinterpret_cast<const float4 *>(c);
+                cv[jj][0] = v.x; cv[jj][1] = v.y; cv[jj][2] = v.z; cv[jj][3] = v.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) cv[jj][q] = i + q < E ? c[q] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < JB; jj++) {
+            const int j = j0 + jj;
+            if (j < topk && vsl[j]) {
+                const float w = wsl[j];
+#pragma unroll
+                for (int q = 0; q < 4; q++) acc[q] = __fadd_rn(acc[q], __fmul_rn(w, cv[jj][q]));
+            }
+        }
+    }
+    float *o = out + (size_t)t * E + i;
+    if (vec) *reinterpret_cast<float4 *>(o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    else
+        for (int q = 0; q < 4; q++)
+            if (i + q < E) o[q] = acc[q];
 }
 
 /* ---- elementwise --------------------------------------------------------------------- */
@@ -709,12 +876,7 @@ extern "C" int k3k_split_bf16(uint16_t *hi, uint16_t *lo, const float *x, size_t
 
 extern "C" int k3k_router_chunk(int T, int hidden, int n_experts)
 {
-    if (T <= RS_T) {
-        /* one lane per (expert, chunk): 256-column chunks, at most 32 of them */
-        int chunk = 256;
-        while ((hidden + chunk - 1) / chunk > RF_KB) chunk += 256;
-        return chunk;
-    }
+    if (T <= RS_T) return RS_CH;          /* one lane per (expert, 128-column chunk) */
     /* enough workgroups to fill the chip, chunks a multiple of 32 columns */
     const long tiles = (long)((n_experts + RP_E - 1) / RP_E) * ((T + RP_T - 1) / RP_T);
     long ks = (2L * k3k_cu_count() + tiles - 1) / tiles;
@@ -736,14 +898,14 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
     const int vec = (hidden % 4 == 0) && ((((uintptr_t)x) | ((uintptr_t)W)) % 16 == 0);
     hipStream_t st = (hipStream_t)stream;
     if (T <= RS_T) {
+        if (chunk != RS_CH) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
         dim3 grid((n_experts + 255) / 256, ks);
-        const size_t lds = (size_t)RS_T * chunk * sizeof(double);
         if (T == 1)
-            hipLaunchKernelGGL(router_partial_small_kernel<1>, grid, dim3(256), (size_t)chunk * 8, st,
-                               part, rbound, x, T, W, hidden, n_experts, chunk, vec);
+            hipLaunchKernelGGL(router_partial_small_kernel<1>, grid, dim3(256), 0, st, part, rbound,
+                               x, T, W, hidden, n_experts, vec);
         else
-            hipLaunchKernelGGL(router_partial_small_kernel<RS_T>, grid, dim3(256), lds, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec);
+            hipLaunchKernelGGL(router_partial_small_kernel<RS_T>, grid, dim3(256), 0, st, part,
+                               rbound, x, T, W, hidden, n_experts, vec);
     } else {
         dim3 grid((n_experts + RP_E - 1) / RP_E, (T + RP_T - 1) / RP_T, ks);
         hipLaunchKernelGGL(router_partial_kernel, grid, dim3(256), 0, st, part, rbound, x, T, W,
@@ -806,9 +968,11 @@ extern "C" int k3k_combine(float *out, const float *contrib, const float *wt, co
                            const void *bank, int n_experts, int T, int topk, int E, void *stream)
 {
     if (T <= 0) return 0;
-    dim3 grid((E / 4 + 255) / 256 + 1, T);
+    if (topk > K3_MAX_TOPK_DEV) return k3k_fail("combine: topk too large", hipErrorInvalidValue);
+    const int vec = (E % 4 == 0) && ((((uintptr_t)out) | ((uintptr_t)contrib)) % 16 == 0);
+    dim3 grid(((E + 3) / 4 + 255) / 256, T);
     hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, (hipStream_t)stream, out, contrib, wt,
-                       idx, bank, n_experts, T, topk, E);
+                       idx, bank, n_experts, T, topk, E, vec);
     K3K_LAUNCH_CHECK("combine launch");
     return 0;
 }
