@@ -116,6 +116,41 @@ def time_layer(layer, T, steps, warmup, nbatch=4):
     return (t1 - t0), stages, u_mean, uniq
 
 
+def time_prefill(layer, T=4096, steps=3, warmup=1):
+    """Prefill layer (config 3): T tokens, bf16 activations, 32-token expert passes on the
+    matrix cores. Eager calls; the stage profile comes from the timed calls themselves."""
+    L = k3amd.lib()
+    x = k3amd.DevBuf(T * E * 4).upload(wl.tokens(T, tag="bench.prefill"))
+    out = k3amd.DevBuf(T * E * 4)
+    idx = k3amd.DevBuf(T * K * 4)
+    wt = k3amd.DevBuf(T * K * 4)
+    ws = k3amd.DevBuf(L.k3d_moe_ws(T, E, I, N, K, 1))
+    for _ in range(warmup):
+        layer.run(x, out, idx, wt, T, ws, prec=1)
+    k3amd.check(L.k3d_sync(None))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        layer.run(x, out, idx, wt, T, ws, prec=1)
+    k3amd.check(L.k3d_sync(None))
+    t1 = time.perf_counter()
+    prof = k3amd.Profile(max_marks=64)
+    layer.run(x, out, idx, wt, T, ws, prec=1)
+    k3amd.check(L.k3d_sync(None))
+    st = prof.end()
+    h = idx.download(np.empty((T, K), np.int32))
+    for b in (x, out, idx, wt, ws):
+        b.free()
+    ms = (t1 - t0) / steps * 1e3
+    flops = T * K * 3 * 2 * E * I                  # 2.886 TFLOP at T=4096
+    expert_ms = sum(st.get(k, (0.0, 0))[0] for k in ("gateup", "down"))
+    return {"tokens": T, "ms_per_step": round(ms, 3), "tokens_per_s": round(T / ms * 1e3, 1),
+            "expert_flops": flops, "expert_ms": round(expert_ms, 3),
+            "expert_TFLOPs": round(flops / (expert_ms * 1e-3) / 1e12, 1) if expert_ms else None,
+            "mfma_frac_of_bf16_peak": round(flops / (expert_ms * 1e-3) / 2.5e15, 4) if expert_ms else None,
+            "unique_experts": int(len(np.unique(h))),
+            "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st.items()}}
+
+
 def time_gemv(steps=200, copies=128):
     """2048x7168 MXFP4 GEMV, one token, rotating over `copies` distinct weight copies
     (>= 1 GB, well past the last-level cache) so every launch streams from HBM."""
@@ -246,6 +281,8 @@ def main():
     log(f"bench: batch-1 layer {b1_ms:.3f} ms/step")
     gemv = time_gemv()
     log(f"bench: gemv {gemv}")
+    prefill = time_prefill(layer)
+    log(f"bench: prefill {prefill}")
 
     line = {
         "metric": "MoE-layer tokens/s + achieved HBM GB/s (MXFP4 expert GEMV), batch 1 & 64",
@@ -276,6 +313,7 @@ def main():
                    "layer_GBps": round(b1_bytes / (b1_ms * 1e-3) / 1e9, 1),
                    "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st1.items()}},
         "gemv_2048x7168": gemv,
+        "prefill_4096": prefill,
     }
     if not args.no_cpu:
         cb = cpu_baseline()

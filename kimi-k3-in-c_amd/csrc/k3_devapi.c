@@ -280,11 +280,15 @@ typedef struct {
     int max_passes;
 } MoeWs;
 
-/* Tokens per expert pass: the LDS-staged expert kernel (8) needs both matrix widths to be
- * multiples of 512; other shapes run the register-fed kernel (16, row-major bank only). */
-static int moe_pass_tok(int hidden, int inter)
+/* Tokens per expert pass. The LDS-staged expert kernels need both matrix widths to be
+ * multiples of 512: passes of 8 tokens, or of 32 (two MFMA column blocks) when the
+ * activations are single bf16 terms and the batch averages at least 8 tokens per expert
+ * (prefill). Other shapes run the register-fed kernel (16, row-major bank only). */
+static int moe_pass_tok(int T, int hidden, int inter, int n_experts, int topk, int prec)
 {
-    return (hidden % 512 == 0 && inter % 512 == 0) ? 8 : 16;
+    if (hidden % 512 || inter % 512) return 16;
+    if (prec == 1 && (long)T * topk >= 8L * n_experts) return 32;
+    return 8;
 }
 
 static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n_experts, int topk,
@@ -292,7 +296,7 @@ static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n
 {
     const size_t N = (size_t)T * topk;
     const int maxjobs = (int)(N < (size_t)n_experts ? N : (size_t)n_experts);
-    w->max_passes = maxjobs + (int)(N / (size_t)moe_pass_tok(hidden, inter)) + 1;
+    w->max_passes = maxjobs + (int)(N / (size_t)moe_pass_tok(T, hidden, inter, n_experts, topk, prec)) + 1;
     w->xhi = (uint16_t *)take(c, (size_t)T * hidden * 2);
     w->xlo = prec == 0 ? (uint16_t *)take(c, (size_t)T * hidden * 2) : NULL;
     w->ahi = (uint16_t *)take(c, N * inter * 2);
@@ -338,7 +342,7 @@ static int moe_check(const char *fn, int hidden, int inter, int n_experts, int t
         snprintf(msg, sizeof msg, "%s: unknown bank layout %d", fn, layout);
         return bad(msg);
     }
-    if (layout == K3D_LAYOUT_TILED && moe_pass_tok(hidden, inter) != 8) {
+    if (layout == K3D_LAYOUT_TILED && (hidden % 512 || inter % 512)) {
         snprintf(msg, sizeof msg, "%s: a tiled bank needs hidden and inter multiples of 512", fn);
         return bad(msg);
     }
@@ -352,7 +356,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
 {
     int *perm = perm_out ? perm_out : w->perm;
     int *offsets = offsets_out ? offsets_out : w->offsets;
-    const int pass_tok = moe_pass_tok(hidden, inter);
+    const int pass_tok = moe_pass_tok(T, hidden, inter, n_experts, topk, prec);
     if (k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
     if (k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
                    w->counts, idx, T, topk, n_experts, bank, pass_tok, stream))

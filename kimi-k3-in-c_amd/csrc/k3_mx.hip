@@ -270,10 +270,11 @@ int launch_mx(const K3kMxArgs *a, int kw, int grid, hipStream_t st)
  * c+1 are in flight (activations issued first, so waiting for them leaves the weight
  * loads outstanding).
  */
-template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT, int DEPTH>
+template <int MODE, int MT, int NS, int PT, int NB, int NW, int WPE, int LAYOUT, int DEPTH>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
 void mx_moe_kernel(K3kMxArgs a)
 {
+    static_assert(PT <= 16 * NB, "a pass fits the MFMA column blocks");
     constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
     constexpr int KC = 512, SPC = 4, LDT = KC + 8;           /* LDS row: 16-byte pad */
     constexpr int NRH = PT * NS;                             /* staged row-halves per chunk */
@@ -346,11 +347,16 @@ void mx_moe_kernel(K3kMxArgs a)
                 gsrc[i] = ((uint32_t)xr * (uint32_t)K + (uint32_t)lane * 8u) * 2u;
             }
         }
-        const int brow = r16 < ntok ? r16 : PT;
-
-        k3_f32x4 acc[MT];
+        /* B operand rows: token column nb*16 + r16 of the pass, or the zero row */
+        int brow[NB];
 #pragma unroll
-        for (int m = 0; m < MT; m++) acc[m] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nb = 0; nb < NB; nb++) brow[nb] = nb * 16 + r16 < ntok ? nb * 16 + r16 : PT;
+
+        k3_f32x4 acc[MT][NB];
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) acc[m][nb] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
 
         /* Weights in registers, DEPTH chunks ahead: qa[slot][d] holds step d of a chunk.
          * DEPTH 1: step d of chunk c+1 is loaded into qa[0][d] right after step d of chunk
@@ -421,14 +427,17 @@ void mx_moe_kernel(K3kMxArgs a)
             if (more2) load_scales(c + DEPTH, DEPTH == 2 ? sqnn : sqn);
 #pragma unroll
             for (int d = 0; d < SPC; d++) {
-                /* B operand: token column r16 (or the zero row), block 4d+g of the chunk */
-                uint4 bh[4], bl[4];
-                const uint4 *bp = reinterpret_cast<const uint4 *>(&bsh[buf][0][brow][(4 * d + g) * 32]);
-                const uint4 *bq = reinterpret_cast<const uint4 *>(&bsh[buf][NS - 1][brow][(4 * d + g) * 32]);
+                /* B operand: token columns (or the zero row), block 4d+g of the chunk */
+                uint4 bh[NB][4], bl[NB][4];
 #pragma unroll
-                for (int pp = 0; pp < 4; pp++) {
-                    bh[pp] = bp[pp];
-                    if (NS == 2) bl[pp] = bq[pp];
+                for (int nb = 0; nb < NB; nb++) {
+                    const uint4 *bp = reinterpret_cast<const uint4 *>(&bsh[buf][0][brow[nb]][(4 * d + g) * 32]);
+                    const uint4 *bq = reinterpret_cast<const uint4 *>(&bsh[buf][NS - 1][brow[nb]][(4 * d + g) * 32]);
+#pragma unroll
+                    for (int pp = 0; pp < 4; pp++) {
+                        bh[nb][pp] = bp[pp];
+                        if (NS == 2) bl[nb][pp] = bq[pp];
+                    }
                 }
                 uint4 qq[MT];
                 float so[MT];
@@ -450,9 +459,12 @@ void mx_moe_kernel(K3kMxArgs a)
                     for (int pp = 0; pp < 4; pp++) {
                         const uint32_t codes = pp == 0 ? qq[m].x : pp == 1 ? qq[m].y : pp == 2 ? qq[m].z : qq[m].w;
                         const k3_bf16x8 av = k3_dequant8_bf16(codes, so[m]);
-                        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh[pp]), acc[m], 0, 0, 0);
-                        if (NS == 2)
-                            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl[pp]), acc[m], 0, 0, 0);
+#pragma unroll
+                        for (int nb = 0; nb < NB; nb++) {
+                            acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh[nb][pp]), acc[m][nb], 0, 0, 0);
+                            if (NS == 2)
+                                acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl[nb][pp]), acc[m][nb], 0, 0, 0);
+                        }
                     }
                 if (more2) load_step(c + DEPTH, d, slot);
             }
@@ -469,15 +481,18 @@ void mx_moe_kernel(K3kMxArgs a)
             if (NSLOT == 2 && c + 1 < nchunk) chunk(c + 1, I1{});
         }
 
-        /* epilogue: lane holds token column r16, rows 4g..4g+3 of each tile */
-        if (r16 < ntok) {
-            const int orow = a.perm[off + tok0 + r16];
+        /* epilogue: lane holds token column nb*16 + r16, rows 4g..4g+3 of each tile */
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            const int tk = nb * 16 + r16;
+            if (tk >= ntok) continue;
+            const int orow = a.perm[off + tok0 + tk];
             for (int m = 0; m < RT; m++) {
                 const int base = rb * rpg + wv * rpw + 16 * m + 4 * g;
                 if (MODE == K3K_MX_GATEUP) {
                     uint16_t hi[4], lo[4];
                     for (int jj = 0; jj < 4; jj++) {
-                        const float v = k3_act_pair(acc[m][jj], acc[m + RT][jj], a.act, a.b1, a.b2);
+                        const float v = k3_act_pair(acc[m][nb][jj], acc[m + RT][nb][jj], a.act, a.b1, a.b2);
                         k3_split2(v, hi[jj], lo[jj]);
                     }
                     uint16_t *oh = a.ahi + (size_t)orow * rows;
@@ -491,10 +506,10 @@ void mx_moe_kernel(K3kMxArgs a)
                     float *o = a.out + (size_t)orow * rows;
                     if (base + 3 < rows && (rows & 3) == 0) {
                         *reinterpret_cast<float4 *>(o + base) =
-                            make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+                            make_float4(acc[m][nb][0], acc[m][nb][1], acc[m][nb][2], acc[m][nb][3]);
                     } else {
                         for (int jj = 0; jj < 4; jj++)
-                            if (base + jj < rows) o[base + jj] = acc[m][jj];
+                            if (base + jj < rows) o[base + jj] = acc[m][nb][jj];
                     }
                 }
             }
@@ -502,10 +517,10 @@ void mx_moe_kernel(K3kMxArgs a)
     }
 }
 
-template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT, int DEPTH = 1>
+template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT, int DEPTH = 1, int NB = 1>
 int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((mx_moe_kernel<MODE, MT, NS, PT, NW, WPE, LAYOUT, DEPTH>), dim3(grid), dim3(64 * NW),
+    hipLaunchKernelGGL((mx_moe_kernel<MODE, MT, NS, PT, NB, NW, WPE, LAYOUT, DEPTH>), dim3(grid), dim3(64 * NW),
                        0, st, *a);
     K3K_LAUNCH_CHECK("mx_moe launch");
     return 0;
@@ -601,6 +616,23 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
         const int grid = items < cus * 8 ? items : cus * 8;
         if (a->nsplit == 2) return launch_mx<K3K_MX_PLAIN, 1, 1, 2, 2, 16>(a, kw, grid, st);
         return launch_mx<K3K_MX_PLAIN, 1, 1, 1, 2, 16>(a, kw, grid, st);
+    }
+    if (a->pass_tok == 32) {
+        /* prefill: 32-token passes, two MFMA column blocks per weight fragment, activations
+         * as one bf16 term (the bf16-MFMA prefill precision) */
+        if (a->K % 512 || a->nsplit != 1)
+            return k3k_fail("mx_moe: 32-token passes need K % 512 == 0 and bf16 activations",
+                            hipErrorInvalidValue);
+        const bool gu = mode == K3K_MX_GATEUP;
+        const int rpg = gu ? 128 : 256;
+        const long items = (long)a->max_passes * ((a->rows + rpg - 1) / rpg);
+        const int grid = (int)(items < (long)cus * 4 ? (items > 0 ? items : 1) : (long)cus * 4);
+        const bool tiled = a->layout == 1;
+        if (gu)
+            return tiled ? launch_moe<K3K_MX_GATEUP, 4, 1, 32, 4, 2, 1, 1, 2>(a, grid, st)
+                         : launch_moe<K3K_MX_GATEUP, 4, 1, 32, 4, 2, 0, 1, 2>(a, grid, st);
+        return tiled ? launch_moe<K3K_MX_DOWN, 4, 1, 32, 4, 2, 1, 1, 2>(a, grid, st)
+                     : launch_moe<K3K_MX_DOWN, 4, 1, 32, 4, 2, 0, 1, 2>(a, grid, st);
     }
     if (a->pass_tok == 8) {
         /* LDS-staged expert kernel: K % 512 == 0. Items are 4 waves x MT tiles of 16 rows;

@@ -63,7 +63,8 @@ typedef struct {
     float *y;                           /* [ntok][ldy] */
     int ntok, ldy;
     /* GATEUP / DOWN: jobs from the gather. A pass is up to pass_tok tokens of one job:
-     * 16 (any K % 32 == 0, row-major bank) or 8 (K % 512 == 0, either bank layout). */
+     * 16 (any K % 32 == 0, row-major bank), 8 (K % 512 == 0, either bank layout) or 32
+     * (K % 512 == 0, bf16 activations: the prefill kernel). */
     const void *bank;                   /* device K3ExpertQ[n_experts] */
     int pass_tok;
     int layout;                         /* 0: row-major bank, 1: tiled (k3k_mx_tile) */
