@@ -63,9 +63,9 @@ class Layer:
         self.bank = k3amd.DevBank(Lazy(), E, I, layout)
         self.router = k3amd.DevBuf(ROUTER_BYTES).upload(wl.router_weights())
 
-    def run(self, x, out, idx, wt, T, ws, prec=0, stream=None):
+    def run(self, x, out, idx, wt, T, ws, prec=0, stream=None, bias=None):
         k3amd.check(k3amd.lib().k3d_moe_routed(
-            out.ptr, idx.ptr, wt.ptr, x.ptr, T, self.router.ptr, None, self.bank.table.ptr,
+            out.ptr, idx.ptr, wt.ptr, x.ptr, T, self.router.ptr, bias, self.bank.table.ptr,
             self.layout, E, I, N, K, 1, 1.0, k3amd.K3_ACT_SILU, 4.0, 25.0, prec, ws.ptr, ws.nbytes,
             None, None, None, stream), "k3d_moe_routed")
 
@@ -148,6 +148,58 @@ def time_prefill(layer, T=4096, steps=3, warmup=1):
             "expert_TFLOPs": round(flops / (expert_ms * 1e-3) / 1e12, 1) if expert_ms else None,
             "mfma_frac_of_bf16_peak": round(flops / (expert_ms * 1e-3) / 2.5e15, 4) if expert_ms else None,
             "unique_experts": int(len(np.unique(h))),
+            "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st.items()}}
+
+
+def time_skewed(layer, T=512, steps=5, warmup=1):
+    """Skewed routing + dense trunk (config 4): T tokens, router selection bias giving
+    Zipf(1.2)-like expert popularity, routed experts with bf16 activations, then the
+    always-on bf16 shared expert (7168 -> 2048 -> 7168) accumulated onto the output."""
+    L = k3amd.lib()
+    x = k3amd.DevBuf(T * E * 4).upload(wl.tokens(T, tag="bench.skewed"))
+    bias = k3amd.DevBuf(N * 4).upload(wl.zipf_bias())
+    w1, w3, w2 = wl.shared_expert_weights()
+    d1, d3, d2 = (k3amd.DevBuf(w.nbytes).upload(w) for w in (w1, w3, w2))
+    out = k3amd.DevBuf(T * E * 4)
+    idx = k3amd.DevBuf(T * K * 4)
+    wt = k3amd.DevBuf(T * K * 4)
+    ws = k3amd.DevBuf(L.k3d_moe_ws(T, E, I, N, K, 1))
+    sws_b = L.k3d_shared_ws(T, E, I, 1)
+    sws = k3amd.DevBuf(sws_b)
+
+    def step():
+        layer.run(x, out, idx, wt, T, ws, prec=1, bias=bias.ptr)
+        k3amd.check(L.k3d_shared_expert(out.ptr, 1, x.ptr, T, d1.ptr, d3.ptr, d2.ptr, E, I,
+                                        k3amd.K3_ACT_SILU, 4.0, 25.0, 1, sws.ptr, sws_b, None),
+                    "k3d_shared_expert")
+    for _ in range(warmup):
+        step()
+    k3amd.check(L.k3d_sync(None))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    k3amd.check(L.k3d_sync(None))
+    t1 = time.perf_counter()
+    prof = k3amd.Profile(max_marks=64)
+    step()
+    k3amd.check(L.k3d_sync(None))
+    st = prof.end()
+    h = idx.download(np.empty((T, K), np.int32))
+    for b in (x, bias, d1, d3, d2, out, idx, wt, ws, sws):
+        b.free()
+    cnt = np.sort(np.bincount(h.ravel(), minlength=N))[::-1]
+    ms = (t1 - t0) / steps * 1e3
+    sh_ms = st.get("shared", (0.0, 1))[0]
+    sh_flops = T * 3 * 2 * E * I
+    return {"tokens": T, "ms_per_step": round(ms, 3), "tokens_per_s": round(T / ms * 1e3, 1),
+            "routing": {"unique_experts": int((cnt > 0).sum()), "max_tokens_per_expert": int(cnt[0]),
+                        "mean_tokens_per_used_expert": round(float(cnt[cnt > 0].mean()), 2),
+                        "share_top1": round(float(cnt[0] / cnt.sum()), 4),
+                        "share_top3": round(float(cnt[:3].sum() / cnt.sum()), 4),
+                        "share_top8": round(float(cnt[:8].sum() / cnt.sum()), 4),
+                        "histogram_top16": [int(v) for v in cnt[:16]]},
+            "shared_expert_ms": round(sh_ms, 4),
+            "shared_expert_TFLOPs": round(sh_flops / (sh_ms * 1e-3) / 1e12, 1) if sh_ms else None,
             "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st.items()}}
 
 
@@ -283,6 +335,8 @@ def main():
     log(f"bench: gemv {gemv}")
     prefill = time_prefill(layer)
     log(f"bench: prefill {prefill}")
+    skewed = time_skewed(layer)
+    log(f"bench: skewed {skewed}")
 
     line = {
         "metric": "MoE-layer tokens/s + achieved HBM GB/s (MXFP4 expert GEMV), batch 1 & 64",
@@ -314,6 +368,7 @@ def main():
                    "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st1.items()}},
         "gemv_2048x7168": gemv,
         "prefill_4096": prefill,
+        "skewed_512_shared": skewed,
     }
     if not args.no_cpu:
         cb = cpu_baseline()

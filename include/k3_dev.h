@@ -47,7 +47,8 @@ int k3d_graph_destroy(void *exec);
  * entry points record an event at each stage boundary; k3d_prof_end synchronises and
  * returns, per stage, the summed milliseconds and the number of samples. Stage ids: */
 enum { K3D_STAGE_BEGIN = 0, K3D_STAGE_ROUTER = 1, K3D_STAGE_GATHER = 2, K3D_STAGE_GATEUP = 3,
-       K3D_STAGE_DOWN = 4, K3D_STAGE_COMBINE = 5, K3D_STAGE_GEMV = 6, K3D_STAGE_COUNT = 7 };
+       K3D_STAGE_DOWN = 4, K3D_STAGE_COMBINE = 5, K3D_STAGE_GEMV = 6, K3D_STAGE_SHARED = 7,
+       K3D_STAGE_COUNT = 8 };
 int k3d_prof_begin(int max_marks);
 int k3d_prof_mark(void *stream, int stage);
 int k3d_prof_end(double *ms, int *count, int n_stages);
@@ -103,6 +104,18 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T,
                    int hidden, int inter, int n_experts, int topk, int renorm, float routed_scale,
                    int act, float b1, float b2, int prec, void *ws, size_t ws_bytes,
                    int *perm_out, int *offsets_out, int *drops_out, void *stream);
+
+/* The always-on dense shared expert with bf16 weights, on the matrix cores:
+ *   s[t] = W2 . act(W1 x[t], W3 x[t]),  W1, W3 [inter][hidden], W2 [hidden][inter] bf16,
+ * y = s (accumulate 0) or y += s (accumulate 1, after the routed sum: the order of the
+ * reference's shared tail, k3_ops.c:650-654). The reference computes each product with
+ * k3_matmul_bf16 (fp64 accumulation); here fp32 MFMA accumulation with the activations as
+ * two bf16 terms (prec 0, max|err| <= 1e-4 ||ref||inf) or one (prec 1, 2e-2 relative).
+ * hidden and inter must be multiples of 512. */
+size_t k3d_shared_ws(int T, int hidden, int inter, int prec);
+int k3d_shared_expert(float *y, int accumulate, const float *x, int T, const uint16_t *w1,
+                      const uint16_t *w3, const uint16_t *w2, int hidden, int inter, int act,
+                      float b1, float b2, int prec, void *ws, size_t ws_bytes, void *stream);
 
 /* The expert half of the layer for a routing already in idx/wt (device). */
 int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x, int T,

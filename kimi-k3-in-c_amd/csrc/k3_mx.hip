@@ -307,15 +307,17 @@ void mx_moe_kernel(K3kMxArgs a)
         const int ntok = min(PT, a.job_cnt[j] - tok0);
         const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[e];
         /* one buffer descriptor per matrix (wave-uniform); per-lane byte offsets */
-        const uint32_t prow = LAYOUT == 0 ? (uint32_t)rows : (uint32_t)((rows + 15) & ~15);
-        const uint32_t pbytes = prow * rstride, sbytes = prow * nblk;
+        const uint32_t prow = LAYOUT == 1 ? (uint32_t)((rows + 15) & ~15) : (uint32_t)rows;
+        /* LAYOUT 2: bf16 weights [rows][K], 2 bytes per element, no scales */
+        const uint32_t pbytes = LAYOUT == 2 ? prow * (uint32_t)K * 2u : prow * rstride;
+        const uint32_t sbytes = LAYOUT == 2 ? 16u : prow * nblk;
         k3_rsrc rp0, rp1, rs0, rs1;
         if (MODE == K3K_MX_GATEUP) {
-            rp0 = k3_make_rsrc(q.p1, pbytes); rs0 = k3_make_rsrc(q.s1, sbytes);
-            rp1 = k3_make_rsrc(q.p3, pbytes); rs1 = k3_make_rsrc(q.s3, sbytes);
+            rp0 = k3_make_rsrc(q.p1, pbytes); rs0 = k3_make_rsrc(LAYOUT == 2 ? q.p1 : q.s1, sbytes);
+            rp1 = k3_make_rsrc(q.p3, pbytes); rs1 = k3_make_rsrc(LAYOUT == 2 ? q.p3 : q.s3, sbytes);
         } else {
             rp0 = rp1 = k3_make_rsrc(q.p2, pbytes);
-            rs0 = rs1 = k3_make_rsrc(q.s2, sbytes);
+            rs0 = rs1 = k3_make_rsrc(LAYOUT == 2 ? q.p2 : q.s2, sbytes);
         }
         uint32_t poff[MT], soff[MT];
         const int ntile = (rows + 15) >> 4;
@@ -326,6 +328,10 @@ void mx_moe_kernel(K3kMxArgs a)
                 const int r = min(rb * rpg + wv * rpw + 16 * mt + r16, rows - 1);
                 poff[m] = (uint32_t)r * rstride + (uint32_t)g * 16u;
                 soff[m] = (uint32_t)r * (uint32_t)nblk;
+            } else if (LAYOUT == 2) {
+                const int r = min(rb * rpg + wv * rpw + 16 * mt + r16, rows - 1);
+                poff[m] = ((uint32_t)r * (uint32_t)K + (uint32_t)g * 32u) * 2u;
+                soff[m] = 0;
             } else {
                 const int t = min((rb * rpg + wv * rpw) / 16 + mt, ntile - 1);
                 poff[m] = (uint32_t)t * (uint32_t)nchunk * 4096u + (uint32_t)lane * 16u;
@@ -364,7 +370,8 @@ void mx_moe_kernel(K3kMxArgs a)
          * chunk c+2 is loaded into chunk c's slot. Scales follow one chunk behind. */
         constexpr int NSLOT = DEPTH == 2 ? 2 : 1;
         constexpr int SQN = MT * (LAYOUT == 0 ? 4 : 1);
-        uint4 qa[NSLOT][SPC][MT];
+        constexpr int WQ = LAYOUT == 2 ? 4 : 1;             /* 16-byte loads per block */
+        uint4 qa[NSLOT][SPC][MT][WQ];
         uint32_t sq[SQN], sqn[SQN], sqnn[SQN];
         uint4 bst[PPW];
 
@@ -386,13 +393,18 @@ void mx_moe_kernel(K3kMxArgs a)
         };
         auto load_step = [&](int c, int d, auto slot) {
             constexpr int S = decltype(slot)::value;
-            const uint32_t bo = LAYOUT == 0 ? (uint32_t)c * 256u + (uint32_t)d * 64u
-                                            : ((uint32_t)c * 4u + (uint32_t)d) * 1024u;
+            const uint32_t bo = LAYOUT == 0   ? (uint32_t)c * 256u + (uint32_t)d * 64u
+                                : LAYOUT == 2 ? (uint32_t)c * 1024u + (uint32_t)d * 256u
+                                              : ((uint32_t)c * 4u + (uint32_t)d) * 1024u;
 #pragma unroll
             for (int m = 0; m < MT; m++)
-                qa[S][d][m] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo);
+#pragma unroll
+                for (int w = 0; w < WQ; w++)
+                    qa[S][d][m][w] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1,
+                                                poff[m] + bo + 16u * w);
         };
         auto load_scales = [&](int c, uint32_t *ss) {
+            if (LAYOUT == 2) return;
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 const k3_rsrc rs = m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1;
@@ -441,24 +453,31 @@ void mx_moe_kernel(K3kMxArgs a)
                 }
                 uint4 qq[MT];
                 float so[MT];
+                if (LAYOUT != 2) {
 #pragma unroll
-                for (int m = 0; m < MT; m++) {
-                    const uint32_t sraw = LAYOUT == 0 ? (sq[4 * m + d] >> (8 * g)) & 0xFFu
-                                                      : (sq[m] >> (8 * d)) & 0xFFu;
-                    const bool nanb = sraw == 255u;          /* NaN byte: the block is 0 */
-                    qq[m] = qa[S][d][m];
-                    qq[m].x = nanb ? 0u : qq[m].x;
-                    qq[m].y = nanb ? 0u : qq[m].y;
-                    qq[m].z = nanb ? 0u : qq[m].z;
-                    qq[m].w = nanb ? 0u : qq[m].w;
-                    so[m] = k3_e8m0_operand(nanb ? 127u : sraw);
+                    for (int m = 0; m < MT; m++) {
+                        const uint32_t sraw = LAYOUT == 0 ? (sq[4 * m + d] >> (8 * g)) & 0xFFu
+                                                          : (sq[m] >> (8 * d)) & 0xFFu;
+                        const bool nanb = sraw == 255u;          /* NaN byte: the block is 0 */
+                        qq[m] = qa[S][d][m][0];
+                        qq[m].x = nanb ? 0u : qq[m].x;
+                        qq[m].y = nanb ? 0u : qq[m].y;
+                        qq[m].z = nanb ? 0u : qq[m].z;
+                        qq[m].w = nanb ? 0u : qq[m].w;
+                        so[m] = k3_e8m0_operand(nanb ? 127u : sraw);
+                    }
                 }
 #pragma unroll
                 for (int m = 0; m < MT; m++)
 #pragma unroll
                     for (int pp = 0; pp < 4; pp++) {
-                        const uint32_t codes = pp == 0 ? qq[m].x : pp == 1 ? qq[m].y : pp == 2 ? qq[m].z : qq[m].w;
-                        const k3_bf16x8 av = k3_dequant8_bf16(codes, so[m]);
+                        k3_bf16x8 av;
+                        if (LAYOUT == 2) {
+                            av = k3_as_bf16x8(qa[S][d][m][WQ == 4 ? pp : 0]);
+                        } else {
+                            const uint32_t codes = pp == 0 ? qq[m].x : pp == 1 ? qq[m].y : pp == 2 ? qq[m].z : qq[m].w;
+                            av = k3_dequant8_bf16(codes, so[m]);
+                        }
 #pragma unroll
                         for (int nb = 0; nb < NB; nb++) {
                             acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh[nb][pp]), acc[m][nb], 0, 0, 0);
@@ -598,7 +617,48 @@ __global__ void mx_tile_kernel(uint8_t *tpacked, uint8_t *tscales, const uint8_t
     }
 }
 
+/* One job over all T tokens (the shared expert): identity permutation, passes of
+ * pass_tok tokens, and the job's bank entry from three weight pointers. */
+__global__ void dense_jobs_kernel(ExpertQDev *slot, const uint8_t *w1, const uint8_t *w3,
+                                  const uint8_t *w2, int *job_expert, int *job_off, int *job_cnt,
+                                  int *pass_job, int *pass_tp, int *counts, int *perm, int T,
+                                  int pass_tok)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int np = (T + pass_tok - 1) / pass_tok;
+    if (i < T) perm[i] = i;
+    if (i < np) {
+        pass_job[i] = 0;
+        pass_tp[i] = i;
+    }
+    if (i == 0) {
+        slot->p1 = w1; slot->s1 = w1;
+        slot->p3 = w3; slot->s3 = w3;
+        slot->p2 = w2; slot->s2 = w2;
+        job_expert[0] = 0;
+        job_off[0] = 0;
+        job_cnt[0] = T;
+        counts[0] = 1;
+        counts[1] = np;
+        counts[2] = 0;
+    }
+}
+
 }  // namespace
+
+extern "C" int k3k_dense_jobs(void *slot, const void *w1, const void *w3, const void *w2,
+                              int *job_expert, int *job_off, int *job_cnt, int *pass_job,
+                              int *pass_tp, int *counts, int *perm, int T, int pass_tok,
+                              void *stream)
+{
+    if (T <= 0) return 0;
+    hipLaunchKernelGGL(dense_jobs_kernel, dim3((T + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       (ExpertQDev *)slot, (const uint8_t *)w1, (const uint8_t *)w3,
+                       (const uint8_t *)w2, job_expert, job_off, job_cnt, pass_job, pass_tp,
+                       counts, perm, T, pass_tok);
+    K3K_LAUNCH_CHECK("dense_jobs launch");
+    return 0;
+}
 
 extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
 {
@@ -616,6 +676,25 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
         const int grid = items < cus * 8 ? items : cus * 8;
         if (a->nsplit == 2) return launch_mx<K3K_MX_PLAIN, 1, 1, 2, 2, 16>(a, kw, grid, st);
         return launch_mx<K3K_MX_PLAIN, 1, 1, 1, 2, 16>(a, kw, grid, st);
+    }
+    if (a->layout == 2) {
+        /* bf16 weights (the dense shared expert): 2 tiles of 16 rows per wave, 32-token
+         * passes with one-term activations or 16-token passes with one or two terms */
+        if (a->K % 512) return k3k_fail("mx_moe bf16: K % 512 != 0", hipErrorInvalidValue);
+        const bool gu = mode == K3K_MX_GATEUP;
+        const int rpg = gu ? 64 : 128;
+        const long items = (long)a->max_passes * ((a->rows + rpg - 1) / rpg);
+        const int grid = (int)(items < (long)cus * 4 ? (items > 0 ? items : 1) : (long)cus * 4);
+        if (a->pass_tok == 32 && a->nsplit == 1)
+            return gu ? launch_moe<K3K_MX_GATEUP, 2, 1, 32, 4, 2, 2, 1, 2>(a, grid, st)
+                      : launch_moe<K3K_MX_DOWN, 2, 1, 32, 4, 2, 2, 1, 2>(a, grid, st);
+        if (a->pass_tok == 16)
+            return a->nsplit == 2
+                       ? (gu ? launch_moe<K3K_MX_GATEUP, 2, 2, 16, 4, 2, 2, 1, 1>(a, grid, st)
+                             : launch_moe<K3K_MX_DOWN, 2, 2, 16, 4, 2, 2, 1, 1>(a, grid, st))
+                       : (gu ? launch_moe<K3K_MX_GATEUP, 2, 1, 16, 4, 2, 2, 1, 1>(a, grid, st)
+                             : launch_moe<K3K_MX_DOWN, 2, 1, 16, 4, 2, 2, 1, 1>(a, grid, st));
+        return k3k_fail("mx_moe bf16: pass size", hipErrorInvalidValue);
     }
     if (a->pass_tok == 32) {
         /* prefill: 32-token passes, two MFMA column blocks per weight fragment, activations

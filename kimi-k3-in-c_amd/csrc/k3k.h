@@ -67,7 +67,8 @@ typedef struct {
      * (K % 512 == 0, bf16 activations: the prefill kernel). */
     const void *bank;                   /* device K3ExpertQ[n_experts] */
     int pass_tok;
-    int layout;                         /* 0: row-major bank, 1: tiled (k3k_mx_tile) */
+    int layout;                         /* 0: row-major MXFP4, 1: tiled MXFP4 (k3k_mx_tile),
+                                           2: bf16 weights [rows][K] (p1/p3/p2 only) */
     const int *job_expert, *job_off, *job_cnt;
     const int *pass_job, *pass_tp, *n_passes;
     const int *perm;                    /* sorted position -> assignment a = t*topk + j */
@@ -83,6 +84,12 @@ typedef struct {
 } K3kMxArgs;
 
 int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
+
+/* The job arrays of one dense expert over T tokens (the shared expert): slot receives the
+ * bank entry {w1, w3, w2}, perm is the identity, passes of pass_tok tokens. */
+int k3k_dense_jobs(void *slot, const void *w1, const void *w3, const void *w2, int *job_expert,
+                   int *job_off, int *job_cnt, int *pass_job, int *pass_tp, int *counts,
+                   int *perm, int T, int pass_tok, void *stream);
 
 /* Row-major MXFP4 matrix [rows][K] (K % 512 == 0) -> the tiled layout of the expert kernel:
  * tpacked [ceil(rows/16)*16][K/2] bytes, tscales [ceil(rows/16)*16][K/32] bytes. */

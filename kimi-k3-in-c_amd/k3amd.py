@@ -22,7 +22,7 @@ K3_WF32, K3_WBF16, K3_WI8 = 0, 1, 2
 K3_ACT_SITU, K3_ACT_SILU = 0, 1
 K3_MAX_TOPK = 64
 K3D_LAYOUT_ROWS, K3D_LAYOUT_TILED = 0, 1
-STAGES = ("begin", "router", "gather", "gateup", "down", "combine", "gemv")
+STAGES = ("begin", "router", "gather", "gateup", "down", "combine", "gemv", "shared")
 
 _lib = None
 
@@ -125,6 +125,8 @@ def _declare(L):
     d("k3d_moe_routed", I, P, P, P, P, I, P, P, P, I, I, I, I, I, I, F, I, F, F, I, P, SZ, P, P,
       P, P)
     d("k3d_moe_experts", I, P, P, P, P, I, P, I, I, I, I, I, I, F, F, I, P, SZ, P, P, P, P)
+    d("k3d_shared_ws", SZ, I, I, I, I)
+    d("k3d_shared_expert", I, P, I, P, I, P, P, P, I, I, I, F, F, I, P, SZ, P)
     d("k3d_mxfp4_tiled_size", I, I, I, P, P)
     d("k3d_mxfp4_tile", I, P, P, P, P, I, I, P)
     # generator
@@ -475,3 +477,27 @@ def router_device(x, W, bias, topk, renorm=1, routed_scale=1.0):
         for b in bufs:
             if b is not None:
                 b.free()
+
+
+def shared_expert_device(x, w1, w3, w2, hidden, inter, act=K3_ACT_SILU, b1=4.0, b2=25.0,
+                         prec=0, y0=None):
+    """k3d_shared_expert on host arrays: w1, w3 [inter][hidden], w2 [hidden][inter] as bf16
+    bit patterns (uint16). Returns s (y0 None) or y0 + s."""
+    L = lib()
+    x = _f32(x).reshape(-1, hidden)
+    T = x.shape[0]
+    ws_b = L.k3d_shared_ws(T, hidden, inter, prec)
+    bufs = [DevBuf(x.nbytes).upload(x), DevBuf(w1.nbytes).upload(w1), DevBuf(w3.nbytes).upload(w3),
+            DevBuf(w2.nbytes).upload(w2), DevBuf(T * hidden * 4), DevBuf(ws_b)]
+    try:
+        dx, d1, d3, d2, dy, dws = bufs
+        if y0 is not None:
+            dy.upload(_f32(y0).reshape(T, hidden))
+        check(L.k3d_shared_expert(dy.ptr, 1 if y0 is not None else 0, dx.ptr, T, d1.ptr, d3.ptr,
+                                  d2.ptr, hidden, inter, act, b1, b2, prec, dws.ptr, ws_b, None),
+              "k3d_shared_expert")
+        check(L.k3d_sync(None), "sync")
+        return dy.download(np.empty((T, hidden), np.float32))
+    finally:
+        for b in bufs:
+            b.free()

@@ -317,3 +317,36 @@ def test_moe_device_prefill_passes(gpu, orc, k3):
     assert np.bincount(idx.ravel(), minlength=N).max() > 32       # several passes per expert
     assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
     assert max_err_rel_inf(out, o2) <= 5e-2
+
+
+def shared_ref(orc, X, w1, w3, w2, hidden, inter):
+    """The reference's shared tail per token: bf16 GEMVs (fp64 accumulation) and SiLU-GLU."""
+    out = np.empty((X.shape[0], hidden), np.float32)
+    for t in range(X.shape[0]):
+        g = orc.matmul_bf16(X[t], w1.reshape(inter, hidden))
+        u = orc.matmul_bf16(X[t], w3.reshape(inter, hidden))
+        a = orc.silu_glu(np.concatenate([g, u]), inter)
+        out[t] = orc.matmul_bf16(a, w2.reshape(hidden, inter))
+    return out
+
+
+@pytest.mark.parametrize("T,prec", [(5, 0), (40, 0), (70, 1)])
+def test_shared_expert_vs_oracle(gpu, orc, k3, T, prec):
+    """The bf16 dense shared expert on the matrix cores against the reference's bf16 GEMV
+    composition: 1e-4 * ||ref||inf with two-term activations, 2e-2 relative with one; the
+    accumulate form adds onto the routed output with one fp32 add."""
+    hidden, inter = 1024, 512
+    say(f"case: shared expert T={T} prec={prec}")
+    w1 = k3.gen_bf16_normal(inter * hidden, 101, 0.0, 0.02)
+    w3 = k3.gen_bf16_normal(inter * hidden, 102, 0.0, 0.02)
+    w2 = k3.gen_bf16_normal(hidden * inter, 103, 0.0, 0.02)
+    X = k3.gen_normal(T * hidden, 104).reshape(T, hidden)
+    ref = shared_ref(orc, X, w1, w3, w2, hidden, inter)
+    got = gpu.shared_expert_device(X, w1, w3, w2, hidden, inter, prec=prec)
+    if prec == 0:
+        assert max_err_rel_inf(got, ref) <= TOL
+    else:
+        assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= TOL_BF16
+    y0 = k3.gen_normal(T * hidden, 105).reshape(T, hidden)
+    got2 = gpu.shared_expert_device(X, w1, w3, w2, hidden, inter, prec=prec, y0=y0)
+    assert np.array_equal(got2, (y0 + got).astype(np.float32))
