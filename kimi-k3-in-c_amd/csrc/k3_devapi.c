@@ -284,9 +284,14 @@ typedef struct {
  * multiples of 512: passes of 8 tokens, or of 32 (two MFMA column blocks) when the
  * activations are single bf16 terms and the batch averages at least 8 tokens per expert
  * (prefill). Other shapes run the register-fed kernel (16, row-major bank only). */
-static int moe_pass_tok(int T, int hidden, int inter, int n_experts, int topk, int prec)
+/* Tokens per expert pass. 8 for decode (fp32-accurate, weight streaming), 16 when the
+ * widths are not multiples of 512; one-term (prefill) activations take 32 from 8 tokens
+ * per expert on average and, for a tiled bank, 48 from 32 tokens per expert. The row-major
+ * choice is never larger than the tiled one, so it sizes the workspace for both. */
+static int moe_pass_tok(int T, int hidden, int inter, int n_experts, int topk, int prec, int layout)
 {
     if (hidden % 512 || inter % 512) return 16;
+    if (prec == 1 && layout == K3D_LAYOUT_TILED && (long)T * topk >= 32L * n_experts) return 48;
     if (prec == 1 && (long)T * topk >= 8L * n_experts) return 32;
     return 8;
 }
@@ -296,7 +301,8 @@ static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n
 {
     const size_t N = (size_t)T * topk;
     const int maxjobs = (int)(N < (size_t)n_experts ? N : (size_t)n_experts);
-    w->max_passes = maxjobs + (int)(N / (size_t)moe_pass_tok(T, hidden, inter, n_experts, topk, prec)) + 1;
+    w->max_passes = maxjobs + (int)(N / (size_t)moe_pass_tok(T, hidden, inter, n_experts, topk, prec,
+                                                                K3D_LAYOUT_ROWS)) + 1;
     w->xhi = (uint16_t *)take(c, (size_t)T * hidden * 2);
     w->xlo = prec == 0 ? (uint16_t *)take(c, (size_t)T * hidden * 2) : NULL;
     w->ahi = (uint16_t *)take(c, N * inter * 2);
@@ -356,7 +362,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
 {
     int *perm = perm_out ? perm_out : w->perm;
     int *offsets = offsets_out ? offsets_out : w->offsets;
-    const int pass_tok = moe_pass_tok(T, hidden, inter, n_experts, topk, prec);
+    const int pass_tok = moe_pass_tok(T, hidden, inter, n_experts, topk, prec, layout);
     if (k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
     if (k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
                    w->counts, idx, T, topk, n_experts, bank, pass_tok, stream))

@@ -545,6 +545,229 @@ int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
     return 0;
 }
 
+/* ---- prefill: large token passes, one-term activations --------------------------------
+ * mx_prefill_kernel: GATEUP / DOWN for passes of up to 16*NB tokens with the activations
+ * as single bf16 terms (the prefill precision), weights tiled MXFP4 (LAYOUT 1) or bf16
+ * (LAYOUT 2). Same item = (pass, row block) and K order as mx_moe_kernel, but K is staged
+ * 256 columns at a time so that up to 96 tokens fit in LDS: each expert's weights are
+ * streamed once per pass of up to 16*NB tokens, and every dequantized weight fragment
+ * feeds MT x NB MFMAs. Stage c covers steps 2(c&1) and 2(c&1)+1 of tiled 512-chunk c>>1.
+ * Activation loads are unconditional (rows clamped to a valid token); only the LDS stores
+ * are masked. */
+template <int MODE, int MT, int NB, int LAYOUT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
+void mx_prefill_kernel(K3kMxArgs a)
+{
+    constexpr int NW = 4, KC = 256, SPC = 2, LDT = KC + 8, PT = 16 * NB, PR = KC / 8;
+    constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
+    constexpr int NPC = PT * PR;                              /* 16-byte pieces per stage */
+    constexpr int PPT = (NPC + 255) / 256;
+    constexpr int WQ = LAYOUT == 2 ? 4 : 1;
+    __shared__ __attribute__((aligned(16))) uint16_t bsh[2][PT + 1][LDT];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int K = a.K, nblk = K >> 5, nstage = K / KC, nchunk = K >> 9;
+    const int rows = a.rows;
+    const uint32_t rstride = (uint32_t)K >> 1;
+    const int rpw = 16 * RT, rpg = NW * rpw;
+    const int n_rb = (rows + rpg - 1) / rpg;
+    const int n_items = (*a.n_passes) * n_rb;
+
+    for (int i = tid; i < 2 * LDT / 8; i += 256)
+        *reinterpret_cast<uint4 *>(&bsh[i / (LDT / 8)][PT][(i % (LDT / 8)) * 8]) = make_uint4(0, 0, 0, 0);
+
+    for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+        const int rb = item % n_rb, pass = item / n_rb;
+        const int j = a.pass_job[pass];
+        const int e = a.job_expert[j];
+        const int off = a.job_off[j];
+        const int tok0 = a.pass_tp[pass] * PT;
+        const int ntok = min(PT, a.job_cnt[j] - tok0);
+        const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[e];
+        const uint32_t prow = LAYOUT == 1 ? (uint32_t)((rows + 15) & ~15) : (uint32_t)rows;
+        const uint32_t pbytes = LAYOUT == 2 ? prow * (uint32_t)K * 2u : prow * rstride;
+        const uint32_t sbytes = LAYOUT == 2 ? 16u : prow * nblk;
+        k3_rsrc rp0, rp1, rs0, rs1;
+        if (MODE == K3K_MX_GATEUP) {
+            rp0 = k3_make_rsrc(q.p1, pbytes); rs0 = k3_make_rsrc(LAYOUT == 2 ? q.p1 : q.s1, sbytes);
+            rp1 = k3_make_rsrc(q.p3, pbytes); rs1 = k3_make_rsrc(LAYOUT == 2 ? q.p3 : q.s3, sbytes);
+        } else {
+            rp0 = rp1 = k3_make_rsrc(q.p2, pbytes);
+            rs0 = rs1 = k3_make_rsrc(LAYOUT == 2 ? q.p2 : q.s2, sbytes);
+        }
+        uint32_t poff[MT], soff[MT];
+        const int ntile = (rows + 15) >> 4;
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            const int mt = (MODE == K3K_MX_GATEUP) ? (m % RT) : m;
+            if (LAYOUT == 2) {
+                const int r = min(rb * rpg + wv * rpw + 16 * mt + r16, rows - 1);
+                poff[m] = ((uint32_t)r * (uint32_t)K + (uint32_t)g * 32u) * 2u;
+                soff[m] = 0;
+            } else {
+                const int t = min((rb * rpg + wv * rpw) / 16 + mt, ntile - 1);
+                poff[m] = (uint32_t)t * (uint32_t)nchunk * 4096u + (uint32_t)lane * 16u;
+                soff[m] = (uint32_t)t * (uint32_t)nchunk * 256u + (uint32_t)lane * 4u;
+            }
+        }
+        /* staging pieces: token row p = pc / PR, 16-byte column piece o = pc % PR */
+        const uint32_t xbytes = (uint32_t)a.n_xrows * (uint32_t)K * 2u;
+        const k3_rsrc rx = k3_make_rsrc(a.xhi, xbytes);
+        uint32_t gsrc[PPT];
+        int ldst[PPT];
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const int pc = tid + 256 * i, p = pc / PR, o = pc % PR;
+            const bool ok = pc < NPC && p < ntok;
+            const int ar = a.perm[off + tok0 + (ok ? p : 0)];
+            const int xr = (MODE == K3K_MX_GATEUP) ? ar / a.topk : ar;
+            gsrc[i] = ((uint32_t)xr * (uint32_t)K + (uint32_t)o * 8u) * 2u;
+            ldst[i] = ok ? p * LDT + o * 8 : -1;
+        }
+        int brow[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) brow[nb] = nb * 16 + r16 < ntok ? nb * 16 + r16 : PT;
+
+        k3_f32x4 acc[MT][NB];
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) acc[m][nb] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
+
+        /* weights two stages ahead: stages alternate between the two register slots */
+        uint4 qa[2][SPC][MT][WQ];
+        uint32_t sq[MT], sqn[MT], sqnn[MT];
+        uint4 bst[PPT];
+        auto load_b = [&](int c) {
+#pragma unroll
+            for (int i = 0; i < PPT; i++) bst[i] = k3_bload16(rx, gsrc[i] + (uint32_t)c * KC * 2u);
+        };
+        auto store_b = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < PPT; i++)
+                if (ldst[i] >= 0) *reinterpret_cast<uint4 *>(&bsh[buf][0][0] + ldst[i]) = bst[i];
+        };
+        auto load_step = [&](int c, int d, auto slot) {
+            constexpr int S = decltype(slot)::value;
+            const uint32_t bo = LAYOUT == 2 ? (uint32_t)c * 512u + (uint32_t)d * 256u
+                                            : ((uint32_t)(c >> 1) * 4u + 2u * (uint32_t)(c & 1) + (uint32_t)d) * 1024u;
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+#pragma unroll
+                for (int w = 0; w < WQ; w++)
+                    qa[S][d][m][w] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo + 16u * w);
+        };
+        auto load_scales = [&](int c, uint32_t *ss) {
+            if (LAYOUT == 2) return;
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                ss[m] = k3_bload4(m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1, soff[m] + (uint32_t)(c >> 1) * 256u);
+        };
+
+        using P0 = std::integral_constant<int, 0>;
+        using P1 = std::integral_constant<int, 1>;
+        load_b(0);
+        load_scales(0, sq);
+#pragma unroll
+        for (int d = 0; d < SPC; d++) load_step(0, d, P0{});
+        if (nstage > 1) {
+            load_scales(1, sqn);
+#pragma unroll
+            for (int d = 0; d < SPC; d++) load_step(1, d, P1{});
+        }
+        store_b(0);
+        __syncthreads();
+        auto stage = [&](int c, auto slot) {
+            constexpr int S = decltype(slot)::value;
+            const int buf = c & 1;
+            const bool more = c + 1 < nstage, more2 = c + 2 < nstage;
+            if (more) load_b(c + 1);
+            if (more2) load_scales(c + 2, sqnn);
+#pragma unroll
+            for (int d = 0; d < SPC; d++) {
+                float so[MT];
+                bool nanb[MT];
+                if (LAYOUT != 2) {
+#pragma unroll
+                    for (int m = 0; m < MT; m++) {
+                        const uint32_t sraw = (sq[m] >> (8 * (2 * (c & 1) + d))) & 0xFFu;
+                        nanb[m] = sraw == 255u;              /* NaN byte: the block is 0 */
+                        so[m] = k3_e8m0_operand(nanb[m] ? 127u : sraw);
+                    }
+                }
+#pragma unroll
+                for (int pp = 0; pp < 4; pp++) {
+                    /* this piece's weights, dequantized once and used by NB MFMAs */
+                    k3_bf16x8 av[MT];
+#pragma unroll
+                    for (int m = 0; m < MT; m++) {
+                        if (LAYOUT == 2) {
+                            av[m] = k3_as_bf16x8(qa[S][d][m][WQ == 4 ? pp : 0]);
+                        } else {
+                            const uint4 qv = qa[S][d][m][0];
+                            const uint32_t codes = pp == 0 ? qv.x : pp == 1 ? qv.y : pp == 2 ? qv.z : qv.w;
+                            av[m] = k3_dequant8_bf16(nanb[m] ? 0u : codes, so[m]);
+                        }
+                    }
+#pragma unroll
+                    for (int nb = 0; nb < NB; nb++) {
+                        const uint4 bv = *reinterpret_cast<const uint4 *>(&bsh[buf][brow[nb]][(4 * d + g) * 32 + pp * 8]);
+#pragma unroll
+                        for (int m = 0; m < MT; m++)
+                            acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[m], k3_as_bf16x8(bv), acc[m][nb], 0, 0, 0);
+                    }
+                }
+                if (more2) load_step(c + 2, d, slot);
+            }
+            if (more) store_b(buf ^ 1);
+#pragma unroll
+            for (int m = 0; m < MT; m++) { sq[m] = sqn[m]; sqn[m] = sqnn[m]; }
+            __syncthreads();
+        };
+        for (int c = 0; c < nstage; c += 2) {
+            stage(c, P0{});
+            if (c + 1 < nstage) stage(c + 1, P1{});
+        }
+
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            const int tk = nb * 16 + r16;
+            if (tk >= ntok) continue;
+            const int orow = a.perm[off + tok0 + tk];
+            for (int m = 0; m < RT; m++) {
+                const int base = rb * rpg + wv * rpw + 16 * m + 4 * g;
+                if (MODE == K3K_MX_GATEUP) {
+                    uint16_t *oh = a.ahi + (size_t)orow * rows;
+                    for (int jj = 0; jj < 4; jj++)
+                        if (base + jj < rows) {
+                            const float v = k3_act_pair(acc[m][nb][jj], acc[m + RT][nb][jj], a.act, a.b1, a.b2);
+                            oh[base + jj] = k3_bf16_rne(v);
+                        }
+                } else {
+                    float *o = a.out + (size_t)orow * rows;
+                    if (base + 3 < rows && (rows & 3) == 0) {
+                        *reinterpret_cast<float4 *>(o + base) =
+                            make_float4(acc[m][nb][0], acc[m][nb][1], acc[m][nb][2], acc[m][nb][3]);
+                    } else {
+                        for (int jj = 0; jj < 4; jj++)
+                            if (base + jj < rows) o[base + jj] = acc[m][nb][jj];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int MODE, int MT, int NB, int LAYOUT>
+int launch_prefill(const K3kMxArgs *a, int grid, hipStream_t st)
+{
+    hipLaunchKernelGGL((mx_prefill_kernel<MODE, MT, NB, LAYOUT>), dim3(grid), dim3(256), 0, st, *a);
+    K3K_LAUNCH_CHECK("mx_prefill launch");
+    return 0;
+}
+
 /* ---- generic vector-unit GEMV: any even K, group <= 64, fp32 arithmetic ---------- */
 /* One wave per row; lane-strided elements, weight = E2M1 * 2^(s-127) in fp32 (exact),
  * fp32 fma accumulation, butterfly reduction. */
@@ -676,6 +899,22 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
         const int grid = items < cus * 8 ? items : cus * 8;
         if (a->nsplit == 2) return launch_mx<K3K_MX_PLAIN, 1, 1, 2, 2, 16>(a, kw, grid, st);
         return launch_mx<K3K_MX_PLAIN, 1, 1, 1, 2, 16>(a, kw, grid, st);
+    }
+    if (a->pass_tok == 48) {
+        /* large prefill batches: 48-token passes, K staged 256 columns at a time, weights
+         * two stages ahead, three MFMA column blocks per weight fragment */
+        if (a->K % 512 || a->nsplit != 1 || a->layout == 0)
+            return k3k_fail("mx_moe: 48-token passes need K % 512 == 0, bf16 activations and "
+                            "tiled or bf16 weights", hipErrorInvalidValue);
+        const bool gu = mode == K3K_MX_GATEUP;
+        const int rpg = gu ? 128 : 256;
+        const long items = (long)a->max_passes * ((a->rows + rpg - 1) / rpg);
+        const int grid = (int)(items < (long)cus * 4 ? (items > 0 ? items : 1) : (long)cus * 4);
+        if (a->layout == 1)
+            return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 1>(a, grid, st)
+                      : launch_prefill<K3K_MX_DOWN, 4, 3, 1>(a, grid, st);
+        return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 2>(a, grid, st)
+                  : launch_prefill<K3K_MX_DOWN, 4, 3, 2>(a, grid, st);
     }
     if (a->layout == 2) {
         /* bf16 weights (the dense shared expert): 2 tiles of 16 rows per wave, 32-token
