@@ -125,13 +125,18 @@ __device__ __forceinline__ k3_rsrc k3_make_rsrc(const void *base, uint32_t bytes
     return __builtin_amdgcn_make_buffer_rsrc(ub, 0, __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 
+/* Cache policy of a load: K3_LD_NT marks data streamed once (expert weights), which moves
+ * through the caches without displacing what is reused. */
+enum { K3_LD_DEFAULT = 0, K3_LD_NT = 2 };
+template <int POL = K3_LD_DEFAULT>
 __device__ __forceinline__ uint4 k3_bload16(k3_rsrc r, uint32_t off)
 {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL));
 }
+template <int POL = K3_LD_DEFAULT>
 __device__ __forceinline__ uint32_t k3_bload4(k3_rsrc r, uint32_t off)
 {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL);
 }
 
 __device__ __forceinline__ k3_bf16x8 k3_as_bf16x8(uint4 v)

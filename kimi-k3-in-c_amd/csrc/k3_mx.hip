@@ -277,6 +277,9 @@ void mx_moe_kernel(K3kMxArgs a)
     static_assert(PT <= 16 * NB, "a pass fits the MFMA column blocks");
     constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
     constexpr int KC = 512, SPC = 4, LDT = KC + 8;           /* LDS row: 16-byte pad */
+    /* MXFP4 weights are streamed once per pass and non-temporal; bf16 (dense) weights are
+     * re-read by every pass of the batch and keep the default policy */
+    constexpr int WPOL = LAYOUT == 2 ? K3_LD_DEFAULT : K3_LD_NT;
     constexpr int NRH = PT * NS;                             /* staged row-halves per chunk */
     constexpr int PPW = (NRH + NW - 1) / NW;                 /* row-halves per wave */
     /* row PT of each buffer/half stays zero: the B operand of absent token columns */
@@ -400,7 +403,7 @@ void mx_moe_kernel(K3kMxArgs a)
             for (int m = 0; m < MT; m++)
 #pragma unroll
                 for (int w = 0; w < WQ; w++)
-                    qa[S][d][m][w] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1,
+                    qa[S][d][m][w] = k3_bload16<WPOL>(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1,
                                                 poff[m] + bo + 16u * w);
         };
         auto load_scales = [&](int c, uint32_t *ss) {
@@ -409,10 +412,10 @@ void mx_moe_kernel(K3kMxArgs a)
             for (int m = 0; m < MT; m++) {
                 const k3_rsrc rs = m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1;
                 if (LAYOUT == 0) {
-                    const uint4 v = k3_bload16(rs, soff[m] + (uint32_t)c * 16u);
+                    const uint4 v = k3_bload16<WPOL>(rs, soff[m] + (uint32_t)c * 16u);
                     ss[4 * m] = v.x; ss[4 * m + 1] = v.y; ss[4 * m + 2] = v.z; ss[4 * m + 3] = v.w;
                 } else {
-                    ss[m] = k3_bload4(rs, soff[m] + (uint32_t)c * 256u);
+                    ss[m] = k3_bload4<WPOL>(rs, soff[m] + (uint32_t)c * 256u);
                 }
             }
         };
@@ -553,7 +556,8 @@ int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
  * streamed once per pass of up to 16*NB tokens, and every dequantized weight fragment
  * feeds MT x NB MFMAs. Stage c covers steps 2(c&1) and 2(c&1)+1 of tiled 512-chunk c>>1.
  * Activation loads are unconditional (rows clamped to a valid token); only the LDS stores
- * are masked. */
+ * are masked. Weight loads keep the default cache policy: an expert with several passes
+ * re-reads its weights, and the caches then serve part of them. */
 template <int MODE, int MT, int NB, int LAYOUT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void mx_prefill_kernel(K3kMxArgs a)
