@@ -176,14 +176,18 @@ int k3d_matmul_mxfp4(float *y, const float *x, int ntok, const uint8_t *packed,
     Carve c = {(char *)ws, 0};
     MxWs w;
     mx_layout(&c, &w, ntok, in);
-    if (k3k_split_bf16(w.xhi, prec == 0 ? w.xlo : NULL, x, (size_t)ntok * in, stream))
-        return fail("split");
     K3kMxArgs a;
     memset(&a, 0, sizeof a);
     a.packed = packed;
     a.scales = scales;
-    a.xhi = w.xhi;
-    a.xlo = w.xlo;
+    if (k3k_mx_small_ok(ntok, in, prec == 0 ? 2 : 1, rows, x)) {
+        a.xf32 = x;                 /* one or two tokens: the kernel splits x itself */
+    } else {
+        if (k3k_split_bf16(w.xhi, prec == 0 ? w.xlo : NULL, x, (size_t)ntok * in, stream))
+            return fail("split");
+        a.xhi = w.xhi;
+        a.xlo = w.xlo;
+    }
     a.y = y;
     a.ntok = ntok;
     a.ldy = rows;

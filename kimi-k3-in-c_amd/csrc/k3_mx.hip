@@ -249,6 +249,190 @@ int launch_mx(const K3kMxArgs *a, int kw, int grid, hipStream_t st)
     return 0;
 }
 
+/* ---- PLAIN, one or two tokens ---------------------------------------------------------
+ * y = W x for ntok <= 2 fp32 token rows; one workgroup per 16-row tile, its waves splitting
+ * K. Each wave issues the activation loads first (they return from the cache while the
+ * weights stream), then every weight and scale load of its K share; the workgroup stages
+ * the activations into LDS as bf16 terms (k3_split2: hi, and lo when NS == 2), so no
+ * separate split pass runs. B operand lanes of token columns >= ntok, and of columns past
+ * K, are masked to zero without branches (a branch there serialises every LDS read). The
+ * waves' partial sums are added in wave order.
+ *
+ * stage_x: the ntok rows [ntok][K] are contiguous, so float4 i holds elements 4i..4i+3 of
+ * the flattened rows and lands at hi[4i], lo[ntok*K + 4i]. */
+template <int NS, int XPT>
+__device__ __forceinline__ void gemv_stage_x(uint16_t *xs, const float4 (&xv)[XPT], int tid,
+                                             int nthr, int nq, int ntok, int K)
+{
+#pragma unroll
+    for (int j = 0; j < XPT; j++) {
+        const int i = tid + j * nthr;
+        if (i < nq) {
+            const float4 v = xv[j];
+            uint16_t h[4], l[4];
+            k3_split2(v.x, h[0], l[0]);
+            k3_split2(v.y, h[1], l[1]);
+            k3_split2(v.z, h[2], l[2]);
+            k3_split2(v.w, h[3], l[3]);
+            *reinterpret_cast<uint2 *>(&xs[4 * i]) =
+                make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+            if (NS == 2)
+                *reinterpret_cast<uint2 *>(&xs[(size_t)ntok * K + 4 * i]) =
+                    make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+        }
+    }
+}
+
+/* One step (4 MX blocks) of one lane: codes of block blk of its row, scale byte ss. */
+template <int NS>
+__device__ __forceinline__ void gemv_step(k3_f32x4 (&acc)[2], uint4 qq, uint32_t ss,
+                                          const uint16_t *xh, const uint16_t *xl, uint32_t bm)
+{
+    if (ss == 255u) {                                       /* NaN byte: the block is 0 */
+        qq = make_uint4(0, 0, 0, 0);
+        ss = 127u;
+    }
+    const float so = k3_e8m0_operand(ss);
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const uint32_t codes = p == 0 ? qq.x : p == 1 ? qq.y : p == 2 ? qq.z : qq.w;
+        const k3_bf16x8 av = k3_dequant8_bf16(codes, so);
+        uint4 bh = *reinterpret_cast<const uint4 *>(xh + 8 * p);
+        bh.x &= bm; bh.y &= bm; bh.z &= bm; bh.w &= bm;
+        acc[p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh), acc[p & 1], 0, 0, 0);
+        if (NS == 2) {
+            uint4 bl = *reinterpret_cast<const uint4 *>(xl + 8 * p);
+            bl.x &= bm; bl.y &= bm; bl.z &= bm; bl.w &= bm;
+            acc[p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl), acc[p & 1], 0, 0, 0);
+        }
+    }
+}
+
+/* The waves' sums in wave order (LDS reused after the products), stored by wave 0. */
+__device__ __forceinline__ void gemv_finish(uint16_t *xs, k3_f32x4 acc, int wv, int kw, int lane,
+                                            int r16, int g, int ntok, int tile, int rows,
+                                            float *y, int ldy)
+{
+    k3_f32x4 *red = reinterpret_cast<k3_f32x4 *>(xs);
+    __syncthreads();
+    red[wv * 64 + lane] = acc;
+    __syncthreads();
+    if (wv == 0) {
+        k3_f32x4 part[16];
+#pragma unroll
+        for (int w = 0; w < 16; w++) part[w] = w < kw ? red[w * 64 + lane] : k3_f32x4{0.f, 0.f, 0.f, 0.f};
+        k3_f32x4 sum = part[0];
+#pragma unroll
+        for (int w = 1; w < 16; w++) sum += part[w];
+        if (r16 < ntok) {
+            float *o = y + (size_t)r16 * ldy;
+            const int base = tile * 16 + 4 * g;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                if (base + jj < rows) o[base + jj] = sum[jj];
+        }
+    }
+}
+
+/* mx_gemv_chunk_kernel: K % 512 == 0, one 512-column chunk per wave (kw = K / 512 <= 16).
+ * A lane loads blocks 4i+g (i = 0..3) of its row and the row's 16 scale bytes of the chunk
+ * in one 16-byte load, with the default cache policy: the two halves of each 128-byte
+ * line come from two load instructions. */
+template <int NS>
+__global__ __launch_bounds__(1024) void mx_gemv_chunk_kernel(K3kMxArgs a, int kw)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+    constexpr int XPT = 4;                                  /* 2 ntok float4 per thread */
+    const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int K = a.K, nblk = K >> 5, rows = a.rows, ntok = a.ntok;
+    const int tile = blockIdx.x;
+    const int nq = ntok * (K >> 2);
+    float4 xv[XPT];
+#pragma unroll
+    for (int j = 0; j < XPT; j++) {
+        const int i = tid + j * nthr;
+        xv[j] = i < nq ? *reinterpret_cast<const float4 *>(a.xf32 + 4 * (size_t)i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    uint4 q[4];
+    uint32_t sc[4];
+    const int row = min(tile * 16 + r16, rows - 1);         /* rows past the end: discarded */
+    const k3_rsrc rp = k3_make_rsrc(a.packed, (uint32_t)rows * (uint32_t)(K >> 1));
+    const k3_rsrc rs = k3_make_rsrc(a.scales, (uint32_t)rows * (uint32_t)nblk);
+    const uint32_t pb = (uint32_t)row * (uint32_t)(K >> 1) + (uint32_t)wv * 256u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = k3_bload16(rp, pb + (uint32_t)(4 * i + g) * 16u);
+    const uint4 sv = k3_bload16(rs, (uint32_t)row * (uint32_t)nblk + (uint32_t)wv * 16u);
+    sc[0] = (sv.x >> (8 * g)) & 0xffu;
+    sc[1] = (sv.y >> (8 * g)) & 0xffu;
+    sc[2] = (sv.z >> (8 * g)) & 0xffu;
+    sc[3] = (sv.w >> (8 * g)) & 0xffu;
+    gemv_stage_x<NS>(xs, xv, tid, nthr, nq, ntok, K);
+    __syncthreads();
+    const int xr = r16 < ntok ? r16 : 0;
+    const uint32_t bm = r16 < ntok ? ~0u : 0u;
+    k3_f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int blk = wv * 16 + 4 * i + g;
+        gemv_step<NS>(acc, q[i], sc[i], &xs[(size_t)xr * K + blk * 32],
+                      &xs[(size_t)(ntok + xr) * K + blk * 32], bm);
+    }
+    gemv_finish(xs, acc[0] + acc[1], wv, kw, lane, r16, g, ntok, tile, a.rows, a.y, a.ldy);
+}
+
+/* mx_gemv_small_kernel: any K % 32 == 0 (row-major), runs of at most SMAX steps per wave
+ * (kw <= 16). A lane loads block 4s+g of its row and that block's scale byte; lanes past
+ * the wave's run or past K take the offset 2^31, beyond the buffer's size (< 2^31), where a
+ * buffer load returns zero. */
+template <int NS, int SMAX>
+__global__ __launch_bounds__(1024) void mx_gemv_small_kernel(K3kMxArgs a, int kw)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+    constexpr int XPT = 8;
+    const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int K = a.K, nblk = K >> 5, nsteps = (nblk + 3) >> 2, rows = a.rows, ntok = a.ntok;
+    const int tile = blockIdx.x;
+    const int s0 = (wv * nsteps) / kw, s1 = ((wv + 1) * nsteps) / kw;
+    const int nq = ntok * (K >> 2);
+    float4 xv[XPT];
+#pragma unroll
+    for (int j = 0; j < XPT; j++) {
+        const int i = tid + j * nthr;
+        xv[j] = i < nq ? *reinterpret_cast<const float4 *>(a.xf32 + 4 * (size_t)i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const int row = min(tile * 16 + r16, rows - 1);
+    const k3_rsrc rp = k3_make_rsrc(a.packed, (uint32_t)rows * (uint32_t)(K >> 1));
+    const k3_rsrc rs = k3_make_rsrc(a.scales, (uint32_t)rows * (uint32_t)nblk);
+    const uint32_t pbase = (uint32_t)row * (uint32_t)(K >> 1), sbase = (uint32_t)row * (uint32_t)nblk;
+    uint4 q[SMAX];
+    uint32_t sc[SMAX];
+#pragma unroll
+    for (int i = 0; i < SMAX; i++) {
+        const int blk = 4 * (s0 + i) + g;
+        const bool v = s0 + i < s1 && blk < nblk;
+        q[i] = k3_bload16(rp, v ? pbase + (uint32_t)blk * 16u : 0x80000000u);
+        sc[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, v ? sbase + (uint32_t)blk : 0x80000000u, 0, 0);
+    }
+    gemv_stage_x<NS>(xs, xv, tid, nthr, nq, ntok, K);
+    __syncthreads();
+    const int xr = r16 < ntok ? r16 : 0;
+    k3_f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int i = 0; i < SMAX; i++) {
+        const int blk0 = 4 * (s0 + i) + g;
+        const bool kv = s0 + i < s1 && blk0 < nblk;          /* columns past K contribute 0 */
+        const int blk = kv ? blk0 : nblk - 1;
+        const uint32_t bm = (r16 < ntok && kv) ? ~0u : 0u;
+        gemv_step<NS>(acc, q[i], sc[i], &xs[(size_t)xr * K + blk * 32],
+                      &xs[(size_t)(ntok + xr) * K + blk * 32], bm);
+    }
+    gemv_finish(xs, acc[0] + acc[1], wv, kw, lane, r16, g, ntok, tile, a.rows, a.y, a.ldy);
+}
+
 /* ---- expert jobs, LDS-staged activations ---------------------------------------------
  * mx_moe_kernel: the GATEUP / DOWN modes in passes of up to PT tokens, K % 512 == 0.
  *
@@ -277,9 +461,10 @@ void mx_moe_kernel(K3kMxArgs a)
     static_assert(PT <= 16 * NB, "a pass fits the MFMA column blocks");
     constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
     constexpr int KC = 512, SPC = 4, LDT = KC + 8;           /* LDS row: 16-byte pad */
-    /* MXFP4 weights are streamed once per pass and non-temporal; bf16 (dense) weights are
-     * re-read by every pass of the batch and keep the default policy */
-    constexpr int WPOL = LAYOUT == 2 ? K3_LD_DEFAULT : K3_LD_NT;
+    /* tiled MXFP4 weights are streamed once per pass and non-temporal; row-major ones keep
+     * the default policy (a 128-byte line is consumed by two steps' loads), as do bf16
+     * (dense) weights, which every pass of the batch re-reads */
+    constexpr int WPOL = LAYOUT == 1 ? K3_LD_NT : K3_LD_DEFAULT;
     constexpr int NRH = PT * NS;                             /* staged row-halves per chunk */
     constexpr int PPW = (NRH + NW - 1) / NW;                 /* row-halves per wave */
     /* row PT of each buffer/half stays zero: the B operand of absent token columns */
@@ -895,6 +1080,26 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
     const int nsteps = (a->K / 32 + 3) / 4;
     if (mode == K3K_MX_PLAIN) {
         if (a->ntok <= 0) return 0;
+        if (a->xf32) {
+            /* one or two fp32 tokens, activations staged in LDS: waves of one 512-column
+             * chunk when K allows, else up to 16 waves of <= 8 steps */
+            if (!k3k_mx_small_ok(a->ntok, a->K, a->nsplit, a->rows, a->xf32))
+                return k3k_fail("mx_gemm: fp32 activations need ntok <= 2 and a small K",
+                                hipErrorInvalidValue);
+            const bool chunked = a->K % 512 == 0 && a->K <= 16 * 512;
+            const int kw = chunked ? a->K / 512 : (nsteps + 7) / 8;
+            size_t lds = (size_t)a->nsplit * a->ntok * a->K * 2;
+            if (lds < (size_t)kw * 1024) lds = (size_t)kw * 1024;
+            const int grid = (a->rows + 15) / 16;
+            void (*kern)(K3kMxArgs, int);
+            if (chunked)
+                kern = a->nsplit == 2 ? mx_gemv_chunk_kernel<2> : mx_gemv_chunk_kernel<1>;
+            else
+                kern = a->nsplit == 2 ? mx_gemv_small_kernel<2, 8> : mx_gemv_small_kernel<1, 8>;
+            hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kw), lds, st, *a, kw);
+            K3K_LAUNCH_CHECK("mx_gemv_small launch");
+            return 0;
+        }
         /* One matrix: items of 16 rows; K split over up to 16 waves of a workgroup so that
          * about 2k waves each issue their whole K share (<= 4 steps) at once. */
         const int items = ((a->rows + 15) / 16) * ((a->ntok + 15) / 16);

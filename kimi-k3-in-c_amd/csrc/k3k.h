@@ -60,6 +60,7 @@ typedef struct {
     /* PLAIN: one job. */
     const uint8_t *packed, *scales;     /* [rows][K/2], [rows][K/32] */
     const uint16_t *xhi, *xlo;          /* [ntok][K] */
+    const float *xf32;                  /* or fp32 rows [ntok][K], ntok <= 2: split in-kernel */
     float *y;                           /* [ntok][ldy] */
     int ntok, ldy;
     /* GATEUP / DOWN: jobs from the gather. A pass is up to pass_tok tokens of one job:
@@ -84,6 +85,15 @@ typedef struct {
 } K3kMxArgs;
 
 int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
+
+/* Whether PLAIN may take fp32 activations (xf32): one or two tokens whose bf16 terms fit in
+ * 64 KB of LDS, K <= 16384, x 16-byte aligned, the packed matrix under 2 GiB. */
+static inline int k3k_mx_small_ok(int ntok, int K, int nsplit, int rows, const void *x)
+{
+    const long nsteps = ((long)K / 32 + 3) / 4;
+    return ntok >= 1 && ntok <= 2 && K % 32 == 0 && (long)nsplit * ntok * K * 2 <= 65536 &&
+           nsteps <= 128 && ((uintptr_t)x % 16) == 0 && (unsigned long long)rows * (K / 2) < 0x80000000ull;
+}
 
 /* The job arrays of one dense expert over T tokens (the shared expert): slot receives the
  * bank entry {w1, w3, w2}, perm is the identity, passes of pass_tok tokens. */

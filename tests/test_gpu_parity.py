@@ -59,6 +59,38 @@ def test_gemv_edge_cases(gpu, gold, case):
     assert max_err_rel_inf(y, gold["edge_" + case]) <= TOL
 
 
+@pytest.mark.parametrize("ntok,prec", [(1, 0), (2, 0), (3, 0), (1, 1), (2, 1)])
+@pytest.mark.parametrize("rows,inn", [(2048, 7168), (37, 224), (100, 16384)])
+def test_gemv_device_tokens(gpu, orc, ntok, prec, rows, inn):
+    """k3d_matmul_mxfp4 on device buffers: one or two tokens take the kernel that splits
+    fp32 activations itself (where they fit in LDS), three the split pass; every token
+    against the oracle: 1e-4 * ||ref||inf with two-term activations, 2e-2 relative with
+    one. Rows not a multiple of 16 and K not a multiple of 128 included."""
+    say(f"case: device gemv rows={rows} in={inn} ntok={ntok} prec={prec}")
+    rng = np.random.default_rng(rows + inn + 10 * ntok + prec)
+    pk = rng.integers(0, 256, rows * inn // 2, dtype=np.uint8)
+    sc = rng.integers(118, 128, rows * inn // 32, dtype=np.uint8)
+    sc[rng.integers(0, sc.size, 8)] = 255                  # NaN bytes: blocks of zeros
+    X = rng.standard_normal((ntok, inn)).astype(np.float32)
+    L = gpu.lib()
+    dp, ds = gpu.DevBuf(pk.nbytes).upload(pk), gpu.DevBuf(sc.nbytes).upload(sc)
+    dx, dy = gpu.DevBuf(X.nbytes).upload(X), gpu.DevBuf(ntok * rows * 4)
+    ws = gpu.DevBuf(max(L.k3d_matmul_mxfp4_ws(ntok, inn), 16))
+    try:
+        gpu.check(L.k3d_matmul_mxfp4(dy.ptr, dx.ptr, ntok, dp.ptr, ds.ptr, inn, rows, prec,
+                                     ws.ptr, ws.nbytes, None), "k3d_matmul_mxfp4")
+        Y = dy.download(np.empty((ntok, rows), np.float32))
+    finally:
+        for b in (dp, ds, dx, dy, ws):
+            b.free()
+    for t in range(ntok):
+        want = orc.matmul_mxfp4(X[t], pk, sc, inn, rows)
+        if prec == 0:
+            assert max_err_rel_inf(Y[t], want) <= TOL
+        else:
+            assert np.linalg.norm(Y[t] - want) / np.linalg.norm(want) <= TOL_BF16
+
+
 def test_dense_gemv_f32_bf16_identical(gpu, orc):
     """k3_matmul_bf16 equals k3_matmul on the widened weights bit for bit, over arbitrary
     finite bf16 patterns (the reference's own check, test_ops.c:811-848)."""
