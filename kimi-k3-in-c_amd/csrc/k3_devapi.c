@@ -300,6 +300,14 @@ static int moe_pass_tok(int T, int hidden, int inter, int n_experts, int topk, i
     return 8;
 }
 
+/* The decode path (k3k_mx_decode): at most 16 assignments, widths multiples of 512 up to
+ * 8192, the tokens 16-byte aligned. */
+static int moe_decode_ok(int T, int hidden, int inter, int topk, const float *x)
+{
+    return (long)T * topk <= 16 && hidden % 512 == 0 && inter % 512 == 0 && hidden <= 8192 &&
+           inter <= 8192 && ((uintptr_t)x % 16) == 0;
+}
+
 static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n_experts, int topk,
                          int prec)
 {
@@ -367,6 +375,45 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     int *perm = perm_out ? perm_out : w->perm;
     int *offsets = offsets_out ? offsets_out : w->offsets;
     const int pass_tok = moe_pass_tok(T, hidden, inter, n_experts, topk, prec, layout);
+    if (moe_decode_ok(T, hidden, inter, topk, x)) {
+        /* a few assignments: one workgroup per (assignment, 16-row tile), straight from idx;
+         * the gather runs only when its permutation is asked for */
+        if ((perm_out || offsets_out) &&
+            k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
+                       w->counts, idx, T, topk, n_experts, bank, pass_tok, stream))
+            return fail("gather");
+        k3k_prof_mark(stream, K3D_STAGE_GATHER);
+        K3kMxArgs a;
+        memset(&a, 0, sizeof a);
+        a.bank = bank;
+        a.layout = layout;
+        a.idx = idx;
+        a.n_assign = T * topk;
+        a.drops = w->counts + 2;
+        a.topk = topk;
+        a.act = act;
+        a.b1 = b1;
+        a.b2 = b2;
+        a.nsplit = prec == 0 ? 2 : 1;
+        a.xf32 = x;
+        a.ahi = w->ahi;
+        a.alo = w->alo;
+        a.rows = inter;
+        a.K = hidden;
+        if (k3k_mx_decode(K3K_MX_GATEUP, &a, stream)) return fail("mx_decode gateup");
+        k3k_prof_mark(stream, K3D_STAGE_GATEUP);
+        a.xhi = w->ahi;
+        a.xlo = w->alo;
+        a.out = w->contrib;
+        a.rows = hidden;
+        a.K = inter;
+        if (k3k_mx_decode(K3K_MX_DOWN, &a, stream)) return fail("mx_decode down");
+        k3k_prof_mark(stream, K3D_STAGE_DOWN);
+        if (k3k_combine(out, w->contrib, wt, idx, bank, n_experts, T, topk, hidden, stream)) return fail("combine");
+        k3k_prof_mark(stream, K3D_STAGE_COMBINE);
+        if (drops_out && k3k_d2d(drops_out, w->counts + 2, 4, stream)) return fail("drops");
+        return 0;
+    }
     if (k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
     if (k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
                    w->counts, idx, T, topk, n_experts, bank, pass_tok, stream))

@@ -433,6 +433,193 @@ __global__ __launch_bounds__(1024) void mx_gemv_small_kernel(K3kMxArgs a, int kw
     gemv_finish(xs, acc[0] + acc[1], wv, kw, lane, r16, g, ntok, tile, a.rows, a.y, a.ldy);
 }
 
+/* ---- decode of a few assignments ------------------------------------------------------
+ * mx_decode_kernel: GATEUP / DOWN when the batch has at most 16 assignments (T * topk),
+ * straight from the router's idx, without the gather. Item = (assignment a, 4 tiles of 16
+ * rows), one workgroup of 4 * KS waves: wave w takes tile w % 4 and the K share w / 4 of
+ * the KS equal shares of 512-column chunks, and streams it with two chunks of weights in
+ * flight. The workgroup stages the activations once (GATEUP: token a / topk from fp32,
+ * split in-kernel; DOWN: assignment a's bf16 terms) plus a 1 KB block of zeros: lanes of
+ * token columns > 0 read the zeros, so the B operands need no masking. The K shares are
+ * added in order, then GATEUP writes act(gate, up) of assignment a as bf16 terms and DOWN
+ * writes contrib[a]. A dropped expert (NULL weights) is skipped; the combine leaves it
+ * out. GATEUP's block 0 stores the number of dropped assignments in *a.drops. */
+template <int MODE, int NS, int LAYOUT, int KS>
+__global__ __launch_bounds__(256 * KS) void mx_decode_kernel(K3kMxArgs a)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* [NS][K], zeros[512] */
+    constexpr int TPW = 4, NM = MODE == K3K_MX_GATEUP ? 2 : 1;     /* gate + up, or down */
+    constexpr int XPT = 16 / KS;                                   /* K <= 8192 */
+    constexpr int WPOL = LAYOUT == 1 ? K3_LD_NT : K3_LD_DEFAULT;
+    const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int K = a.K, nblk = K >> 5, rows = a.rows, ntile = (rows + 15) >> 4, nchunk = K >> 9;
+    const int ngrp = (ntile + TPW - 1) / TPW;
+    const int asg = blockIdx.x / ngrp, tg = blockIdx.x % ngrp;
+    const int tw = tg * TPW + wv % TPW, ks = wv / TPW;
+    const int tile = min(tw, ntile - 1);                    /* past the last tile: discarded */
+    const int c0 = ks * nchunk / KS, c1 = (ks + 1) * nchunk / KS;
+    if (MODE == K3K_MX_GATEUP && blockIdx.x == 0 && tid == 0) {
+        int nd = 0;
+        for (int i = 0; i < a.n_assign; i++)
+            nd += reinterpret_cast<const ExpertQDev *>(a.bank)[a.idx[i]].p1 == nullptr;
+        *a.drops = nd;
+    }
+    const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[a.idx[asg]];
+    const uint8_t *pm[NM], *sm[NM];
+    if (MODE == K3K_MX_GATEUP) {
+        pm[0] = q.p1; sm[0] = q.s1;
+        pm[NM - 1] = q.p3; sm[NM - 1] = q.s3;
+    } else {
+        pm[0] = q.p2; sm[0] = q.s2;
+    }
+    if (pm[0] == nullptr) return;                           /* dropped expert */
+    /* activation loads first: they return while the weights stream */
+    float4 xv[XPT];
+    uint4 hv[XPT];
+    const int nq = MODE == K3K_MX_GATEUP ? K >> 2 : NS * (K >> 3);
+#pragma unroll
+    for (int j = 0; j < XPT; j++) {
+        const int i = tid + j * nthr;
+        if (MODE == K3K_MX_GATEUP)
+            xv[j] = i < nq ? *reinterpret_cast<const float4 *>(a.xf32 + (size_t)(asg / a.topk) * K + 4 * i)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        else
+            hv[j] = i < nq ? *reinterpret_cast<const uint4 *>((i < (K >> 3) ? a.xhi : a.xlo) + (size_t)asg * K +
+                                                                8 * (i % (K >> 3)))
+                           : make_uint4(0, 0, 0, 0);
+    }
+    const uint32_t prow = LAYOUT == 1 ? (uint32_t)ntile * 16u : (uint32_t)rows;
+    k3_rsrc rp[NM], rs[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        rp[m] = k3_make_rsrc(pm[m], prow * (uint32_t)(K >> 1));
+        rs[m] = k3_make_rsrc(sm[m], prow * (uint32_t)nblk);
+    }
+    const int row = min(tile * 16 + r16, rows - 1);
+    /* chunk c of this wave's tile: LAYOUT 1, four contiguous 1 KB loads and one scale
+     * dword (byte i = step i); LAYOUT 0, blocks 4i+g of the lane's row and the row's 16
+     * scale bytes (dword i, byte g = step i) */
+    uint4 qa[2][NM][4];
+    uint4 sq[2][NM];
+    auto load = [&](int c, auto slot) {
+        constexpr int S = decltype(slot)::value;
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            if (LAYOUT == 1) {
+                const uint32_t tc = (uint32_t)tile * (uint32_t)nchunk + (uint32_t)c;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    qa[S][m][i] = k3_bload16<WPOL>(rp[m], tc * 4096u + (uint32_t)i * 1024u + (uint32_t)lane * 16u);
+                sq[S][m].x = k3_bload4<WPOL>(rs[m], tc * 256u + (uint32_t)lane * 4u);
+            } else {
+                const uint32_t pb = (uint32_t)row * (uint32_t)(K >> 1) + (uint32_t)c * 256u;
+#pragma unroll
+                for (int i = 0; i < 4; i++) qa[S][m][i] = k3_bload16<WPOL>(rp[m], pb + (uint32_t)(4 * i + g) * 16u);
+                sq[S][m] = k3_bload16<WPOL>(rs[m], (uint32_t)row * (uint32_t)nblk + (uint32_t)c * 16u);
+            }
+        }
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    if (c0 < c1) load(c0, P0{});
+    if (c0 + 1 < c1) load(c0 + 1, P1{});
+    for (int i = tid; i < 64; i += nthr)
+        reinterpret_cast<uint4 *>(&xs[(size_t)NS * K])[i] = make_uint4(0, 0, 0, 0);
+    if (MODE == K3K_MX_GATEUP) {
+        gemv_stage_x<NS>(xs, xv, tid, nthr, nq, 1, K);
+    } else {
+#pragma unroll
+        for (int j = 0; j < XPT; j++) {
+            const int i = tid + j * nthr;
+            if (i < nq) *reinterpret_cast<uint4 *>(&xs[8 * i]) = hv[j];    /* hi then lo */
+        }
+    }
+    __syncthreads();
+    k3_f32x4 acc[NM][2];
+#pragma unroll
+    for (int m = 0; m < NM; m++) acc[m][0] = acc[m][1] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
+    auto comp = [&](int c, auto slot) {
+        constexpr int S = decltype(slot)::value;
+        const uint16_t *hb = r16 == 0 ? &xs[c * 512 + g * 32] : &xs[(size_t)NS * K + g * 32];
+        const uint16_t *lb = r16 == 0 ? &xs[(size_t)K + c * 512 + g * 32] : hb;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint4 qm[NM];
+            float so[NM];
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                const uint32_t sw = LAYOUT == 1 ? sq[S][m].x >> (8 * i)
+                                  : (i == 0 ? sq[S][m].x : i == 1 ? sq[S][m].y : i == 2 ? sq[S][m].z : sq[S][m].w) >> (8 * g);
+                uint32_t ss = sw & 0xffu;
+                qm[m] = qa[S][m][i];
+                if (ss == 255u) {                           /* NaN byte: the block is 0 */
+                    qm[m] = make_uint4(0, 0, 0, 0);
+                    ss = 127u;
+                }
+                so[m] = k3_e8m0_operand(ss);
+            }
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const uint4 bh = *reinterpret_cast<const uint4 *>(hb + 128 * i + 8 * p);
+                uint4 bl = make_uint4(0, 0, 0, 0);
+                if (NS == 2) bl = *reinterpret_cast<const uint4 *>(lb + 128 * i + 8 * p);
+#pragma unroll
+                for (int m = 0; m < NM; m++) {
+                    const uint32_t codes = p == 0 ? qm[m].x : p == 1 ? qm[m].y : p == 2 ? qm[m].z : qm[m].w;
+                    const k3_bf16x8 av = k3_dequant8_bf16(codes, so[m]);
+                    acc[m][p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh), acc[m][p & 1], 0, 0, 0);
+                    if (NS == 2)
+                        acc[m][p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl), acc[m][p & 1], 0, 0, 0);
+                }
+            }
+        }
+    };
+    for (int c = c0; c < c1; c += 2) {
+        comp(c, P0{});
+        if (c + 2 < c1) load(c + 2, P0{});
+        if (c + 1 < c1) {
+            comp(c + 1, P1{});
+            if (c + 3 < c1) load(c + 3, P1{});
+        }
+    }
+    /* K shares in order: share 0 adds those of shares 1.. (LDS reused after the products) */
+    k3_f32x4 *red = reinterpret_cast<k3_f32x4 *>(xs);
+    if (KS > 1) {
+        __syncthreads();
+        if (ks > 0)
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+                red[(((ks - 1) * TPW + wv % TPW) * NM + m) * 64 + lane] = acc[m][0] + acc[m][1];
+        __syncthreads();
+    }
+    if (ks == 0 && r16 == 0 && tw < ntile) {
+        k3_f32x4 sum[NM];
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            sum[m] = acc[m][0] + acc[m][1];
+#pragma unroll
+            for (int k2 = 1; k2 < KS; k2++) sum[m] += red[(((k2 - 1) * TPW + wv % TPW) * NM + m) * 64 + lane];
+        }
+        const int base = tw * 16 + 4 * g;
+        if (MODE == K3K_MX_GATEUP) {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                if (base + jj < rows) {
+                    uint16_t hi, lo;
+                    k3_split2(k3_act_pair(sum[0][jj], sum[NM - 1][jj], a.act, a.b1, a.b2), hi, lo);
+                    a.ahi[(size_t)asg * rows + base + jj] = hi;
+                    if (NS == 2) a.alo[(size_t)asg * rows + base + jj] = lo;
+                }
+        } else {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                if (base + jj < rows) a.out[(size_t)asg * rows + base + jj] = sum[0][jj];
+        }
+    }
+}
+
 /* ---- expert jobs, LDS-staged activations ---------------------------------------------
  * mx_moe_kernel: the GATEUP / DOWN modes in passes of up to PT tokens, K % 512 == 0.
  *
@@ -1204,6 +1391,31 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
     }
     if (a->nsplit == 2) return launch_mx<K3K_MX_DOWN, 2, 1, 2, 2, 8>(a, kw, (int)grid, st);
     return launch_mx<K3K_MX_DOWN, 2, 1, 1, 2, 8>(a, kw, (int)grid, st);
+}
+
+extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
+{
+    if (a->n_assign <= 0) return 0;
+    if (a->K % 512 || a->K > 16 * 512 || a->n_assign > 16 || a->layout > 1 ||
+        (mode == K3K_MX_GATEUP && (uintptr_t)a->xf32 % 16) ||
+        (size_t)((a->rows + 15) / 16 * 16) * (a->K / 2) >= 0x80000000u)
+        return k3k_fail("mx_decode: shape", hipErrorInvalidValue);
+    /* K split over two waves per tile (measured best for both gate/up and down) */
+    const int nm = mode == K3K_MX_GATEUP ? 2 : 1, ks = 2;
+    size_t lds = (size_t)a->nsplit * a->K * 2 + 1024;
+    if (lds < (size_t)(ks - 1) * 4 * nm * 1024) lds = (size_t)(ks - 1) * 4 * nm * 1024;
+    const int grid = a->n_assign * (((a->rows + 15) / 16 + 3) / 4);
+    void (*kern)(K3kMxArgs);
+    const bool ns2 = a->nsplit == 2, tiled = a->layout == 1;
+    if (mode == K3K_MX_GATEUP)
+        kern = tiled ? (ns2 ? mx_decode_kernel<K3K_MX_GATEUP, 2, 1, 2> : mx_decode_kernel<K3K_MX_GATEUP, 1, 1, 2>)
+                     : (ns2 ? mx_decode_kernel<K3K_MX_GATEUP, 2, 0, 2> : mx_decode_kernel<K3K_MX_GATEUP, 1, 0, 2>);
+    else
+        kern = tiled ? (ns2 ? mx_decode_kernel<K3K_MX_DOWN, 2, 1, 2> : mx_decode_kernel<K3K_MX_DOWN, 1, 1, 2>)
+                     : (ns2 ? mx_decode_kernel<K3K_MX_DOWN, 2, 0, 2> : mx_decode_kernel<K3K_MX_DOWN, 1, 0, 2>);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256 * ks), lds, (hipStream_t)stream, *a);
+    K3K_LAUNCH_CHECK("mx_decode launch");
+    return 0;
 }
 
 extern "C" int k3k_mx_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,

@@ -82,9 +82,19 @@ typedef struct {
     int rows, K, nsplit;
     int n_xrows;                        /* rows of the activation arrays (xhi/xlo) */
     int max_passes;                     /* host-side bound on *n_passes (grid sizing) */
+    /* k3k_mx_decode: the router's idx [n_assign] (assignment a = t*topk + j -> expert);
+     * GATEUP reads tokens from xf32 and stores the dropped count in *drops; DOWN reads
+     * the activation terms xhi/xlo [n_assign][K]. */
+    const int *idx;
+    int n_assign;
+    int *drops;
 } K3kMxArgs;
 
 int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
+
+/* GATEUP / DOWN for at most 16 assignments without the gather: one workgroup per
+ * (assignment, 16-row tile), K % 512 == 0 and K <= 8192, row-major or tiled bank. */
+int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream);
 
 /* Whether PLAIN may take fp32 activations (xf32): one or two tokens whose bf16 terms fit in
  * 64 KB of LDS, K <= 16384, x 16-byte aligned, the packed matrix under 2 GiB. */

@@ -130,6 +130,52 @@ def test_moe_device_layouts_vs_oracle(gpu, orc, small_layer, prec):
         assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
 
 
+@pytest.mark.parametrize("T,K,prec", [(1, 8, 0), (2, 8, 0), (1, 8, 1), (3, 5, 0), (2, 7, 1)])
+def test_moe_device_decode_path(gpu, orc, k3, T, K, prec):
+    """At most 16 assignments (T * topk) take the decode kernels straight from the router's
+    idx, one workgroup per (assignment, 16-row tile), without the gather: outputs against
+    the oracle's per-slot sum (1e-4 * ||ref||inf with two-term activations, 2e-2 relative
+    with one), row-major and tiled banks bit-identical, a NaN-scaled expert, and a dropped
+    expert that contributes nothing and is counted."""
+    E, I, N = 1024, 1536, 12
+    say(f"case: device moe decode path T={T} K={K} prec={prec}")
+    rng = np.random.default_rng(100 * T + K + prec)
+    bank = [k3.gen_expert(E, I, 61, e) for e in range(N)]
+    bank[5] = nan_scaled(k3, E, I, 61, 5)
+    W = (rng.standard_normal((N, E)) * 0.05).astype(np.float32)
+    X = rng.standard_normal((T, E)).astype(np.float32)
+    _, idx0, _ = orc.moe_routed(X, W, None, bank, E, I, K)
+    victim = int(idx0[0, 1])
+    holed = list(bank)
+    holed[victim] = None
+    res = {}
+    for layout in (gpu.K3D_LAYOUT_ROWS, gpu.K3D_LAYOUT_TILED):
+        b = gpu.DevBank(holed, E, I, layout)
+        try:
+            res[layout] = gpu.moe_routed_device(b, X, W, None, K, prec=prec, inter=I)
+        finally:
+            b.free()
+    r, t = res[gpu.K3D_LAYOUT_ROWS], res[gpu.K3D_LAYOUT_TILED]
+    for a, b in zip(r, t):
+        assert np.array_equal(np.asarray(a), np.asarray(b))
+    out, idx, wt, perm, off, drops = r
+    assert np.array_equal(idx, idx0)
+    p2, off2 = stable_gather(idx0, N)
+    assert np.array_equal(perm, p2) and np.array_equal(off, off2)
+    assert drops == int((idx == victim).sum()) >= 1
+    for tk in range(T):
+        acc = np.zeros(E, np.float32)
+        for j in range(K):
+            e = int(idx[tk, j])
+            if e == victim:
+                continue
+            acc = acc + np.float32(wt[tk, j]) * orc.expert_ffn(X[tk], bank[e], E, I, act=1, wt=1.0)
+        if prec == 0:
+            assert max_err_rel_inf(out[tk], acc) <= TOL, tk
+        else:
+            assert np.linalg.norm(out[tk] - acc) / np.linalg.norm(acc) <= TOL_BF16, tk
+
+
 def test_moe_device_tiled_decode_golden(gpu, wl, gold):
     """Full decode shape (7168 x 2048, 384 experts, top-8) from a tiled bank: the reference's
     golden routing and outputs for 8 tokens."""
