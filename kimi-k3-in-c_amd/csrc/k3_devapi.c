@@ -223,7 +223,8 @@ static size_t router_layout(Carve *c, RtWs *w, int T, int hidden, int n_experts)
 {
     w->chunk = k3k_router_chunk(T, hidden, n_experts);
     const size_t ks = (size_t)((hidden + w->chunk - 1) / w->chunk);
-    w->part = (double *)take(c, ks * T * n_experts * 8);
+    /* chunk partials, or (a few tokens) one 16-byte scored record per logit */
+    w->part = (double *)take(c, (ks < 2 ? 2 : ks) * T * n_experts * 8);
     w->rbound = (float *)take(c, ks * T * n_experts * 4);
     w->nrecomp = (int *)take(c, (size_t)T * 4);
     return c->off;
@@ -243,7 +244,7 @@ static int router_run(int *idx, float *wt, const float *x, int T, const float *W
     const K3kExc *exc;
     int rc = exc_table(&exc);
     if (rc) return rc;
-    if (k3k_router_partial(w->part, w->rbound, x, T, W, hidden, n_experts, w->chunk, stream))
+    if (k3k_router_partial(w->part, w->rbound, x, T, W, hidden, n_experts, w->chunk, exc, stream))
         return fail("router_partial");
     if (k3k_router_final(idx, wt, w->nrecomp, w->part, w->rbound, w->chunk, x, W, bias, T, hidden,
                          n_experts, topk, renorm, routed_scale, exc, stream))

@@ -360,11 +360,209 @@ __device__ __forceinline__ void round_interval(float f, double &lo, double &hi)
     hi = isinf(up) ? 0x1.ffffffp+127 : 0.5 * ((double)f + (double)up);
 }
 
+/* The certification of a logit from its chunk sums (S = Q, the sum of P_k in k order, and
+ * bs, the sum of C_k |Q_k| + 2 R_k + |Q_{k+1}|): with u = 2^-53, B = 1.01 u bs + 4u|S|
+ * bounds |S - a_n| (the reference's chain). If every value in [S - B, S + B] rounds to the
+ * same float, that float is the logit (ok); otherwise scmax is the score of the largest
+ * float the logit can be. Non-finite sums come from inf/NaN inputs and propagate alike in
+ * any order (ok). */
+struct Certified {
+    float sc, scmax;
+    bool ok;
+};
+
+__device__ __forceinline__ Certified certify_score(double Q, double bs, const ExcTable &exc)
+{
+    const float f = (float)Q;
+    bool ok = true;
+    float fhi = f;
+    if (fabs(Q) <= 0x1.fffffffffffffp+1023) {
+        const double B = 1.01 * 0x1p-53 * bs + 4.0 * 0x1p-53 * fabs(Q) + 0x1p-1060;
+        double mlo, mhi;
+        round_interval(f, mlo, mhi);
+        ok = (Q - B > mlo) && (Q + B < mhi);
+        if (!ok) {
+            const float hb = (float)(Q + B);
+            fhi = fabsf(hb) <= 0x1.fffffep+127f ? next_float(hb, true) : hb;
+        }
+    }
+    Certified r;
+    r.sc = router_score(f, exc);
+    r.ok = ok;
+    r.scmax = ok ? r.sc : router_score(fhi, exc);
+    return r;
+}
+
+/* Router logits of a few tokens (T <= RS_T, hidden <= 64 * RS_CH), certified and scored in
+ * one kernel: a wave per expert, lane k runs the chain of 128-column chunk k for every
+ * token (as router_partial_small_kernel), then one lane per token sums the lanes' partials
+ * in k order, certifies (certify_score) and stores pre[t][e] = {score, score of the upper
+ * end, uncertified ? 1 : 0, 0}.
+ * W is read in full 128-byte lines: for 32-column sub-block sb, lane l loads columns
+ * 4(l % 8).. of sub-block sb of chunks l / 8 + 8j (j < 8), and a per-wave LDS buffer turns
+ * that into one chunk per lane. The tokens are staged once, rows padded to ks * RS_CH.
+ * In both LDS layouts a chunk's 16-byte group q sits at group (q + k) mod (its groups), so
+ * the lanes' 16-byte reads of their own chunks fall on distinct banks. */
+template <int NT>
+__global__ __launch_bounds__(256) void router_small_kernel(float4 *pre, const float *x, int T,
+                                                           const float *W, int hidden,
+                                                           int n_experts, int vec, ExcTable exc)
+{
+    extern __shared__ __attribute__((aligned(16))) float xsf[];   /* [T][ks * RS_CH] */
+    __shared__ __attribute__((aligned(16))) float wsh[4][64 * 32]; /* per wave: 64 chunks x 32 */
+    __shared__ double psh[4][NT][64];
+    __shared__ float rsh[4][NT][64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int e = blockIdx.x * 4 + wv;
+    const int ks = (hidden + RS_CH - 1) / RS_CH;
+    const int kb0 = lane * RS_CH, len = max(0, min(RS_CH, hidden - kb0));
+    const float *wr = W + (size_t)min(e, n_experts - 1) * hidden;
+    /* W loads: sub-block sb, j: chunk l / 8 + 8j, columns 4(l % 8)..4(l % 8) + 3 */
+    float4 wl[4][8];
+    const int lq = lane & 7, lk = lane >> 3;
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int col = (lk + 8 * j) * RS_CH + sb * 32 + 4 * lq;
+            if (vec && col + 3 < hidden)
+                wl[sb][j] = *reinterpret_cast<const float4 *>(wr + col);
+            else
+                wl[sb][j] = make_float4(col < hidden ? wr[col] : 0.f, col + 1 < hidden ? wr[col + 1] : 0.f,
+                                        col + 2 < hidden ? wr[col + 2] : 0.f, col + 3 < hidden ? wr[col + 3] : 0.f);
+        }
+    /* stage the tokens: eight loads per thread in flight, then the stores */
+    const int rowp = ks * RS_CH;
+    auto slot = [&](int t, int col) {
+        const int k = col / RS_CH, j = col % RS_CH;
+        return t * rowp + k * RS_CH + ((j + 4 * k) & (RS_CH - 1));
+    };
+    if (vec) {
+        const int nq = T * hidden / 4, rq = hidden / 4;
+        for (int i0 = 0; i0 < nq; i0 += 256 * 8) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + tid + 256 * j;
+                v[j] = i < nq ? reinterpret_cast<const float4 *>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + tid + 256 * j;
+                if (i < nq) *reinterpret_cast<float4 *>(&xsf[slot(i / rq, 4 * (i % rq))]) = v[j];
+            }
+        }
+    } else {
+        const int n = T * hidden;
+        for (int i0 = 0; i0 < n; i0 += 256 * 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + tid + 256 * j;
+                v[j] = i < n ? x[i] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + tid + 256 * j;
+                if (i < n) xsf[slot(i / hidden, i % hidden)] = v[j];
+            }
+        }
+    }
+    __syncthreads();
+    double acc[NT], rb[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) { acc[t] = 0.0; rb[t] = 0.0; }
+    float *wb = wsh[wv];
+    const int xk = lane < ks ? kb0 : 0;             /* lanes past the last chunk read chunk 0 */
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++) {
+        /* this sub-block of every chunk through the wave's buffer: chunk k at 32 k, group q
+         * of it at (q + k) mod 8 */
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k = lk + 8 * j;
+            *reinterpret_cast<float4 *>(&wb[k * 32 + 4 * ((lq + k) & 7)]) = wl[sb][j];
+        }
+        __builtin_amdgcn_wave_barrier();
+        float4 wq[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) wq[q] = *reinterpret_cast<const float4 *>(&wb[lane * 32 + 4 * ((q + lane) & 7)]);
+        __builtin_amdgcn_wave_barrier();
+        float wn = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            wn += fabsf(wq[q].x) + fabsf(wq[q].y) + fabsf(wq[q].z) + fabsf(wq[q].w);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t >= T) break;
+            float xv[32];
+            float xm = 0.0f;
+#pragma unroll
+            for (int j4 = 0; j4 < 8; j4++) {
+                const int k = sb * 32 + 4 * j4;
+                const float4 v = *reinterpret_cast<const float4 *>(&xsf[t * rowp + xk + ((k + 4 * lane) & (RS_CH - 1))]);
+                xv[4 * j4] = k < len ? v.x : 0.0f;
+                xv[4 * j4 + 1] = k + 1 < len ? v.y : 0.0f;
+                xv[4 * j4 + 2] = k + 2 < len ? v.z : 0.0f;
+                xv[4 * j4 + 3] = k + 3 < len ? v.w : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 32; j++) xm = fmaxf(xm, fabsf(xv[j]));
+            rb[t] = fma(32.0, fabs(acc[t]) + (double)wn * (double)xm, rb[t]);
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                acc[t] = fma((double)wq[q].x, (double)xv[4 * q], acc[t]);
+                acc[t] = fma((double)wq[q].y, (double)xv[4 * q + 1], acc[t]);
+                acc[t] = fma((double)wq[q].z, (double)xv[4 * q + 2], acc[t]);
+                acc[t] = fma((double)wq[q].w, (double)xv[4 * q + 3], acc[t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        psh[wv][t][lane] = acc[t];
+        /* rounded up: the float sums of |w| carry at most a 2^-18 relative error */
+        rsh[wv][t][lane] = (float)(rb[t] * (1.0 + 0x1p-17)) * (1.0f + 0x1p-20f);
+    }
+    __syncthreads();
+    if (lane < T && e < n_experts) {
+        const int t = lane;
+        double pv[64];
+        float rv[64];
+#pragma unroll
+        for (int k = 0; k < 64; k++) {
+            pv[k] = psh[wv][t][k];
+            rv[k] = rsh[wv][t][k];
+        }
+        /* Q_{k+1} = Q_k + P_k in k order (the rounding the bound describes); bs, the sum of
+         * C_k |Q_k| + 2 R_k + |Q_{k+1}|, only bounds and is added in any order (its own
+         * relative error, under 2^-45, is far inside the bound's 1% slack) */
+        double qk[65];
+        qk[0] = 0.0;
+#pragma unroll
+        for (int k = 0; k < 64; k++) qk[k + 1] = k < ks ? qk[k] + pv[k] : qk[k];
+        double term[64];
+#pragma unroll
+        for (int k = 0; k < 64; k++) {
+            const int ck = min(RS_CH, hidden - k * RS_CH);
+            term[k] = k < ks ? fma((double)ck, fabs(qk[k]), fma(2.0, (double)rv[k], fabs(qk[k + 1]))) : 0.0;
+        }
+#pragma unroll
+        for (int w = 32; w > 0; w >>= 1)
+#pragma unroll
+            for (int k = 0; k < w; k++) term[k] += term[k + w];
+        const Certified cs = certify_score(qk[64], term[0], exc);
+        pre[(size_t)t * n_experts + e] = make_float4(cs.sc, cs.scmax, cs.ok ? 0.0f : 1.0f, 0.0f);
+    }
+}
+
 /* One workgroup per token, one lane per expert (SL experts per lane past 1024): certify
- * the logit, score, then topk rounds of the reference's rule -- largest choice, lowest
- * index among equals, strictly above -inf, none left: idx 0, weight 0 (k3_ops.c:459-467)
- * -- with a wave argmax and one barrier per round; recompute what matters and repeat;
- * renormalise and scale (k3_ops.c:469-475). nrecomp[t] (optional) counts recomputes. */
+ * the logit, score, then the reference's rule topk times -- largest choice, lowest index
+ * among equals, strictly above -inf, none left: idx 0, weight 0 (k3_ops.c:459-467) -- as
+ * topk extractions of a wave maximum (DPP) per wave, then over the waves' candidates in
+ * wave 0, one barrier between; recompute what matters and repeat; renormalise and scale
+ * (k3_ops.c:469-475). nrecomp[t] (optional) counts recomputes. KB: chunk partials loaded
+ * per batch (64 for up to 512 experts, one batch at decode sizes). */
 constexpr int RF_MAXE = 2048, RF_MAXW = 16, RF_KB = 32;
 
 /* unsigned order of a non-NaN float that matches its numeric order (-0 as +0) */
@@ -374,46 +572,42 @@ __device__ __forceinline__ uint32_t choice_order(float v)
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o)
+/* 32-bit max / min of the wave by DPP, the same in every lane: pairs, quads (quad_perm),
+ * 8 (row half mirror), 16 (row mirror), then rows 0-1 and 2-3 (row_bcast15 into rows 1,
+ * 3) and rows 0-3 (row_bcast31 into rows 2, 3), so lane 63 holds the result. */
+/* (rows outside RM read the identity of the operation, so each step is one DPP max/min) */
+template <int CTRL, int RM, uint32_t ID>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v)
 {
-    const uint32_t lo = __shfl_xor((uint32_t)v, o, 64), hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)ID, (int)v, CTRL, RM, 0xf, false);
+}
+
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v)
+{
+    constexpr uint32_t ID = MAX ? 0u : 0xffffffffu;
+    auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    v = op(v, dpp_u32<0xB1, 0xf, ID>(v));      /* quad_perm [1,0,3,2] */
+    v = op(v, dpp_u32<0x4E, 0xf, ID>(v));      /* quad_perm [2,3,0,1] */
+    v = op(v, dpp_u32<0x141, 0xf, ID>(v));     /* row_half_mirror */
+    v = op(v, dpp_u32<0x140, 0xf, ID>(v));     /* row_mirror */
+    v = op(v, dpp_u32<0x142, 0xa, ID>(v));     /* row_bcast15 */
+    v = op(v, dpp_u32<0x143, 0xc, ID>(v));     /* row_bcast31 */
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+/* Selection key (order-preserving bits of the choice) << 32 | ~expert: the largest key is
+ * the largest choice, then the lowest expert. The wave's largest key, in every lane: the
+ * largest high word, then the largest low word among the lanes holding it. */
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k)
+{
+    const uint32_t hi = wave_reduce_u32<true>((uint32_t)(k >> 32));
+    const uint32_t lo = wave_reduce_u32<true>((uint32_t)(k >> 32) == hi ? (uint32_t)k : 0u);
     return ((uint64_t)hi << 32) | lo;
 }
 
-/* bitonic sort of one key per lane across the wave, descending (lane 0 the largest) */
-__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane)
-{
-#pragma unroll
-    for (int sz = 2; sz <= 64; sz <<= 1)
-#pragma unroll
-        for (int j = sz >> 1; j > 0; j >>= 1) {
-            const uint64_t o = shfl_xor64(k, j);
-            const bool first = (lane & j) == 0;          /* lower lane of the pair */
-            const bool desc = (lane & sz) == 0;          /* this block sorts descending */
-            const bool take_max = first == desc;
-            k = take_max ? (k > o ? k : o) : (k < o ? k : o);
-        }
-    return k;
-}
-
-/* two descending lists a, b across the wave -> the 64 largest of their union, descending */
-__device__ __forceinline__ uint64_t wave_merge_desc(uint64_t a, uint64_t b, int lane)
-{
-    /* reverse b and keep the pairwise max: a bitonic sequence holding the top 64 */
-    const uint64_t br = ((uint64_t)__shfl((uint32_t)(b >> 32), 63 - lane, 64) << 32) |
-                        (uint64_t)__shfl((uint32_t)b, 63 - lane, 64);
-    uint64_t k = a > br ? a : br;
-#pragma unroll
-    for (int j = 32; j > 0; j >>= 1) {
-        const uint64_t o = shfl_xor64(k, j);
-        const bool first = (lane & j) == 0;
-        k = first ? (k > o ? k : o) : (k < o ? k : o);
-    }
-    return k;
-}
-
-template <int SL>
-__global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt, int *nrecomp,
+template <int SL, int KB, bool PRE>
+__global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int *idx, float *wt, int *nrecomp,
                                                             const double *part,
                                                             const float *rbound, int ksplit,
                                                             int chunk, const float *x,
@@ -439,21 +633,32 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
         cmax[i] = -INFINITY;
         sc[i] = 0.0f;
         unc[i] = false;
-        if (e < n_experts) {
+        if (e < n_experts && PRE) {
+            /* scored by router_small_kernel: {score, score of the upper end, uncertified} */
+            const float4 pr = reinterpret_cast<const float4 *>(part)[(size_t)t * n_experts + e];
+            sc[i] = pr.x;
+            const float bb = bias ? bias[e] : 0.0f;
+            c[i] = sc[i] + bb;
+            cmax[i] = c[i];
+            if (pr.z != 0.0f) {
+                unc[i] = true;
+                cmax[i] = pr.y + bb;
+            }
+        } else if (e < n_experts) {
             double Q = 0.0, bs = 0.0;
-            for (int k0 = 0; k0 < ksplit; k0 += RF_KB) {
+            for (int k0 = 0; k0 < ksplit; k0 += KB) {
                 /* one batch of chunk loads in flight together */
-                double pv[RF_KB];
-                float rv[RF_KB];
+                double pv[KB];
+                float rv[KB];
 #pragma unroll
-                for (int kk = 0; kk < RF_KB; kk++) {
+                for (int kk = 0; kk < KB; kk++) {
                     const int k = min(k0 + kk, ksplit - 1);
                     const size_t o = ((size_t)k * T + t) * n_experts + e;
                     pv[kk] = part[o];
                     rv[kk] = rbound[o];
                 }
 #pragma unroll
-                for (int kk = 0; kk < RF_KB; kk++) {
+                for (int kk = 0; kk < KB; kk++) {
                     const int k = k0 + kk;
                     if (k < ksplit) {
                         const int ck = min(chunk, hidden - k * chunk);
@@ -463,27 +668,14 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
                     }
                 }
             }
-            const float f = (float)Q;
-            /* non-finite sums come from inf/NaN inputs and propagate alike in any order */
-            bool ok = true;
-            float fhi = f;
-            if (fabs(Q) <= 0x1.fffffffffffffp+1023) {
-                const double B = 1.01 * 0x1p-53 * bs + 4.0 * 0x1p-53 * fabs(Q) + 0x1p-1060;
-                double mlo, mhi;
-                round_interval(f, mlo, mhi);
-                ok = (Q - B > mlo) && (Q + B < mhi);
-                if (!ok) {
-                    const float hb = (float)(Q + B);
-                    fhi = fabsf(hb) <= 0x1.fffffep+127f ? next_float(hb, true) : hb;
-                }
-            }
-            sc[i] = router_score(f, exc);
+            const Certified cs = certify_score(Q, bs, exc);
+            sc[i] = cs.sc;
             const float bb = bias ? bias[e] : 0.0f;
             c[i] = sc[i] + bb;
             cmax[i] = c[i];
-            if (!ok) {
+            if (!cs.ok) {
                 unc[i] = true;
-                cmax[i] = router_score(fhi, exc) + bb;      /* choice is monotone in logit */
+                cmax[i] = cs.scmax + bb;                    /* choice is monotone in logit */
             }
         }
     }
@@ -502,29 +694,30 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
                          ? ((uint64_t)choice_order(c[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e)
                          : 0ull;
         }
-        /* 1. each wave sorts its keys (descending, across lanes; SL > 1: lane-local first) */
-        uint64_t kw = key[0];
+        /* 1. each wave extracts its topk largest keys, largest first (topk rounds of a
+         *    wave max; a key taken is zeroed); 2. wave 0 does the same over the waves'
+         *    candidates. Keys are distinct (the expert index is part of the key). */
+        for (int j = 0; j < topk; j++) {
+            uint64_t b = key[0];
 #pragma unroll
-        for (int i = 1; i < SL; i++) kw = kw > key[i] ? kw : key[i];
-        /* SL == 2 (past 1024 experts): the second key of each lane joins by a second sort */
-        kw = wave_sort_desc(kw, lane);
-        if (SL == 2) {
-            uint64_t k2 = key[0] < key[1] ? key[0] : key[1];
-            k2 = wave_sort_desc(k2, lane);
-            /* merge two descending lists: lane l keeps the l-th largest of their union */
-            kw = wave_merge_desc(kw, k2, lane);
+            for (int i = 1; i < SL; i++) b = b > key[i] ? b : key[i];
+            const uint64_t m = wave_max_key(b);
+#pragma unroll
+            for (int i = 0; i < SL; i++)
+                if (key[i] == m) key[i] = 0ull;
+            if (lane == 0) candk[wv][j] = m;
         }
-        if (lane < topk) candk[wv][lane] = kw;
         __syncthreads();
-        /* 2. wave 0 merges the waves' top-k lists */
         if (wv == 0) {
             const int ncand = nw * topk;
             if (ncand <= 64) {
-                uint64_t m = lane < ncand ? candk[lane / topk][lane % topk] : 0ull;
-                m = wave_sort_desc(m, lane);
-                if (lane < topk) selk[lane] = m;
+                uint64_t mk = lane < ncand ? candk[lane / topk][lane % topk] : 0ull;
+                for (int j = 0; j < topk; j++) {
+                    const uint64_t m = wave_max_key(mk);
+                    if (mk == m) mk = 0ull;
+                    if (lane == 0) selk[j] = m;
+                }
             } else {
-                /* up to 16 candidates per lane; topk rounds of a wave max */
                 uint64_t mk[RF_MAXW];
 #pragma unroll
                 for (int q = 0; q < RF_MAXW; q++) {
@@ -535,18 +728,11 @@ __global__ __launch_bounds__(1024) void router_final_kernel(int *idx, float *wt,
                     uint64_t b = 0ull;
 #pragma unroll
                     for (int q = 0; q < RF_MAXW; q++) b = b > mk[q] ? b : mk[q];
-                    const uint64_t mine = b;
+                    const uint64_t m = wave_max_key(b);
 #pragma unroll
-                    for (int o = 1; o < 64; o <<= 1) {
-                        const uint64_t ob = shfl_xor64(b, o);
-                        b = b > ob ? b : ob;
-                    }
-                    if (b != 0ull && mine == b) {
-#pragma unroll
-                        for (int q = 0; q < RF_MAXW; q++)
-                            if (mk[q] == b) mk[q] = 0ull;
-                    }
-                    if (lane == 0) selk[j] = b;
+                    for (int q = 0; q < RF_MAXW; q++)
+                        if (mk[q] == m) mk[q] = 0ull;
+                    if (lane == 0) selk[j] = m;
                 }
             }
         }
@@ -888,16 +1074,64 @@ extern "C" int k3k_router_chunk(int T, int hidden, int n_experts)
     return chunk;
 }
 
+/* Up to RS_T tokens and 64 chunks of RS_CH columns whose staged rows fit in LDS beside
+ * the kernel's own 45 KB: router_small_kernel certifies and scores the logits itself, and
+ * the final kernel starts from its records. */
+constexpr size_t RS_LDS_DYN = 160 * 1024 - 45 * 1024;
+
+static bool router_small_mode(int T, int hidden)
+{
+    const size_t ks = (size_t)(hidden + RS_CH - 1) / RS_CH;
+    return T <= RS_T && ks <= 64 && (size_t)T * ks * RS_CH * 4 <= RS_LDS_DYN;
+}
+
+static ExcTable exc_view(const K3kExc *exc)
+{
+    ExcTable e;
+    memset(&e, 0, sizeof e);
+    if (exc) {
+        e.pairs = exc->pairs;
+        e.index = exc->index;
+        e.bits = exc->bits;
+        e.kmin = exc->kmin;
+        e.kmax = exc->kmax;
+        e.base = exc->base;
+        e.mmin = exc->mmin;
+        e.mwords = exc->mwords;
+        e.n = exc->n;
+    }
+    return e;
+}
+
 extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, int T,
                                   const float *W, int hidden, int n_experts, int chunk,
-                                  void *stream)
+                                  const K3kExc *exc, void *stream)
 {
     if (T <= 0 || n_experts <= 0) return 0;
     if (chunk <= 0 || chunk % RP_KS) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
     const int ks = (hidden + chunk - 1) / chunk;
     const int vec = (hidden % 4 == 0) && ((((uintptr_t)x) | ((uintptr_t)W)) % 16 == 0);
     hipStream_t st = (hipStream_t)stream;
-    if (T <= RS_T) {
+    if (router_small_mode(T, hidden)) {
+        if (chunk != RS_CH) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
+        const size_t lds = (size_t)T * ks * RS_CH * 4;
+        const ExcTable e = exc_view(exc);
+        float4 *pre = reinterpret_cast<float4 *>(part);
+        const dim3 grid((n_experts + 3) / 4);
+        if (T == 1) {
+            hipLaunchKernelGGL(router_small_kernel<1>, grid, dim3(256), lds, st, pre, x, T, W, hidden,
+                               n_experts, vec, e);
+        } else {
+            static bool attr = false;
+            if (!attr) {
+                (void)hipFuncSetAttribute(reinterpret_cast<const void *>(router_small_kernel<RS_T>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)RS_LDS_DYN);
+                attr = true;
+            }
+            hipLaunchKernelGGL(router_small_kernel<RS_T>, grid, dim3(256), lds, st, pre, x, T, W,
+                               hidden, n_experts, vec, e);
+        }
+    } else if (T <= RS_T) {
         if (chunk != RS_CH) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
         dim3 grid((n_experts + 255) / 256, ks);
         if (T == 1)
@@ -923,31 +1157,34 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
     if (T <= 0) return 0;
     if (n_experts > RF_MAXE || topk > 64)
         return k3k_fail("router_final: n_experts or topk too large", hipErrorInvalidValue);
-    ExcTable e;
-    memset(&e, 0, sizeof e);
-    if (exc) {
-        e.pairs = exc->pairs;
-        e.index = exc->index;
-        e.bits = exc->bits;
-        e.kmin = exc->kmin;
-        e.kmax = exc->kmax;
-        e.base = exc->base;
-        e.mmin = exc->mmin;
-        e.mwords = exc->mwords;
-        e.n = exc->n;
-    }
+    const ExcTable e = exc_view(exc);
     const int ks = (hidden + chunk - 1) / chunk;
     int nw = (n_experts + 63) / 64;
     if (nw > RF_MAXW) nw = RF_MAXW;
     hipStream_t st = (hipStream_t)stream;
-    if (n_experts <= 64 * RF_MAXW)
-        hipLaunchKernelGGL(router_final_kernel<1>, dim3(T), dim3(64 * nw), 0, st, idx, wt, nrecomp,
-                           part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm,
-                           routed_scale, e);
+    /* scored records (a few tokens), else the chunk partials: up to 512 experts (<= 8
+     * waves) in one batch of up to 64 loads */
+    const bool pre = router_small_mode(T, hidden);
+    if (pre && n_experts <= 64 * RF_MAXW)
+        hipLaunchKernelGGL((router_final_kernel<1, RF_KB, true>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
+                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
+                           renorm, routed_scale, e);
+    else if (pre)
+        hipLaunchKernelGGL((router_final_kernel<2, RF_KB, true>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
+                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
+                           renorm, routed_scale, e);
+    else if (n_experts <= 512 && ks <= 64)
+        hipLaunchKernelGGL((router_final_kernel<1, 64, false>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
+                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
+                           renorm, routed_scale, e);
+    else if (n_experts <= 64 * RF_MAXW)
+        hipLaunchKernelGGL((router_final_kernel<1, RF_KB, false>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
+                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
+                           renorm, routed_scale, e);
     else
-        hipLaunchKernelGGL(router_final_kernel<2>, dim3(T), dim3(64 * nw), 0, st, idx, wt, nrecomp,
-                           part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm,
-                           routed_scale, e);
+        hipLaunchKernelGGL((router_final_kernel<2, RF_KB, false>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
+                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
+                           renorm, routed_scale, e);
     K3K_LAUNCH_CHECK("router_final launch");
     return 0;
 }

@@ -152,7 +152,7 @@ typedef struct {
  * receives the number of recomputed logits per token. */
 int k3k_router_chunk(int T, int hidden, int n_experts);
 int k3k_router_partial(double *part, float *rbound, const float *x, int T, const float *W,
-                       int hidden, int n_experts, int chunk, void *stream);
+                       int hidden, int n_experts, int chunk, const K3kExc *exc, void *stream);
 int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, const float *rbound,
                      int chunk, const float *x, const float *W, const float *bias, int T,
                      int hidden, int n_experts, int topk, int renorm, float routed_scale,
