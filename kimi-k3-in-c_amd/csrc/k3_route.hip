@@ -1162,8 +1162,9 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
     int nw = (n_experts + 63) / 64;
     if (nw > RF_MAXW) nw = RF_MAXW;
     hipStream_t st = (hipStream_t)stream;
-    /* scored records (a few tokens), else the chunk partials: up to 512 experts (<= 8
-     * waves) in one batch of up to 64 loads */
+    /* scored records (a few tokens), else the chunk partials: for up to 64 tokens and 512
+     * experts (<= 8 waves) in one batch of up to 64 loads (more registers, fewer waves per
+     * CU: only while the tokens do not fill the chip) */
     const bool pre = router_small_mode(T, hidden);
     if (pre && n_experts <= 64 * RF_MAXW)
         hipLaunchKernelGGL((router_final_kernel<1, RF_KB, true>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
@@ -1173,7 +1174,7 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
         hipLaunchKernelGGL((router_final_kernel<2, RF_KB, true>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
                            nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
                            renorm, routed_scale, e);
-    else if (n_experts <= 512 && ks <= 64)
+    else if (n_experts <= 512 && ks <= 64 && T <= 64)
         hipLaunchKernelGGL((router_final_kernel<1, 64, false>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
                            nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
                            renorm, routed_scale, e);
