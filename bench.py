@@ -151,6 +151,52 @@ def time_prefill(layer, T=4096, steps=3, warmup=1):
             "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st.items()}}
 
 
+def time_expert_ffn(layer, per_graph=16, reps=20):
+    """One routed expert SwiGLU FFN at decode (config 1): one token, gate/up/down out of the
+    resident tiled bank, combine weight 0.125, through k3d_moe_experts with one assignment
+    (the decode path). A HIP graph holds per_graph calls on per_graph different experts; the
+    graph is replayed reps times, each replay on the next experts, so weights come from HBM."""
+    L = k3amd.lib()
+    x = k3amd.DevBuf(E * 4).upload(wl.expert_input())
+    out = k3amd.DevBuf(E * 4)
+    ids = np.arange(N, dtype=np.int32)
+    idx = k3amd.DevBuf(N * 4).upload(ids)
+    wt = k3amd.DevBuf(4).upload(np.array([0.125], np.float32))
+    ws = k3amd.DevBuf(L.k3d_moe_ws(1, E, I, N, 1, 0))
+    stream = L.k3d_stream_create()
+    ngraph = N // per_graph
+    graphs = []
+    for gi in range(ngraph):
+        k3amd.check(L.k3d_graph_begin(stream), "k3d_graph_begin")
+        for c in range(per_graph):
+            e = gi * per_graph + c
+            k3amd.check(L.k3d_moe_experts(out.ptr, idx.ptr + 4 * e, wt.ptr, x.ptr, 1, layer.bank.table.ptr,
+                                          layer.layout, E, I, N, 1, k3amd.K3_ACT_SILU, 4.0, 25.0, 0,
+                                          ws.ptr, ws.nbytes, None, None, None, stream), "k3d_moe_experts")
+        ex = C.c_void_p()
+        k3amd.check(L.k3d_graph_end(stream, C.byref(ex)), "k3d_graph_end")
+        graphs.append(ex)
+    for g in graphs[:2]:
+        k3amd.check(L.k3d_graph_launch(g, stream), "k3d_graph_launch")
+    k3amd.check(L.k3d_sync(stream))
+    t0 = time.perf_counter()
+    for r in range(reps):
+        k3amd.check(L.k3d_graph_launch(graphs[r % ngraph], stream), "k3d_graph_launch")
+    k3amd.check(L.k3d_sync(stream))
+    t1 = time.perf_counter()
+    for g in graphs:
+        L.k3d_graph_destroy(g)
+    L.k3d_stream_destroy(stream)
+    for b in (x, out, idx, wt, ws):
+        b.free()
+    us = (t1 - t0) / (reps * per_graph) * 1e6
+    algo = EXPERT_BYTES + 2 * E * 4
+    return {"tokens": 1, "experts_rotated": N, "us_per_call": round(us, 2),
+            "tokens_per_s": round(1e6 / us, 1), "algorithmic_bytes": algo,
+            "GBps": round(algo / (us * 1e-6) / 1e9, 1),
+            "frac_of_peak": round(algo / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+
+
 def time_skewed(layer, T=512, steps=5, warmup=1):
     """Skewed routing + dense trunk (config 4): T tokens, router selection bias giving
     Zipf(1.2)-like expert popularity, routed experts with bf16 activations, then the
@@ -333,6 +379,8 @@ def main():
     log(f"bench: batch-1 layer {b1_ms:.3f} ms/step")
     gemv = time_gemv()
     log(f"bench: gemv {gemv}")
+    ffn = time_expert_ffn(layer)
+    log(f"bench: expert ffn {ffn}")
     prefill = time_prefill(layer)
     log(f"bench: prefill {prefill}")
     skewed = time_skewed(layer)
@@ -367,6 +415,7 @@ def main():
                    "layer_GBps": round(b1_bytes / (b1_ms * 1e-3) / 1e9, 1),
                    "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st1.items()}},
         "gemv_2048x7168": gemv,
+        "expert_ffn_decode": ffn,
         "prefill_4096": prefill,
         "skewed_512_shared": skewed,
     }

@@ -435,24 +435,28 @@ __global__ __launch_bounds__(1024) void mx_gemv_small_kernel(K3kMxArgs a, int kw
 
 /* ---- decode of a few assignments ------------------------------------------------------
  * mx_decode_kernel: GATEUP / DOWN when the batch has at most 16 assignments (T * topk),
- * straight from the router's idx, without the gather. Item = (assignment a, 4 tiles of 16
- * rows), one workgroup of 4 * KS waves: wave w takes tile w % 4 and the K share w / 4 of
- * the KS equal shares of 512-column chunks, and streams it with two chunks of weights in
- * flight. The workgroup stages the activations once (GATEUP: token a / topk from fp32,
- * split in-kernel; DOWN: assignment a's bf16 terms) plus a 1 KB block of zeros: lanes of
- * token columns > 0 read the zeros, so the B operands need no masking. The K shares are
- * added in order, then GATEUP writes act(gate, up) of assignment a as bf16 terms and DOWN
- * writes contrib[a]. A dropped expert (NULL weights) is skipped; the combine leaves it
- * out. GATEUP's block 0 stores the number of dropped assignments in *a.drops. */
-template <int MODE, int NS, int LAYOUT, int KS>
-__global__ __launch_bounds__(256 * KS) void mx_decode_kernel(K3kMxArgs a)
+ * straight from the router's idx, without the gather. Item = (assignment a, TPW tiles of
+ * 16 rows), one workgroup each; its TPW * ks waves (ks = blockDim / (64 TPW)): wave w takes
+ * tile w % TPW and the K share w / TPW of the ks equal shares of 512-column chunks, and
+ * streams it with two chunks of weights in flight. (4 tiles x 2 shares when the
+ * assignments fill the chip; 1 tile x up to 16 shares for one or two assignments.) The
+ * workgroup stages the activations once (GATEUP: token a / topk from fp32, split
+ * in-kernel; DOWN: assignment a's bf16 terms) plus a 1 KB block of zeros: lanes of token
+ * columns > 0 read the zeros, so the B operands need no masking. The K shares are added
+ * in order, then GATEUP writes act(gate, up) of assignment a as bf16 terms and DOWN writes
+ * contrib[a]. A dropped expert (NULL weights) is skipped; the combine leaves it out.
+ * GATEUP's block 0 stores the number of dropped assignments in *a.drops. */
+template <int MODE, int NS, int LAYOUT, int TPW>
+__global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* [NS][K], zeros[512] */
-    constexpr int TPW = 4, NM = MODE == K3K_MX_GATEUP ? 2 : 1;     /* gate + up, or down */
-    constexpr int XPT = 16 / KS;                                   /* K <= 8192 */
+    constexpr int NM = MODE == K3K_MX_GATEUP ? 2 : 1;              /* gate + up, or down */
+    /* activation pieces per thread: K <= 8192, the host keeps 64 TPW ks XPT >= 2048 */
+    constexpr int XPT = TPW == 4 ? 4 : 8;
     constexpr int WPOL = LAYOUT == 1 ? K3_LD_NT : K3_LD_DEFAULT;
     const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KS = nthr / (64 * TPW);
     const int r16 = lane & 15, g = lane >> 4;
     const int K = a.K, nblk = K >> 5, rows = a.rows, ntile = (rows + 15) >> 4, nchunk = K >> 9;
     const int ngrp = (ntile + TPW - 1) / TPW;
@@ -599,7 +603,6 @@ __global__ __launch_bounds__(256 * KS) void mx_decode_kernel(K3kMxArgs a)
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             sum[m] = acc[m][0] + acc[m][1];
-#pragma unroll
             for (int k2 = 1; k2 < KS; k2++) sum[m] += red[(((k2 - 1) * TPW + wv % TPW) * NM + m) * 64 + lane];
         }
         const int base = tw * 16 + 4 * g;
@@ -1400,20 +1403,31 @@ extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
         (mode == K3K_MX_GATEUP && (uintptr_t)a->xf32 % 16) ||
         (size_t)((a->rows + 15) / 16 * 16) * (a->K / 2) >= 0x80000000u)
         return k3k_fail("mx_decode: shape", hipErrorInvalidValue);
-    /* K split over two waves per tile (measured best for both gate/up and down) */
-    const int nm = mode == K3K_MX_GATEUP ? 2 : 1, ks = 2;
+    /* 4 tiles per workgroup, K over 2 waves per tile, when that gives >= 256 workgroups;
+     * otherwise (one or two assignments) 1 tile per workgroup, K over up to 16 waves
+     * (at least 4, which the activation staging needs) */
+    const int nm = mode == K3K_MX_GATEUP ? 2 : 1;
+    const int ntile = (a->rows + 15) / 16, nchunk = a->K / 512;
+    const bool wide = (long)a->n_assign * ((ntile + 3) / 4) >= 256 || nchunk < 4;
+    const int tpw = wide ? 4 : 1;
+    const int ks = wide ? 2 : (nchunk < 16 ? nchunk : 16);
     size_t lds = (size_t)a->nsplit * a->K * 2 + 1024;
-    if (lds < (size_t)(ks - 1) * 4 * nm * 1024) lds = (size_t)(ks - 1) * 4 * nm * 1024;
-    const int grid = a->n_assign * (((a->rows + 15) / 16 + 3) / 4);
+    if (lds < (size_t)(ks - 1) * tpw * nm * 1024) lds = (size_t)(ks - 1) * tpw * nm * 1024;
+    const int grid = a->n_assign * ((ntile + tpw - 1) / tpw);
     void (*kern)(K3kMxArgs);
     const bool ns2 = a->nsplit == 2, tiled = a->layout == 1;
-    if (mode == K3K_MX_GATEUP)
-        kern = tiled ? (ns2 ? mx_decode_kernel<K3K_MX_GATEUP, 2, 1, 2> : mx_decode_kernel<K3K_MX_GATEUP, 1, 1, 2>)
-                     : (ns2 ? mx_decode_kernel<K3K_MX_GATEUP, 2, 0, 2> : mx_decode_kernel<K3K_MX_GATEUP, 1, 0, 2>);
-    else
-        kern = tiled ? (ns2 ? mx_decode_kernel<K3K_MX_DOWN, 2, 1, 2> : mx_decode_kernel<K3K_MX_DOWN, 1, 1, 2>)
-                     : (ns2 ? mx_decode_kernel<K3K_MX_DOWN, 2, 0, 2> : mx_decode_kernel<K3K_MX_DOWN, 1, 0, 2>);
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256 * ks), lds, (hipStream_t)stream, *a);
+#define K3_DEC(MODE, TPW)                                                                          \
+    kern = tiled ? (ns2 ? mx_decode_kernel<MODE, 2, 1, TPW> : mx_decode_kernel<MODE, 1, 1, TPW>)     \
+                 : (ns2 ? mx_decode_kernel<MODE, 2, 0, TPW> : mx_decode_kernel<MODE, 1, 0, TPW>)
+    if (mode == K3K_MX_GATEUP) {
+        if (wide) K3_DEC(K3K_MX_GATEUP, 4);
+        else K3_DEC(K3K_MX_GATEUP, 1);
+    } else {
+        if (wide) K3_DEC(K3K_MX_DOWN, 4);
+        else K3_DEC(K3K_MX_DOWN, 1);
+    }
+#undef K3_DEC
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * tpw * ks), lds, (hipStream_t)stream, *a);
     K3K_LAUNCH_CHECK("mx_decode launch");
     return 0;
 }
