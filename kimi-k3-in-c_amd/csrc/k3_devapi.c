@@ -291,11 +291,13 @@ typedef struct {
  * (prefill). Other shapes run the register-fed kernel (16, row-major bank only). */
 /* Tokens per expert pass. 8 for decode (fp32-accurate, weight streaming), 16 when the
  * widths are not multiples of 512; one-term (prefill) activations take 32 from 8 tokens
- * per expert on average and, for a tiled bank, 48 from 32 tokens per expert. The row-major
- * choice is never larger than the tiled one, so it sizes the workspace for both. */
+ * per expert on average and, for a tiled bank, 48 from 32 and 96 from 64 tokens per
+ * expert. The row-major choice is never larger than the tiled one, so it sizes the
+ * workspace for both. */
 static int moe_pass_tok(int T, int hidden, int inter, int n_experts, int topk, int prec, int layout)
 {
     if (hidden % 512 || inter % 512) return 16;
+    if (prec == 1 && layout == K3D_LAYOUT_TILED && (long)T * topk >= 64L * n_experts) return 96;
     if (prec == 1 && layout == K3D_LAYOUT_TILED && (long)T * topk >= 32L * n_experts) return 48;
     if (prec == 1 && (long)T * topk >= 8L * n_experts) return 32;
     return 8;

@@ -927,17 +927,17 @@ int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
  * mx_prefill_kernel: GATEUP / DOWN for passes of up to 16*NB tokens with the activations
  * as single bf16 terms (the prefill precision), weights tiled MXFP4 (LAYOUT 1) or bf16
  * (LAYOUT 2). Same item = (pass, row block) and K order as mx_moe_kernel, but K is staged
- * 256 columns at a time so that up to 96 tokens fit in LDS: each expert's weights are
- * streamed once per pass of up to 16*NB tokens, and every dequantized weight fragment
- * feeds MT x NB MFMAs. Stage c covers steps 2(c&1) and 2(c&1)+1 of tiled 512-chunk c>>1.
+ * 128 * SPC columns at a time so that the pass's tokens fit in LDS: each expert's weights
+ * are streamed once per pass of up to 16*NB tokens, and every dequantized weight fragment
+ * feeds MT x NB MFMAs. Stage c covers steps c SPC .. c SPC + SPC - 1 (128 columns each).
  * Activation loads are unconditional (rows clamped to a valid token); only the LDS stores
  * are masked. Weight loads keep the default cache policy: an expert with several passes
  * re-reads its weights, and the caches then serve part of them. */
-template <int MODE, int MT, int NB, int LAYOUT>
+template <int MODE, int MT, int NB, int LAYOUT, int SPC = 2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void mx_prefill_kernel(K3kMxArgs a)
 {
-    constexpr int NW = 4, KC = 256, SPC = 2, LDT = KC + 8, PT = 16 * NB, PR = KC / 8;
+    constexpr int NW = 4, KC = 128 * SPC, LDT = KC + 8, PT = 16 * NB, PR = KC / 8;
     constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
     constexpr int NPC = PT * PR;                              /* 16-byte pieces per stage */
     constexpr int PPT = (NPC + 255) / 256;
@@ -1030,8 +1030,9 @@ void mx_prefill_kernel(K3kMxArgs a)
         };
         auto load_step = [&](int c, int d, auto slot) {
             constexpr int S = decltype(slot)::value;
-            const uint32_t bo = LAYOUT == 2 ? (uint32_t)c * 512u + (uint32_t)d * 256u
-                                            : ((uint32_t)(c >> 1) * 4u + 2u * (uint32_t)(c & 1) + (uint32_t)d) * 1024u;
+            /* step s = c SPC + d: 128 columns, 1 KB per tile (tiled MXFP4), 256 B per row (bf16) */
+            const uint32_t st = (uint32_t)(c * SPC + d);
+            const uint32_t bo = LAYOUT == 2 ? st * 256u : st * 1024u;
 #pragma unroll
             for (int m = 0; m < MT; m++)
 #pragma unroll
@@ -1042,7 +1043,7 @@ void mx_prefill_kernel(K3kMxArgs a)
             if (LAYOUT == 2) return;
 #pragma unroll
             for (int m = 0; m < MT; m++)
-                ss[m] = k3_bload4(m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1, soff[m] + (uint32_t)(c >> 1) * 256u);
+                ss[m] = k3_bload4(m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1, soff[m] + (uint32_t)((c * SPC) >> 2) * 256u);
         };
 
         using P0 = std::integral_constant<int, 0>;
@@ -1071,7 +1072,7 @@ void mx_prefill_kernel(K3kMxArgs a)
                 if (LAYOUT != 2) {
 #pragma unroll
                     for (int m = 0; m < MT; m++) {
-                        const uint32_t sraw = (sq[m] >> (8 * (2 * (c & 1) + d))) & 0xFFu;
+                        const uint32_t sraw = (sq[m] >> (8 * ((c * SPC + d) & 3))) & 0xFFu;
                         nanb[m] = sraw == 255u;              /* NaN byte: the block is 0 */
                         so[m] = k3_e8m0_operand(nanb[m] ? 127u : sraw);
                     }
@@ -1139,10 +1140,10 @@ void mx_prefill_kernel(K3kMxArgs a)
     }
 }
 
-template <int MODE, int MT, int NB, int LAYOUT>
+template <int MODE, int MT, int NB, int LAYOUT, int SPC = 2>
 int launch_prefill(const K3kMxArgs *a, int grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((mx_prefill_kernel<MODE, MT, NB, LAYOUT>), dim3(grid), dim3(256), 0, st, *a);
+    hipLaunchKernelGGL((mx_prefill_kernel<MODE, MT, NB, LAYOUT, SPC>), dim3(grid), dim3(256), 0, st, *a);
     K3K_LAUNCH_CHECK("mx_prefill launch");
     return 0;
 }
@@ -1299,21 +1300,23 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
         if (a->nsplit == 2) return launch_mx<K3K_MX_PLAIN, 1, 1, 2, 2, 16>(a, kw, grid, st);
         return launch_mx<K3K_MX_PLAIN, 1, 1, 1, 2, 16>(a, kw, grid, st);
     }
-    if (a->pass_tok == 48) {
-        /* large prefill batches: 48-token passes, K staged 256 columns at a time, weights
-         * two stages ahead, three MFMA column blocks per weight fragment */
-        if (a->K % 512 || a->nsplit != 1 || a->layout == 0)
-            return k3k_fail("mx_moe: 48-token passes need K % 512 == 0, bf16 activations and "
-                            "tiled or bf16 weights", hipErrorInvalidValue);
+    if (a->pass_tok == 48 || a->pass_tok == 96) {
+        /* large prefill batches on a tiled bank: 48-token passes (K staged 256 columns at a
+         * time) or 96-token passes (128 columns at a time, so the pass fits in LDS twice
+         * per CU); weights two stages ahead; each dequantized weight fragment feeds 3 or 6
+         * MFMA column blocks */
+        if (a->K % 512 || a->nsplit != 1 || a->layout != 1)
+            return k3k_fail("mx_moe: 48/96-token passes need K % 512 == 0, bf16 activations and "
+                            "a tiled bank", hipErrorInvalidValue);
         const bool gu = mode == K3K_MX_GATEUP;
         const int rpg = gu ? 128 : 256;
         const long items = (long)a->max_passes * ((a->rows + rpg - 1) / rpg);
         const int grid = (int)(items < (long)cus * 4 ? (items > 0 ? items : 1) : (long)cus * 4);
-        if (a->layout == 1)
-            return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 1>(a, grid, st)
-                      : launch_prefill<K3K_MX_DOWN, 4, 3, 1>(a, grid, st);
-        return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 2>(a, grid, st)
-                  : launch_prefill<K3K_MX_DOWN, 4, 3, 2>(a, grid, st);
+        if (a->pass_tok == 96)
+            return gu ? launch_prefill<K3K_MX_GATEUP, 4, 6, 1, 1>(a, grid, st)
+                      : launch_prefill<K3K_MX_DOWN, 4, 6, 1, 1>(a, grid, st);
+        return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 1>(a, grid, st)
+                  : launch_prefill<K3K_MX_DOWN, 4, 3, 1>(a, grid, st);
     }
     if (a->layout == 2) {
         /* bf16 weights (the dense shared expert): 2 tiles of 16 rows per wave, 32-token

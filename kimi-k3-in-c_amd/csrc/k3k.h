@@ -64,8 +64,9 @@ typedef struct {
     float *y;                           /* [ntok][ldy] */
     int ntok, ldy;
     /* GATEUP / DOWN: jobs from the gather. A pass is up to pass_tok tokens of one job:
-     * 16 (any K % 32 == 0, row-major bank), 8 (K % 512 == 0, either bank layout) or 32
-     * (K % 512 == 0, bf16 activations: the prefill kernel). */
+     * 16 (any K % 32 == 0, row-major bank), 8 (K % 512 == 0, either bank layout), 32
+     * (K % 512 == 0, bf16 activations) or 48 / 96 (the same on a tiled bank: the prefill
+     * kernel). */
     const void *bank;                   /* device K3ExpertQ[n_experts] */
     int pass_tok;
     int layout;                         /* 0: row-major MXFP4, 1: tiled MXFP4 (k3k_mx_tile),

@@ -370,6 +370,36 @@ def test_moe_device_prefill_passes(gpu, orc, k3):
     assert max_err_rel_inf(out, o2) <= 5e-2
 
 
+def test_moe_device_prefill_96_passes(gpu, orc, k3):
+    """Very large prefill batches on a tiled bank (>= 64 tokens per expert on average) run
+    96-token passes with K staged 128 columns at a time: routing exact, outputs within
+    2e-2 relative of the oracle and equal to the row-major bank's 32-token passes (the
+    same K order per token), ragged last passes, experts with 2-3 passes."""
+    E, I, N, K, T = 1536, 1024, 8, 4, 400
+    say(f"case: prefill 96-token passes E={E} I={I} N={N} K={K} T={T}")
+    rng = np.random.default_rng(59)
+    bank = [k3.gen_expert(E, I, 67, e) for e in range(N)]
+    W = (rng.standard_normal((N, E)) * 0.05).astype(np.float32)
+    X = rng.standard_normal((T, E)).astype(np.float32)
+    res = {}
+    for layout in (gpu.K3D_LAYOUT_ROWS, gpu.K3D_LAYOUT_TILED):
+        b = gpu.DevBank(bank, E, I, layout)
+        try:
+            res[layout] = gpu.moe_routed_device(b, X, W, None, K, prec=1, inter=I)
+        finally:
+            b.free()
+    out, idx, wt, perm, off, drops = res[gpu.K3D_LAYOUT_TILED]
+    o2, i2, w2 = orc.moe_routed(X, W, None, bank, E, I, K)
+    assert np.array_equal(idx, i2)
+    cnt = np.bincount(idx.ravel(), minlength=N)
+    assert cnt.max() > 192 and (cnt % 96 != 0).any()
+    assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
+    assert max_err_rel_inf(out, o2) <= 5e-2
+    rows_out = np.asarray(res[gpu.K3D_LAYOUT_ROWS][0])
+    assert np.array_equal(np.asarray(res[gpu.K3D_LAYOUT_ROWS][1]), idx)
+    assert np.abs(out - rows_out).max() <= 1e-6 * np.abs(rows_out).max()
+
+
 def test_moe_device_prefill_48_passes(gpu, orc, k3):
     """Large prefill batches on a tiled bank (>= 32 tokens per expert on average) run
     48-token passes with K staged 256 columns at a time: routing exact, outputs within 2e-2
