@@ -89,10 +89,11 @@ __device__ __forceinline__ float router_score(float logit, const ExcTable &x)
  * like the separate multiply and add). Run literally, that is a 7168-step dependent chain
  * per logit. Instead:
  *
- * 1. router_partial_kernel computes, per K chunk k of C_k columns, the chunk's own chain
- *    P_k (from 0, ascending) and R_k, an upper bound on the sum of |r_i| over the chunk's
- *    intermediate values r_i: per 32-column sub-block, 32 * (|r at its start| + ||w||_1 *
- *    ||x||_inf of the sub-block).
+ * 1. The partial kernels compute, per K chunk k of C_k columns, the chunk's own sum P_k
+ *    (from 0, its products added in any order with at most 32 roundings per 32-column
+ *    sub-block) and R_k, an upper bound on the sum of |r_i| over the intermediate values
+ *    r_i that are rounded: per sub-block, 32 * (|r at its start| + ||w||_1 * ||x||_inf of
+ *    the sub-block).
  * 2. router_final_kernel sums S = P_0 + P_1 + ... in k order and bounds |S - a_n|: with
  *    u = 2^-53 and Q_k the prefix before chunk k, the reference's chain errs from the
  *    exact sum by at most u * sum_i |a_i| <= u * sum_k (C_k |Q_k| + R_k), this
@@ -102,30 +103,59 @@ __device__ __forceinline__ float router_score(float logit, const ExcTable &x)
  * 3. Logits that are not certified and could matter -- the expert is selected (its weight
  *    must be exact) or its choice could reach the selection -- are recomputed with the
  *    reference's chain itself, and the selection is redone until no such logit is left.
- *
- * The partial kernel: a workgroup computes 32 experts x 64 tokens over one chunk, a thread
- * 2 experts x 4 tokens. W and x are staged in LDS 32 columns at a time (double buffered),
- * widened to fp64 once while staging (the conversion costs four times an fp64 fma), with
- * the sub-block norms; the threads' LDS reads are mostly broadcasts. */
-constexpr int RP_E = 32, RP_T = 64, RP_KS = 32, RP_SUB = 32, RP_LD = RP_KS + 2;
+ */
 
-__global__ __launch_bounds__(256) void router_partial_kernel(double *part, float *rbound,
-                                                             const float *x, int T, const float *W,
-                                                             int hidden, int n_experts, int chunk,
-                                                             int vec)
+/* A computed bound rb with relative error below rel - 1 as a float that is no smaller
+ * than the true bound: scaled up, converted, scaled by one more float rounding; the floor
+ * 2^-120 covers the absolute (subnormal) rounding errors that escape the relative form. */
+__device__ __forceinline__ float bound_up(double rb, double rel)
 {
-    __shared__ __attribute__((aligned(16))) double ws[2][RP_E][RP_LD];
-    __shared__ __attribute__((aligned(16))) double xs[2][RP_T][RP_LD];
-    __shared__ float wn[2][RP_E];                    /* sum |w| over the sub-block */
-    __shared__ float xn[2][RP_T];                    /* max |x| over the sub-block */
-    const int tid = threadIdx.x;
-    const int eg = tid & 15, tg = tid >> 4;          /* experts 2eg, 2eg+1; tokens 4tg.. */
-    const int e0 = blockIdx.x * RP_E, t0 = blockIdx.y * RP_T, ks = blockIdx.z;
+    return (float)(rb * rel) * (1.0f + 0x1p-20f) + 0x1p-120f;
+}
+
+constexpr int RP_KS = 32, RP_SUB = 32;     /* chunk granule and bound sub-block, columns */
+
+/* Partials of more than four tokens on the fp64 matrix cores. v_mfma_f64_16x16x4f64 adds
+ * to each element of a 16 x 16 block four exact products (fp32 operands widened to fp64
+ * multiply exactly) with at most four round-to-nearest additions, so a chunk's value is
+ * again a sum of its products with at most 32 roundings per 32-column sub-block, each of
+ * an intermediate bounded by |r at the sub-block's start| + ||w||_1 ||x||_inf of the
+ * sub-block: R_k keeps the form above. (Measured on gfx950: the instruction adds the four
+ * products to the accumulator one after another in k order, each addition rounded to
+ * nearest even; the bound needs only their count.) The order of the products inside a
+ * sub-block is free (both operands take the same permutation): lane group q = l / 16
+ * takes columns 8q .. 8q + 7, so a lane's operands of a sub-block are two 16-byte LDS
+ * reads.
+ *
+ * Tokens are the rows of the blocks (A operand, row i at lane i + 16 q), experts the
+ * columns (B operand), so element (i, j) sits at lane j + 16 (i % 4), register i / 4 and
+ * 16 lanes store 16 consecutive experts of one token. A wave computes MT x ME blocks
+ * (16 MT tokens x 16 ME experts), the 4 waves of a workgroup 2 x 2 of those. W and x are
+ * staged in LDS as fp32 (rows padded to 36 floats: the 16-byte reads of 8 consecutive
+ * lanes fall on distinct banks), double buffered, with the sub-block norms. The bound is
+ * accumulated in fp32, rounded up at the end by its relative error ((nsub + 4) 2^-24). */
+constexpr int RM_LD = 36;
+
+template <int MT, int ME>
+__global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, float *rbound,
+                                                                  const float *x, int T,
+                                                                  const float *W, int hidden,
+                                                                  int n_experts, int chunk, int vec)
+{
+    typedef double d4 __attribute__((ext_vector_type(4)));
+    constexpr int TB = 32 * MT, EB = 32 * ME;           /* workgroup tile: tokens, experts */
+    constexpr int NWP = EB / 32, NXP = TB / 32;         /* float4 pieces per thread: W, x */
+    __shared__ __attribute__((aligned(16))) float ws[2][EB * RM_LD];
+    __shared__ __attribute__((aligned(16))) float xs[2][TB * RM_LD];
+    __shared__ float wn[2][EB];                          /* sum |w| over the sub-block */
+    __shared__ float xn[2][TB];                          /* max |x| over the sub-block */
+    const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
+    const int wt = wv >> 1, we = wv & 1;                 /* the wave's block of the tile */
+    const int e0 = blockIdx.x * EB, t0 = blockIdx.y * TB, ks = blockIdx.z;
     const int kb0 = ks * chunk, kb1 = min(hidden, kb0 + chunk);
     const int nsub = (kb1 - kb0 + RP_KS - 1) / RP_KS;
     const float *Wt = W + (size_t)e0 * hidden, *xt = x + (size_t)t0 * hidden;
-    /* staging: W 32 rows x 8 float4 = 256 pieces (1 per thread), x 64 x 8 = 512 (2) */
-    float4 wst, xst[2];
+    float4 wst[NWP], xst[NXP];
     auto fetch = [&](const float *base, int rows_valid, int r, int k) {
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (r < rows_valid) {
@@ -140,47 +170,50 @@ __global__ __launch_bounds__(256) void router_partial_kernel(double *part, float
         }
         return v;
     };
+    /* piece p = tid + 256 i: row p / 8, columns 4 (p % 8) .. + 3 */
     auto load = [&](int sc) {
-        const int k0 = kb0 + sc * RP_KS;
-        wst = fetch(Wt, n_experts - e0, tid >> 3, k0 + (tid & 7) * 4);
+        const int k0 = kb0 + sc * RP_KS + (tid & 7) * 4;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int pc = tid + 256 * i;
-            xst[i] = fetch(xt, T - t0, pc >> 3, k0 + (pc & 7) * 4);
-        }
-    };
-    auto put = [&](double *dst, float4 v) {
-        reinterpret_cast<double2 *>(dst)[0] = make_double2((double)v.x, (double)v.y);
-        reinterpret_cast<double2 *>(dst)[1] = make_double2((double)v.z, (double)v.w);
+        for (int i = 0; i < NWP; i++) wst[i] = fetch(Wt, n_experts - e0, (tid + 256 * i) >> 3, k0);
+#pragma unroll
+        for (int i = 0; i < NXP; i++) xst[i] = fetch(xt, T - t0, (tid + 256 * i) >> 3, k0);
     };
     auto store = [&](int buf) {
-        /* 8 consecutive threads hold one row's 32 columns */
-        {
-            const int r = tid >> 3, c = (tid & 7) * 4;
-            put(&ws[buf][r][c], wst);
-            float a = fabsf(wst.x) + fabsf(wst.y) + fabsf(wst.z) + fabsf(wst.w);
+        const int c = (tid & 7) * 4;
+#pragma unroll
+        for (int i = 0; i < NWP; i++) {
+            const int r = (tid + 256 * i) >> 3;
+            *reinterpret_cast<float4 *>(&ws[buf][r * RM_LD + c]) = wst[i];
+            float a = fabsf(wst[i].x) + fabsf(wst[i].y) + fabsf(wst[i].z) + fabsf(wst[i].w);
             a += __shfl_xor(a, 1, 64);
             a += __shfl_xor(a, 2, 64);
             a += __shfl_xor(a, 4, 64);
             if ((tid & 7) == 0) wn[buf][r] = a;
         }
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int pc = tid + 256 * i, r = pc >> 3, c = (pc & 7) * 4;
-            put(&xs[buf][r][c], xst[i]);
+        for (int i = 0; i < NXP; i++) {
+            const int r = (tid + 256 * i) >> 3;
+            *reinterpret_cast<float4 *>(&xs[buf][r * RM_LD + c]) = xst[i];
             float m = fmaxf(fmaxf(fabsf(xst[i].x), fabsf(xst[i].y)), fmaxf(fabsf(xst[i].z), fabsf(xst[i].w)));
             m = fmaxf(m, __shfl_xor(m, 1, 64));
             m = fmaxf(m, __shfl_xor(m, 2, 64));
             m = fmaxf(m, __shfl_xor(m, 4, 64));
-            if ((pc & 7) == 0) xn[buf][r] = m;
+            if ((tid & 7) == 0) xn[buf][r] = m;
         }
     };
 
-    double acc[2][4], rb[2][4];
+    const int q = l >> 4, r16 = l & 15;
+    const int trow = wt * 16 * MT, erow = we * 16 * ME;  /* the wave's first token / expert */
+    d4 acc[MT][ME];
+    float rb[MT][ME][4];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < MT; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) { acc[a][b] = 0.0; rb[a][b] = 0.0; }
+        for (int b = 0; b < ME; b++) {
+            acc[a][b] = d4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int r = 0; r < 4; r++) rb[a][b][r] = 0.0f;
+        }
 
     load(0);
     store(0);
@@ -188,50 +221,70 @@ __global__ __launch_bounds__(256) void router_partial_kernel(double *part, float
     for (int sc = 0; sc < nsub; sc++) {
         const int buf = sc & 1;
         if (sc + 1 < nsub) load(sc + 1);
-        /* bound term of this sub-block, from the chains' values at its start */
+        /* bound term of this sub-block from the chains' values at its start: element
+         * (i, j) of block (a, b) is token trow + 16 a + 4 r + q, expert erow + 16 b + r16 */
+        {
+            float xr[MT][4], we_[ME];
 #pragma unroll
-        for (int a = 0; a < 2; a++)
+            for (int a = 0; a < MT; a++)
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const double an = (double)wn[buf][2 * eg + a] * (double)xn[buf][4 * tg + b];
-                rb[a][b] = fma((double)RP_SUB, fabs(acc[a][b]) + an, rb[a][b]);
-            }
-#pragma unroll 4
-        for (int k = 0; k < RP_KS; k += 2) {
-            const double2 w0 = *reinterpret_cast<const double2 *>(&ws[buf][2 * eg][k]);
-            const double2 w1 = *reinterpret_cast<const double2 *>(&ws[buf][2 * eg + 1][k]);
-            double2 xv[4];
+                for (int r = 0; r < 4; r++) xr[a][r] = xn[buf][trow + 16 * a + 4 * r + q];
 #pragma unroll
-            for (int b = 0; b < 4; b++) xv[b] = *reinterpret_cast<const double2 *>(&xs[buf][4 * tg + b][k]);
+            for (int b = 0; b < ME; b++) we_[b] = wn[buf][erow + 16 * b + r16];
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                acc[0][b] = fma(w0.x, xv[b].x, acc[0][b]);
-                acc[1][b] = fma(w1.x, xv[b].x, acc[1][b]);
-            }
+            for (int a = 0; a < MT; a++)
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                acc[0][b] = fma(w0.y, xv[b].y, acc[0][b]);
-                acc[1][b] = fma(w1.y, xv[b].y, acc[1][b]);
+                for (int b = 0; b < ME; b++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        rb[a][b][r] = fmaf((float)RP_SUB, (float)fabs(acc[a][b][r]) + we_[b] * xr[a][r],
+                                           rb[a][b][r]);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float4 xa[MT], wb[ME];
+#pragma unroll
+            for (int a = 0; a < MT; a++)
+                xa[a] = *reinterpret_cast<const float4 *>(&xs[buf][(trow + 16 * a + r16) * RM_LD + 8 * q + 4 * h]);
+#pragma unroll
+            for (int b = 0; b < ME; b++)
+                wb[b] = *reinterpret_cast<const float4 *>(&ws[buf][(erow + 16 * b + r16) * RM_LD + 8 * q + 4 * h]);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                double av[MT], bv[ME];
+#pragma unroll
+                for (int a = 0; a < MT; a++) av[a] = (double)(s == 0 ? xa[a].x : s == 1 ? xa[a].y : s == 2 ? xa[a].z : xa[a].w);
+#pragma unroll
+                for (int b = 0; b < ME; b++) bv[b] = (double)(s == 0 ? wb[b].x : s == 1 ? wb[b].y : s == 2 ? wb[b].z : wb[b].w);
+#pragma unroll
+                for (int a = 0; a < MT; a++)
+#pragma unroll
+                    for (int b = 0; b < ME; b++)
+                        acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b], acc[a][b], 0, 0, 0);
             }
         }
         if (sc + 1 < nsub) store(buf ^ 1);
         __syncthreads();
     }
+    /* relative error of the fp32 bound: (nsub + 4) roundings of 2^-24, the float sums of
+     * |w| at most 2^-18 */
+    const double up = 1.0 + 0x1p-17 + (double)(nsub + 4) * 0x1p-24;
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < MT; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int e = e0 + 2 * eg + a, t = t0 + 4 * tg + b;
-            if (e < n_experts && t < T) {
-                const size_t o = ((size_t)ks * T + t) * n_experts + e;
-                part[o] = acc[a][b];
-                /* rounded up: the float sums of |w| carry at most a 2^-18 relative error */
-                rbound[o] = (float)(rb[a][b] * (1.0 + 0x1p-17)) * (1.0f + 0x1p-20f);
+        for (int b = 0; b < ME; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = t0 + trow + 16 * a + 4 * r + q, e = e0 + erow + 16 * b + r16;
+                if (e < n_experts && t < T) {
+                    const size_t o = ((size_t)ks * T + t) * n_experts + e;
+                    part[o] = acc[a][b][r];
+                    rbound[o] = bound_up((double)rb[a][b][r], up);
+                }
             }
-        }
 }
 
-/* The same partials for a few tokens (T <= RS_T): one lane per (expert, chunk of RS_CH
+/* The partials of a few tokens (T <= RS_T): one lane per (expert, chunk of RS_CH
  * columns) runs the chunk's chain for every token. The lane issues all of its W row
  * segment's loads at once (32 x 16 bytes) so that one memory latency covers the chunk;
  * the tokens' chunk is staged in LDS as fp64 (read as broadcasts) with the per-sub-block
@@ -323,7 +376,7 @@ __global__ __launch_bounds__(256) void router_partial_small_kernel(double *part,
         if (t < T) {
             const size_t o = ((size_t)ks * T + t) * n_experts + e;
             part[o] = acc[t];
-            rbound[o] = (float)(rb[t] * (1.0 + 0x1p-17)) * (1.0f + 0x1p-20f);
+            rbound[o] = bound_up(rb[t], 1.0 + 0x1p-17);
         }
 }
 
@@ -522,7 +575,7 @@ __global__ __launch_bounds__(256) void router_small_kernel(float4 *pre, const fl
     for (int t = 0; t < NT; t++) {
         psh[wv][t][lane] = acc[t];
         /* rounded up: the float sums of |w| carry at most a 2^-18 relative error */
-        rsh[wv][t][lane] = (float)(rb[t] * (1.0 + 0x1p-17)) * (1.0f + 0x1p-20f);
+        rsh[wv][t][lane] = bound_up(rb[t], 1.0 + 0x1p-17);
     }
     __syncthreads();
     if (lane < T && e < n_experts) {
@@ -1060,18 +1113,31 @@ extern "C" int k3k_split_bf16(uint16_t *hi, uint16_t *lo, const float *x, size_t
     return 0;
 }
 
+/* Matrix-core partials: a workgroup covers RM_TB tokens x RM_EB experts (one 16 x 32
+ * block per wave: 92 VGPRs, four workgroups per CU). */
+constexpr int RM_TB = 32, RM_EB = 64;
+
 extern "C" int k3k_router_chunk(int T, int hidden, int n_experts)
 {
     if (T <= RS_T) return RS_CH;          /* one lane per (expert, 128-column chunk) */
-    /* enough workgroups to fill the chip, chunks a multiple of 32 columns */
-    const long tiles = (long)((n_experts + RP_E - 1) / RP_E) * ((T + RP_T - 1) / RP_T);
-    long ks = (2L * k3k_cu_count() + tiles - 1) / tiles;
-    const long kmax = (hidden + 255) / 256;
-    if (ks > kmax) ks = kmax;
-    if (ks < 1) ks = 1;
-    int chunk = (int)((hidden + ks - 1) / ks);
-    chunk = (chunk + RP_KS - 1) / RP_KS * RP_KS;
-    return chunk;
+    /* chunks a multiple of 32 columns and at least 256; among those, the split whose
+     * busiest CU has the least work (workgroups per CU x columns per workgroup), the most
+     * workgroups among equals (a shorter tail) up to 12 per CU (more partials to sum) */
+    const long tiles = (long)((n_experts + RM_EB - 1) / RM_EB) * ((T + RM_TB - 1) / RM_TB);
+    const long cus = k3k_cu_count() > 0 ? k3k_cu_count() : 1;
+    long kmax = (hidden + 255) / 256;
+    if (kmax < 1) kmax = 1;
+    long best_chunk = 0, best_load = -1;
+    for (long ks = 1; ks <= kmax; ks++) {
+        long chunk = (hidden + ks - 1) / ks;
+        chunk = (chunk + RP_KS - 1) / RP_KS * RP_KS;
+        const long n = (hidden + chunk - 1) / chunk;
+        const long per_cu = (tiles * n + cus - 1) / cus;
+        if (best_load >= 0 && per_cu > 12) break;
+        const long load = per_cu * chunk;
+        if (best_load < 0 || load <= best_load) { best_load = load; best_chunk = chunk; }
+    }
+    return (int)best_chunk;
 }
 
 /* Up to RS_T tokens and 64 chunks of RS_CH columns whose staged rows fit in LDS beside
@@ -1141,9 +1207,10 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
             hipLaunchKernelGGL(router_partial_small_kernel<RS_T>, grid, dim3(256), 0, st, part,
                                rbound, x, T, W, hidden, n_experts, vec);
     } else {
-        dim3 grid((n_experts + RP_E - 1) / RP_E, (T + RP_T - 1) / RP_T, ks);
-        hipLaunchKernelGGL(router_partial_kernel, grid, dim3(256), 0, st, part, rbound, x, T, W,
-                           hidden, n_experts, chunk, vec);
+        static_assert(RM_TB == 32 * 1 && RM_EB == 32 * 2, "tile of router_partial_mfma_kernel<1, 2>");
+        dim3 grid((n_experts + RM_EB - 1) / RM_EB, (T + RM_TB - 1) / RM_TB, ks);
+        hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2>), grid, dim3(256), 0, st, part, rbound,
+                           x, T, W, hidden, n_experts, chunk, vec);
     }
     K3K_LAUNCH_CHECK("router_partial launch");
     return 0;

@@ -203,11 +203,13 @@ def test_moe_device_tiled_decode_golden(gpu, wl, gold):
 @pytest.mark.parametrize("T,hidden,N,K,biased", [
     (1, 7168, 384, 8, False), (2, 1001, 70, 5, True), (3, 7168, 384, 8, True),
     (7, 7168, 384, 8, True), (31, 1001, 70, 5, True),
-    (33, 1000, 70, 5, False), (64, 7168, 384, 8, False), (100, 520, 131, 16, True)])
+    (33, 1000, 70, 5, False), (64, 7168, 384, 8, False), (100, 520, 131, 16, True),
+    (129, 7168, 384, 8, False), (300, 1000, 200, 5, True)])
 def test_router_device_bit_exact(gpu, orc, T, hidden, N, K, biased):
-    """Both tile shapes of the chain kernel (few / many tokens), widths that are not a
-    multiple of the staging chunk (and an odd one: scalar staging), expert counts that are
-    not a multiple of 64: idx and weight bits equal to the oracle's per-token router."""
+    """Every partial kernel (one lane per chunk for a few tokens, both matrix-core tile
+    shapes past that), widths that are not a multiple of the staging chunk (and an odd one:
+    scalar staging), expert and token counts that are not multiples of the tiles: idx and
+    weight bits equal to the oracle's per-token router."""
     say(f"case: router T={T} hidden={hidden} N={N} K={K} bias={biased}")
     rng = np.random.default_rng(T * 1000 + hidden)
     W = (rng.standard_normal((N, hidden)) * 0.02).astype(np.float32)
@@ -252,7 +254,7 @@ def test_router_device_ties_and_nonfinite(gpu, orc):
 
 
 @pytest.mark.parametrize("hidden", [1024, 7168])
-@pytest.mark.parametrize("ntok", [2, 40])
+@pytest.mark.parametrize("ntok", [2, 40, 200])
 def test_router_device_uncertified_logits(gpu, orc, hidden, ntok):
     """Rows built so that a chunked fp64 sum and the reference's sequential chain round to
     different floats (1 + 2^-24 - 2^-52 then 2^-53 terms: the chain ties to even at every
