@@ -380,19 +380,52 @@ __global__ __launch_bounds__(256) void router_partial_small_kernel(double *part,
         }
 }
 
-/* The reference's own chain for one logit (the fallback of the certification). */
-__device__ __forceinline__ double router_chain(const float *w, const float *x, int hidden)
+/* The reference's own chain for one logit (the fallback of the certification), computed
+ * by a whole workgroup: acc = 0; for k ascending: acc = fma(w_k, x_k, acc). The chain is one dependent fp64 add per column, so one thread runs it
+ * (thread 0), adding the exact products w_k x_k (a product of two floats is exact in
+ * fp64, so acc + w_k x_k rounds like fma(w_k, x_k, acc)) that the other waves write into
+ * an LDS ring of two RF_BLK-column blocks one block ahead. Every thread of the workgroup
+ * calls it; the result is valid in thread 0. */
+constexpr int RF_BLK = 512, RF_LIST = 64;
+
+__device__ double chain_block(double (*ring)[RF_BLK], const float *w, const float *x, int hidden)
 {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const bool many = nthr > 64;                 /* producers: waves 1.., else every lane */
+    const int p0 = many ? tid - 64 : tid, np = many ? nthr - 64 : nthr;
+    const int nb = (hidden + RF_BLK - 1) / RF_BLK;
+    auto produce = [&](int b) {
+        if (p0 < 0) return;
+        double *dst = ring[b & 1];
+        for (int i = p0; i < RF_BLK; i += np) {
+            const int k = b * RF_BLK + i;
+            dst[i] = k < hidden ? (double)w[k] * (double)x[k] : 0.0;
+        }
+    };
     double acc = 0.0;
-    int k = 0;
-    for (; k + 8 <= hidden; k += 8) {
-        float wv[8], xv[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) { wv[j] = w[k + j]; xv[j] = x[k + j]; }
-#pragma unroll
-        for (int j = 0; j < 8; j++) acc = fma((double)wv[j], (double)xv[j], acc);
+    produce(0);
+    __syncthreads();
+    for (int b = 0; b < nb; b++) {
+        if (b + 1 < nb) produce(b + 1);
+        if (tid == 0) {
+            const double2 *p2 = reinterpret_cast<const double2 *>(ring[b & 1]);
+            const int n = min(RF_BLK, hidden - b * RF_BLK);
+            int i = 0;
+            for (; i + 8 <= n; i += 8) {
+                const double2 a0 = p2[i / 2], a1 = p2[i / 2 + 1], a2 = p2[i / 2 + 2], a3 = p2[i / 2 + 3];
+                acc += a0.x;
+                acc += a0.y;
+                acc += a1.x;
+                acc += a1.y;
+                acc += a2.x;
+                acc += a2.y;
+                acc += a3.x;
+                acc += a3.y;
+            }
+            for (; i < n; i++) acc += ring[b & 1][i];
+        }
+        __syncthreads();
     }
-    for (; k < hidden; k++) acc = fma((double)w[k], (double)x[k], acc);
     return acc;
 }
 
@@ -415,8 +448,10 @@ __device__ __forceinline__ void round_interval(float f, double &lo, double &hi)
 
 /* The certification of a logit from its chunk sums (S = Q, the sum of P_k in k order, and
  * bs, the sum of C_k |Q_k| + 2 R_k + |Q_{k+1}|): with u = 2^-53, B = 1.01 u bs + 4u|S|
- * bounds |S - a_n| (the reference's chain). If every value in [S - B, S + B] rounds to the
- * same float, that float is the logit (ok); otherwise scmax is the score of the largest
+ * bounds |S - a_n| (the reference's chain), so the logit (float)a_n is one of the floats
+ * from (float)(S - B) to (float)(S + B) (rounding is monotone). The score is certain (ok)
+ * when that range is one float, or two neighbouring floats whose scores are equal (the
+ * choice, score + bias, is then certain too); otherwise scmax is the score of the largest
  * float the logit can be. Non-finite sums come from inf/NaN inputs and propagate alike in
  * any order (ok). */
 struct Certified {
@@ -427,22 +462,32 @@ struct Certified {
 __device__ __forceinline__ Certified certify_score(double Q, double bs, const ExcTable &exc)
 {
     const float f = (float)Q;
-    bool ok = true;
-    float fhi = f;
+    Certified r;
+    r.sc = router_score(f, exc);
+    r.scmax = r.sc;
+    r.ok = true;
     if (fabs(Q) <= 0x1.fffffffffffffp+1023) {
         const double B = 1.01 * 0x1p-53 * bs + 4.0 * 0x1p-53 * fabs(Q) + 0x1p-1060;
         double mlo, mhi;
         round_interval(f, mlo, mhi);
-        ok = (Q - B > mlo) && (Q + B < mhi);
-        if (!ok) {
-            const float hb = (float)(Q + B);
-            fhi = fabsf(hb) <= 0x1.fffffep+127f ? next_float(hb, true) : hb;
+        if (!((Q - B > mlo) && (Q + B < mhi))) {
+            const float lo = (float)(Q - B), hi = (float)(Q + B);
+            const bool finite = fabsf(lo) <= 0x1.fffffep+127f && fabsf(hi) <= 0x1.fffffep+127f;
+            if (finite && (lo == hi || next_float(lo, true) == hi)) {
+                const float slo = router_score(lo, exc), shi = router_score(hi, exc);
+                if (slo == shi) {
+                    r.sc = slo;
+                    r.scmax = slo;
+                } else {
+                    r.ok = false;
+                    r.scmax = fmaxf(slo, shi);
+                }
+            } else {
+                r.ok = false;
+                r.scmax = router_score(fabsf(hi) <= 0x1.fffffep+127f ? next_float(hi, true) : hi, exc);
+            }
         }
     }
-    Certified r;
-    r.sc = router_score(f, exc);
-    r.ok = ok;
-    r.scmax = ok ? r.sc : router_score(fhi, exc);
     return r;
 }
 
@@ -672,7 +717,10 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
     __shared__ uint64_t candk[RF_MAXW][64];
     __shared__ uint64_t selk[64];
     __shared__ float csh[RF_MAXE], ssh[RF_MAXE];
-    __shared__ int nre_sh;
+    __shared__ int nre_sh, nlist_sh;
+    __shared__ int list_sh[RF_LIST];
+    __shared__ double res_sh[RF_LIST];
+    __shared__ __attribute__((aligned(16))) double prod_sh[2][RF_BLK];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
     const int nthr = blockDim.x;
     const int t = blockIdx.x;
@@ -814,18 +862,34 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
             need[i] = unc[i] && (sel[i] || nsel < topk || cmax[i] >= ckth);
             need_any |= need[i];
         }
+        if (tid == 0) nlist_sh = 0;
         if (!__syncthreads_or(need_any)) break;
+        /* list up to RF_LIST of them; the rest wait for the next round */
+        int slot[SL];
+#pragma unroll
+        for (int i = 0; i < SL; i++) slot[i] = need[i] ? atomicAdd(&nlist_sh, 1) : RF_LIST;
+        __syncthreads();
+        const int nl = min(nlist_sh, RF_LIST);
 #pragma unroll
         for (int i = 0; i < SL; i++)
-            if (need[i]) {
+            if (slot[i] < RF_LIST) list_sh[slot[i]] = tid + nthr * i;
+        __syncthreads();
+        for (int j = 0; j < nl; j++) {
+            const double a = chain_block(prod_sh, W + (size_t)list_sh[j] * hidden,
+                                         x + (size_t)t * hidden, hidden);
+            if (tid == 0) res_sh[j] = a;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < SL; i++)
+            if (slot[i] < RF_LIST) {
                 const int e = tid + nthr * i;
-                const double a = router_chain(W + (size_t)e * hidden, x + (size_t)t * hidden, hidden);
-                sc[i] = router_score((float)a, exc);
+                sc[i] = router_score((float)res_sh[slot[i]], exc);
                 c[i] = sc[i] + (bias ? bias[e] : 0.0f);
                 cmax[i] = c[i];
                 unc[i] = false;
-                atomicAdd(&nre_sh, 1);
             }
+        if (tid == 0) nre_sh += nl;
         __syncthreads();
     }
     __syncthreads();

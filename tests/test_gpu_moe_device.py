@@ -255,33 +255,42 @@ def test_router_device_ties_and_nonfinite(gpu, orc):
 
 @pytest.mark.parametrize("hidden", [1024, 7168])
 @pytest.mark.parametrize("ntok", [2, 40, 200])
-def test_router_device_uncertified_logits(gpu, orc, hidden, ntok):
+@pytest.mark.parametrize("scale", [1.0, -16.0])
+def test_router_device_uncertified_logits(gpu, orc, hidden, ntok, scale):
     """Rows built so that a chunked fp64 sum and the reference's sequential chain round to
     different floats (1 + 2^-24 - 2^-52 then 2^-53 terms: the chain ties to even at every
-    step, a chunked sum does not): the router must detect the ambiguous rounding and use
-    the reference's chain. Expert 2's logit is exactly 1.0, a tie with the crafted experts
-    under the reference (lowest index first), and the crafted experts carry the largest
-    weights, so both the order of idx and the weight bits would expose a wrong logit."""
-    say(f"case: router uncertified logits hidden={hidden}")
+    step, a chunked sum does not), times a power of two (the roundings scale with it).
+    Expert 2's logit is exactly `scale`, a tie with the crafted experts under the reference
+    (lowest index first), and the three are chosen first (a bias lifts them when the scale
+    is negative), so both the order of idx and the weight bits would expose a wrong logit.
+    At scale -16 the two candidate floats of a crafted logit have scores 30 ulps apart, so
+    the router must run the reference's chain for them; at scale 1 the scores of the two
+    candidates may coincide, which certifies the score without the chain."""
+    say(f"case: router uncertified logits hidden={hidden} ntok={ntok} scale={scale}")
     N, K = 16, 4
     rng = np.random.default_rng(hidden)
     W = (rng.standard_normal((N, hidden)) * 1e-3).astype(np.float32)
     crafted = np.full(hidden, 2.0 ** -53, np.float32)
     crafted[:3] = [1.0, 2.0 ** -24, -2.0 ** -52]
     for e in (5, 11):
-        W[e] = crafted
+        W[e] = crafted * np.float32(scale)
     W[2] = 0.0
-    W[2, 0] = 1.0
+    W[2, 0] = scale
+    bias = None
+    if scale < 0:
+        bias = np.zeros(N, np.float32)
+        bias[[2, 5, 11]] = 1.0
     X = np.stack([np.ones(hidden, np.float32)] +
                  [rng.standard_normal(hidden).astype(np.float32) for _ in range(ntok - 1)])
-    idx, wt = gpu.router_device(X, W, None, K)
+    idx, wt = gpu.router_device(X, W, bias, K)
     rec = gpu.router_device.recomputed
     for t in range(ntok):
-        i2, w2 = orc.router(X[t], W, None, K)
+        i2, w2 = orc.router(X[t], W, bias, K)
         assert np.array_equal(idx[t], i2), (t, idx[t], i2)
         assert np.array_equal(bits(wt[t]), bits(w2)), t
     assert list(idx[0][:3]) == [2, 5, 11]
-    assert rec[0] >= 2          # both crafted logits went through the reference's chain
+    if scale < 0:
+        assert rec[0] >= 2      # both crafted logits went through the reference's chain
 
 
 def test_moe_graph_replay_matches_eager(gpu, small_layer):
