@@ -14,6 +14,10 @@ typedef float k3_f32x2 __attribute__((ext_vector_type(2)));
 /* Upper bound on top-k, as the reference's K3_MAX_TOPK (include/k3/k3.h:557). */
 #define K3_MAX_TOPK_DEV 64
 
+/* XCDs of an MI355X (8 x 32 CUs, an L2 each); the dispatcher hands workgroup b to XCD
+ * b % 8. Kernels use it only to group work that shares data; results do not depend on it. */
+#define K3_NXCD 8
+
 /* Record a launch/runtime failure for k3k_error() (defined in k3_rt.hip). */
 extern "C" int k3k_fail(const char *what, hipError_t e);
 #define K3K_LAUNCH_CHECK(what)                                   \

@@ -932,15 +932,16 @@ int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
  * feeds MT x NB MFMAs. Stage c covers steps c SPC .. c SPC + SPC - 1 (128 columns each).
  * Activation loads are unconditional (rows clamped to a valid token); only the LDS stores
  * are masked. Weight loads keep the default cache policy: an expert with several passes
- * re-reads its weights, and the caches then serve part of them. */
-template <int MODE, int MT, int NB, int LAYOUT, int SPC = 2>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
+ * re-reads its weights, and the caches then serve part of them. NW waves share one staged
+ * copy of the pass's activations. */
+template <int MODE, int MT, int NB, int LAYOUT, int SPC = 2, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void mx_prefill_kernel(K3kMxArgs a)
 {
-    constexpr int NW = 4, KC = 128 * SPC, LDT = KC + 8, PT = 16 * NB, PR = KC / 8;
+    constexpr int NTH = 64 * NW, KC = 128 * SPC, LDT = KC + 8, PT = 16 * NB, PR = KC / 8;
     constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
     constexpr int NPC = PT * PR;                              /* 16-byte pieces per stage */
-    constexpr int PPT = (NPC + 255) / 256;
+    constexpr int PPT = (NPC + NTH - 1) / NTH;
     constexpr int WQ = LAYOUT == 2 ? 4 : 1;
     __shared__ __attribute__((aligned(16))) uint16_t bsh[2][PT + 1][LDT];
 
@@ -952,18 +953,29 @@ void mx_prefill_kernel(K3kMxArgs a)
     const uint32_t rstride = (uint32_t)K >> 1;
     const int rpw = 16 * RT, rpg = NW * rpw;
     const int n_rb = (rows + rpg - 1) / rpg;
-    const int n_items = (*a.n_passes) * n_rb;
+    /* Workgroups go to the XCDs in turn (workgroup b to XCD b % 8). Group x of workgroups
+     * (b % nx == x) takes the passes [P x / nx, P (x + 1) / nx) -- an expert's passes are
+     * consecutive -- with the row block innermost, so the workgroups of one pass run at
+     * about the same time on one XCD and fetch its activations (and the passes of one
+     * expert its weights) into that XCD's L2 once. */
+    const int npass = *a.n_passes;
+    const int nx = min((int)gridDim.x, K3_NXCD);
+    const int xg = blockIdx.x % nx, li = blockIdx.x / nx;
+    const int nlw = ((int)gridDim.x - 1 - xg) / nx + 1;
+    const int pbeg = (int)((long)npass * xg / nx), pend = (int)((long)npass * (xg + 1) / nx);
+    const int n_items = (pend - pbeg) * n_rb;
 
-    for (int i = tid; i < 2 * LDT / 8; i += 256)
+    for (int i = tid; i < 2 * LDT / 8; i += NTH)
         *reinterpret_cast<uint4 *>(&bsh[i / (LDT / 8)][PT][(i % (LDT / 8)) * 8]) = make_uint4(0, 0, 0, 0);
 
-    for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-        const int rb = item % n_rb, pass = item / n_rb;
+    for (int item = li; item < n_items; item += nlw) {
+        const int rb = item % n_rb, pass = pbeg + item / n_rb;
         const int j = a.pass_job[pass];
         const int e = a.job_expert[j];
         const int off = a.job_off[j];
         const int tok0 = a.pass_tp[pass] * PT;
-        const int ntok = min(PT, a.job_cnt[j] - tok0);
+        const int ntok = __builtin_amdgcn_readfirstlane(min(PT, a.job_cnt[j] - tok0));
+        const int nbu = (ntok + 15) >> 4;             /* token blocks holding tokens */
         const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[e];
         const uint32_t prow = LAYOUT == 1 ? (uint32_t)((rows + 15) & ~15) : (uint32_t)rows;
         const uint32_t pbytes = LAYOUT == 2 ? prow * (uint32_t)K * 2u : prow * rstride;
@@ -998,7 +1010,7 @@ void mx_prefill_kernel(K3kMxArgs a)
         int ldst[PPT];
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
-            const int pc = tid + 256 * i, p = pc / PR, o = pc % PR;
+            const int pc = tid + NTH * i, p = pc / PR, o = pc % PR;
             const bool ok = pc < NPC && p < ntok;
             const int ar = a.perm[off + tok0 + (ok ? p : 0)];
             const int xr = (MODE == K3K_MX_GATEUP) ? ar / a.topk : ar;
@@ -1048,23 +1060,24 @@ void mx_prefill_kernel(K3kMxArgs a)
 
         using P0 = std::integral_constant<int, 0>;
         using P1 = std::integral_constant<int, 1>;
+        /* Every prefetch is issued unconditionally (past the last stage the loads read
+         * data that is never used, or zeros past the end of a buffer), so that the wait for
+         * a stage's weights counts exactly the loads issued after them instead of draining
+         * the queue; the stage count is even (K % 512 == 0). */
         load_b(0);
         load_scales(0, sq);
 #pragma unroll
         for (int d = 0; d < SPC; d++) load_step(0, d, P0{});
-        if (nstage > 1) {
-            load_scales(1, sqn);
+        load_scales(1, sqn);
 #pragma unroll
-            for (int d = 0; d < SPC; d++) load_step(1, d, P1{});
-        }
+        for (int d = 0; d < SPC; d++) load_step(1, d, P1{});
         store_b(0);
         __syncthreads();
         auto stage = [&](int c, auto slot) {
             constexpr int S = decltype(slot)::value;
             const int buf = c & 1;
-            const bool more = c + 1 < nstage, more2 = c + 2 < nstage;
-            if (more) load_b(c + 1);
-            if (more2) load_scales(c + 2, sqnn);
+            load_b(c + 1);
+            load_scales(c + 2, sqnn);
 #pragma unroll
             for (int d = 0; d < SPC; d++) {
                 float so[MT];
@@ -1093,22 +1106,23 @@ void mx_prefill_kernel(K3kMxArgs a)
                     }
 #pragma unroll
                     for (int nb = 0; nb < NB; nb++) {
+                        if (nb >= nbu) break;             /* a pass's last blocks may be empty */
                         const uint4 bv = *reinterpret_cast<const uint4 *>(&bsh[buf][brow[nb]][(4 * d + g) * 32 + pp * 8]);
 #pragma unroll
                         for (int m = 0; m < MT; m++)
                             acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[m], k3_as_bf16x8(bv), acc[m][nb], 0, 0, 0);
                     }
                 }
-                if (more2) load_step(c + 2, d, slot);
+                load_step(c + 2, d, slot);
             }
-            if (more) store_b(buf ^ 1);
+            store_b(buf ^ 1);
 #pragma unroll
             for (int m = 0; m < MT; m++) { sq[m] = sqn[m]; sqn[m] = sqnn[m]; }
             __syncthreads();
         };
         for (int c = 0; c < nstage; c += 2) {
             stage(c, P0{});
-            if (c + 1 < nstage) stage(c + 1, P1{});
+            stage(c + 1, P1{});
         }
 
 #pragma unroll
@@ -1140,10 +1154,10 @@ void mx_prefill_kernel(K3kMxArgs a)
     }
 }
 
-template <int MODE, int MT, int NB, int LAYOUT, int SPC = 2>
+template <int MODE, int MT, int NB, int LAYOUT, int SPC = 2, int NW = 4>
 int launch_prefill(const K3kMxArgs *a, int grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((mx_prefill_kernel<MODE, MT, NB, LAYOUT, SPC>), dim3(grid), dim3(256), 0, st, *a);
+    hipLaunchKernelGGL((mx_prefill_kernel<MODE, MT, NB, LAYOUT, SPC, NW>), dim3(grid), dim3(64 * NW), 0, st, *a);
     K3K_LAUNCH_CHECK("mx_prefill launch");
     return 0;
 }
@@ -1309,14 +1323,16 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
             return k3k_fail("mx_moe: 48/96-token passes need K % 512 == 0, bf16 activations and "
                             "a tiled bank", hipErrorInvalidValue);
         const bool gu = mode == K3K_MX_GATEUP;
-        const int rpg = gu ? 128 : 256;
+        /* 8 waves per workgroup (one workgroup per CU at two waves per SIMD): twice the rows
+         * per staged copy of the pass's activations of 4 waves, half the activation reads */
+        const int rpg = gu ? 256 : 512;
         const long items = (long)a->max_passes * ((a->rows + rpg - 1) / rpg);
-        const int grid = (int)(items < (long)cus * 4 ? (items > 0 ? items : 1) : (long)cus * 4);
+        const int grid = (int)(items < (long)cus ? (items > 0 ? items : 1) : (long)cus);
         if (a->pass_tok == 96)
-            return gu ? launch_prefill<K3K_MX_GATEUP, 4, 6, 1, 1>(a, grid, st)
-                      : launch_prefill<K3K_MX_DOWN, 4, 6, 1, 1>(a, grid, st);
-        return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 1>(a, grid, st)
-                  : launch_prefill<K3K_MX_DOWN, 4, 3, 1>(a, grid, st);
+            return gu ? launch_prefill<K3K_MX_GATEUP, 4, 6, 1, 1, 8>(a, grid, st)
+                      : launch_prefill<K3K_MX_DOWN, 4, 6, 1, 1, 8>(a, grid, st);
+        return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 1, 2, 8>(a, grid, st)
+                  : launch_prefill<K3K_MX_DOWN, 4, 3, 1, 2, 8>(a, grid, st);
     }
     if (a->layout == 2) {
         /* bf16 weights (the dense shared expert): 2 tiles of 16 rows per wave, 32-token
