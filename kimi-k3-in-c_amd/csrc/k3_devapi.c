@@ -280,7 +280,7 @@ int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const
 /* ---- MoE experts ----------------------------------------------------------------------- */
 typedef struct {
     uint16_t *xhi, *xlo, *ahi, *alo;
-    int *offsets, *perm, *job_expert, *job_off, *job_cnt, *pass_job, *pass_tp, *counts;
+    int *offsets, *perm, *job_expert, *job_off, *job_cnt, *pass_job, *pass_tp, *counts, *ghist;
     float *contrib;
     int max_passes;
 } MoeWs;
@@ -330,6 +330,10 @@ static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n
     w->pass_job = (int *)take(c, (size_t)w->max_passes * 4);
     w->pass_tp = (int *)take(c, (size_t)w->max_passes * 4);
     w->counts = (int *)take(c, 16);
+    {
+        const size_t gs = k3k_gather_scratch(T, topk, n_experts);
+        w->ghist = gs ? (int *)take(c, gs * 4) : NULL;
+    }
     w->contrib = (float *)take(c, N * hidden * 4);
     return c->off;
 }
@@ -383,7 +387,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
          * the gather runs only when its permutation is asked for */
         if ((perm_out || offsets_out) &&
             k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
-                       w->counts, idx, T, topk, n_experts, bank, pass_tok, stream))
+                       w->counts, w->ghist, idx, T, topk, n_experts, bank, pass_tok, stream))
             return fail("gather");
         k3k_prof_mark(stream, K3D_STAGE_GATHER);
         K3kMxArgs a;
@@ -419,7 +423,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     }
     if (k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
     if (k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
-                   w->counts, idx, T, topk, n_experts, bank, pass_tok, stream))
+                   w->counts, w->ghist, idx, T, topk, n_experts, bank, pass_tok, stream))
         return fail("gather");
     k3k_prof_mark(stream, K3D_STAGE_GATHER);
     K3kMxArgs a;

@@ -943,25 +943,14 @@ __device__ __forceinline__ int block_scan_excl(int v, int *wtot, int lane, int w
     return base + x - v;
 }
 
-__global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, int *job_expert,
-                                                      int *job_off, int *job_cnt, int *pass_job,
-                                                      int *pass_tp, int *counts, const int *idx,
-                                                      int N, int n_experts, const void *bank,
-                                                      int pass_tok)
+/* From per-expert counts cnt[] (LDS): offsets[], fill[] (= offsets, in LDS), the jobs,
+ * the passes and counts[0..2], as the gather's header describes. Called by all 1024
+ * threads; ends with a barrier. */
+__device__ void gather_plan(const int *cnt, int *fill, int *wtot, int *offsets, int *job_expert,
+                            int *job_off, int *job_cnt, int *pass_job, int *pass_tp, int *counts,
+                            int n_experts, const void *bank, int pass_tok)
 {
-    __shared__ int cnt[G_MAXE];
-    __shared__ int fill[G_MAXE];
-    __shared__ int wtot[16];
-    __shared__ unsigned short wcnt[16][G_WCNT_E];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    for (int e = tid; e < n_experts; e += 1024) cnt[e] = 0;
-    __syncthreads();
-    for (int a = tid; a < N; a += 1024) {
-        const int e = idx[a];
-        if (e >= 0 && e < n_experts) atomicAdd(&cnt[e], 1);
-    }
-    __syncthreads();
-
     /* per-thread sums over a contiguous expert range, then workgroup scans */
     const int per = (n_experts + 1023) / 1024;
     const int ea = tid * per, eb = min(n_experts, ea + per);
@@ -1006,6 +995,28 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
         counts[2] = tot_d;
     }
     __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, int *job_expert,
+                                                      int *job_off, int *job_cnt, int *pass_job,
+                                                      int *pass_tp, int *counts, const int *idx,
+                                                      int N, int n_experts, const void *bank,
+                                                      int pass_tok)
+{
+    __shared__ int cnt[G_MAXE];
+    __shared__ int fill[G_MAXE];
+    __shared__ int wtot[16];
+    __shared__ unsigned short wcnt[16][G_WCNT_E];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int e = tid; e < n_experts; e += 1024) cnt[e] = 0;
+    __syncthreads();
+    for (int a = tid; a < N; a += 1024) {
+        const int e = idx[a];
+        if (e >= 0 && e < n_experts) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    gather_plan(cnt, fill, wtot, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp, counts,
+                n_experts, bank, pass_tok);
 
     /* stable placement */
     const bool wide = n_experts > G_WCNT_E;
@@ -1053,6 +1064,98 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
                 __syncthreads();
             }
         }
+    }
+}
+
+/* The same gather over many workgroups, for large batches (more than GM_MIN assignments,
+ * at most G_WCNT_E experts): chunks of GM_C assignments.
+ *  1. gather_hist_kernel: chunk c's count of expert e -> hist[c * n_experts + e].
+ *  2. gather_scan_kernel (one workgroup): per-expert totals, then gather_plan; hist becomes
+ *     the position in perm of chunk c's first assignment of expert e.
+ *  3. gather_place_kernel: each chunk ranks its assignments stably (ballots inside a wave,
+ *     per-wave counts across waves) from those positions.
+ * perm comes out identical to the one-workgroup kernel's. */
+constexpr int GM_C = 512, GM_MIN = 4096;
+
+__global__ __launch_bounds__(GM_C) void gather_hist_kernel(int *hist, const int *idx, int N,
+                                                           int n_experts, int nchunk)
+{
+    __shared__ int cnt[G_WCNT_E];
+    const int c = blockIdx.x, tid = threadIdx.x;
+    for (int e = tid; e < n_experts; e += GM_C) cnt[e] = 0;
+    __syncthreads();
+    const int a = c * GM_C + tid;
+    if (a < N) {
+        const int e = idx[a];
+        if (e >= 0 && e < n_experts) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    for (int e = tid; e < n_experts; e += GM_C) hist[(size_t)c * n_experts + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(1024) void gather_scan_kernel(int *hist, int *offsets, int *job_expert,
+                                                           int *job_off, int *job_cnt, int *pass_job,
+                                                           int *pass_tp, int *counts, int n_experts,
+                                                           int nchunk, const void *bank, int pass_tok)
+{
+    __shared__ int cnt[G_WCNT_E];
+    __shared__ int fill[G_WCNT_E];
+    __shared__ int wtot[16];
+    const int tid = threadIdx.x;
+    /* a thread per expert; its chunk counts are a strided column (coalesced across the
+     * threads), read 16 at a time so that the loads overlap */
+    for (int e = tid; e < n_experts; e += 1024) {
+        int t = 0;
+#pragma unroll 16
+        for (int c = 0; c < nchunk; c++) t += hist[(size_t)c * n_experts + e];
+        cnt[e] = t;
+    }
+    __syncthreads();
+    gather_plan(cnt, fill, wtot, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp, counts,
+                n_experts, bank, pass_tok);
+    for (int e = tid; e < n_experts; e += 1024) {
+        int run = fill[e];
+#pragma unroll 16
+        for (int c = 0; c < nchunk; c++) {
+            const int v = hist[(size_t)c * n_experts + e];
+            hist[(size_t)c * n_experts + e] = run;
+            run += v;
+        }
+    }
+}
+
+__global__ __launch_bounds__(GM_C) void gather_place_kernel(int *perm, const int *hist,
+                                                            const int *idx, int N, int n_experts,
+                                                            int nchunk)
+{
+    constexpr int NWV = GM_C / 64;
+    __shared__ unsigned short wcnt[NWV][G_WCNT_E];
+    const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int i = tid; i < NWV * n_experts; i += GM_C) wcnt[i / n_experts][i % n_experts] = 0;
+    const int a = c * GM_C + tid;
+    const int e = a < N ? idx[a] : -1;
+    const bool ok = e >= 0 && e < n_experts;
+    /* rank among earlier lanes of this wave with the same expert */
+    uint64_t pending = __ballot(ok);
+    int rank = 0;
+    uint64_t mine = 0;
+    while (pending) {
+        const int leader = __ffsll((unsigned long long)pending) - 1;
+        const int el = __shfl(e, leader, 64);
+        const uint64_t m = __ballot(ok && e == el);
+        if (ok && e == el) {
+            mine = m;
+            rank = __popcll(m & ((1ull << lane) - 1ull));
+        }
+        pending &= ~m;
+    }
+    __syncthreads();
+    if (ok && rank == 0) wcnt[wv][e] = (unsigned short)__popcll(mine);
+    __syncthreads();
+    if (ok) {
+        int base = hist[(size_t)c * n_experts + e];
+        for (int w = 0; w < wv; w++) base += wcnt[w][e];
+        perm[base + rank] = a;
     }
 }
 
@@ -1322,15 +1425,37 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
 }
 
 extern "C" int k3k_gather(int *offsets, int *perm, int *job_expert, int *job_off, int *job_cnt,
-                          int *pass_job, int *pass_tp, int *counts, const int *idx, int T,
-                          int topk, int n_experts, const void *bank, int pass_tok, void *stream)
+                          int *pass_job, int *pass_tp, int *counts, int *hist, const int *idx,
+                          int T, int topk, int n_experts, const void *bank, int pass_tok,
+                          void *stream)
 {
     if (n_experts > G_MAXE) return k3k_fail("gather: too many experts", hipErrorInvalidValue);
-    hipLaunchKernelGGL(gather_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, offsets, perm,
-                       job_expert, job_off, job_cnt, pass_job, pass_tp, counts, idx, T * topk,
-                       n_experts, bank, pass_tok);
+    hipStream_t st = (hipStream_t)stream;
+    const int N = T * topk;
+    const size_t need = k3k_gather_scratch(T, topk, n_experts);
+    if (need && hist) {
+        const int nchunk = (N + GM_C - 1) / GM_C;
+        hipLaunchKernelGGL(gather_hist_kernel, dim3(nchunk), dim3(GM_C), 0, st, hist, idx, N,
+                           n_experts, nchunk);
+        hipLaunchKernelGGL(gather_scan_kernel, dim3(1), dim3(1024), 0, st, hist, offsets, job_expert,
+                           job_off, job_cnt, pass_job, pass_tp, counts, n_experts, nchunk, bank,
+                           pass_tok);
+        hipLaunchKernelGGL(gather_place_kernel, dim3(nchunk), dim3(GM_C), 0, st, perm, hist, idx, N,
+                           n_experts, nchunk);
+    } else {
+        hipLaunchKernelGGL(gather_kernel, dim3(1), dim3(1024), 0, st, offsets, perm, job_expert,
+                           job_off, job_cnt, pass_job, pass_tp, counts, idx, N, n_experts, bank,
+                           pass_tok);
+    }
     K3K_LAUNCH_CHECK("gather launch");
     return 0;
+}
+
+extern "C" size_t k3k_gather_scratch(int T, int topk, int n_experts)
+{
+    const long N = (long)T * topk;
+    if (N <= GM_MIN || n_experts > G_WCNT_E) return 0;
+    return (size_t)((N + GM_C - 1) / GM_C) * (size_t)n_experts;
 }
 
 extern "C" int k3k_combine(float *out, const float *contrib, const float *wt, const int *idx,

@@ -160,15 +160,18 @@ int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, cons
                      const K3kExc *exc, void *stream);
 
 /* ---- gather / combine -------------------------------------------------------------- */
-/* Stable expert-major gather of the T*topk assignments in idx (one workgroup). Outputs:
+/* Stable expert-major gather of the T*topk assignments in idx. Outputs:
  *   offsets[n_experts+1]; perm[T*topk]: sorted position -> assignment t*topk+j, experts
  *   ascending and (t, j) ascending inside one expert; jobs = experts with at least one
  *   assignment and a present bank entry, ascending: job_expert/job_off/job_cnt; passes
  *   of up to pass_tok tokens of one job: pass_job/pass_tp; counts[0] = n_jobs,
  *   counts[1] = n_passes, counts[2] = assignments whose bank entry is NULL (dropped). */
 int k3k_gather(int *offsets, int *perm, int *job_expert, int *job_off, int *job_cnt,
-               int *pass_job, int *pass_tp, int *counts, const int *idx, int T, int topk,
-               int n_experts, const void *bank, int pass_tok, void *stream);
+               int *pass_job, int *pass_tp, int *counts, int *hist, const int *idx, int T,
+               int topk, int n_experts, const void *bank, int pass_tok, void *stream);
+/* Ints of scratch (hist) that lets k3k_gather spread a large batch over many workgroups;
+ * 0: one workgroup (hist may be NULL). */
+size_t k3k_gather_scratch(int T, int topk, int n_experts);
 /* out[t][i] = 0 + sum_j wt[t][j] * contrib[t*topk+j][i], j ascending, skipping
  * assignments whose expert index is outside [0, n_experts) or whose bank entry has a
  * NULL pointer (bank == NULL: every in-range expert is present). */

@@ -411,6 +411,51 @@ def test_moe_device_prefill_96_passes(gpu, orc, k3):
     assert np.abs(out - rows_out).max() <= 1e-6 * np.abs(rows_out).max()
 
 
+@pytest.mark.parametrize("prec", [0, 1])
+def test_moe_device_gather_many_workgroups(gpu, orc, k3, prec):
+    """More than 4096 assignments take the gather over many workgroups (per-chunk counts,
+    one scan, per-chunk stable placement; the last chunk ragged): perm and offsets equal to
+    a stable argsort of idx, a missing expert's assignments counted as drops and left out
+    of the output, experts without tokens, and outputs against the oracle's."""
+    E, I, N, K, T = 512, 512, 64, 8, 700
+    say(f"case: gather over many workgroups T={T} K={K} N={N} prec={prec}")
+    rng = np.random.default_rng(83)
+    bank = [k3.gen_expert(E, I, 89, e) for e in range(N)]
+    W = (rng.standard_normal((N, E)) * 0.05).astype(np.float32)
+    W[[3, 40]] *= 0.0
+    bias = np.zeros(N, np.float32)
+    bias[[3, 40]] = -1e30                        # never chosen: experts without tokens
+    X = rng.standard_normal((T, E)).astype(np.float32)
+    _, idx0, _ = orc.moe_routed(X, W, bias, bank, E, I, K)
+    victim = int(np.bincount(idx0.ravel(), minlength=N).argmax())
+    holed = list(bank)
+    holed[victim] = None
+    b = gpu.DevBank(holed, E, I, gpu.K3D_LAYOUT_TILED)
+    try:
+        out, idx, wt, perm, off, drops = gpu.moe_routed_device(b, X, W, bias, K, prec=prec, inter=I)
+    finally:
+        b.free()
+    assert np.array_equal(idx, idx0)
+    cnt = np.bincount(idx.ravel(), minlength=N)
+    assert idx.size > 4096 and cnt[3] == 0 and cnt[40] == 0
+    p2, off2 = stable_gather(idx0, N)
+    assert np.array_equal(perm, p2) and np.array_equal(off, off2)
+    assert drops == int(cnt[victim]) > 0
+    o2, _, _ = orc.moe_routed(X, W, bias, bank, E, I, K)
+    for tk in np.nonzero((idx == victim).any(axis=1))[0]:     # the victim contributes nothing
+        acc = np.zeros(E, np.float32)
+        for j in range(K):
+            e = int(idx[tk, j])
+            if e != victim:
+                acc = acc + np.float32(wt[tk, j]) * orc.expert_ffn(X[tk], bank[e], E, I, act=1, wt=1.0)
+        o2[tk] = acc
+    if prec == 0:
+        for tk in range(T):
+            assert max_err_rel_inf(out[tk], o2[tk]) <= TOL, tk
+    else:
+        assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
+
+
 def test_moe_device_prefill_48_passes(gpu, orc, k3):
     """Large prefill batches on a tiled bank (>= 32 tokens per expert on average) run
     48-token passes with K staged 256 columns at a time: routing exact, outputs within 2e-2
