@@ -1075,7 +1075,7 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
  *  3. gather_place_kernel: each chunk ranks its assignments stably (ballots inside a wave,
  *     per-wave counts across waves) from those positions.
  * perm comes out identical to the one-workgroup kernel's. */
-constexpr int GM_C = 512, GM_MIN = 4096;
+constexpr int GM_C = 512, GM_MIN = 2048;
 
 __global__ __launch_bounds__(GM_C) void gather_hist_kernel(int *hist, const int *idx, int N,
                                                            int n_experts, int nchunk)

@@ -413,7 +413,7 @@ def test_moe_device_prefill_96_passes(gpu, orc, k3):
 
 @pytest.mark.parametrize("prec", [0, 1])
 def test_moe_device_gather_many_workgroups(gpu, orc, k3, prec):
-    """More than 4096 assignments take the gather over many workgroups (per-chunk counts,
+    """More than 2048 assignments take the gather over many workgroups (per-chunk counts,
     one scan, per-chunk stable placement; the last chunk ragged): perm and offsets equal to
     a stable argsort of idx, a missing expert's assignments counted as drops and left out
     of the output, experts without tokens, and outputs against the oracle's."""
@@ -437,7 +437,7 @@ def test_moe_device_gather_many_workgroups(gpu, orc, k3, prec):
         b.free()
     assert np.array_equal(idx, idx0)
     cnt = np.bincount(idx.ravel(), minlength=N)
-    assert idx.size > 4096 and cnt[3] == 0 and cnt[40] == 0
+    assert idx.size > 2048 and cnt[3] == 0 and cnt[40] == 0
     p2, off2 = stable_gather(idx0, N)
     assert np.array_equal(perm, p2) and np.array_equal(off, off2)
     assert drops == int(cnt[victim]) > 0
