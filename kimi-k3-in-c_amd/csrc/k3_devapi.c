@@ -281,8 +281,9 @@ int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const
 typedef struct {
     uint16_t *xhi, *xlo, *ahi, *alo;
     int *offsets, *perm, *job_expert, *job_off, *job_cnt, *pass_job, *pass_tp, *counts, *ghist;
+    int *pass_job2, *pass_tp2;
     float *contrib;
-    int max_passes;
+    int max_passes, max_passes2;
 } MoeWs;
 
 /* Tokens per expert pass. The LDS-staged expert kernels need both matrix widths to be
@@ -301,6 +302,16 @@ static int moe_pass_tok(int T, int hidden, int inter, int n_experts, int topk, i
     if (prec == 1 && layout == K3D_LAYOUT_TILED && (long)T * topk >= 32L * n_experts) return 48;
     if (prec == 1 && (long)T * topk >= 8L * n_experts) return 32;
     return 8;
+}
+
+/* Batches that run 32-token passes on a tiled bank (8-32 tokens per expert on average) give
+ * the experts holding more than 32 assignments -- the hot ones of a skewed routing -- the
+ * prefill kernel's 96-token passes instead (a second pass list): their weights stream once
+ * per 96 tokens rather than per 32. */
+#define MOE_PASS_TOK2 96
+static int moe_pass_tok2(int pass_tok, int layout, int prec)
+{
+    return pass_tok == 32 && layout == K3D_LAYOUT_TILED && prec == 1 ? MOE_PASS_TOK2 : 0;
 }
 
 /* The decode path (k3k_mx_decode): at most 16 assignments, widths multiples of 512 up to
@@ -329,6 +340,11 @@ static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n
     w->job_cnt = (int *)take(c, (size_t)maxjobs * 4);
     w->pass_job = (int *)take(c, (size_t)w->max_passes * 4);
     w->pass_tp = (int *)take(c, (size_t)w->max_passes * 4);
+    /* second list (one-term activations): experts of more than 32 assignments, each pass
+     * of up to 96 tokens -- at most N / 96 full passes plus one per such expert */
+    w->max_passes2 = prec == 1 ? (int)(N / MOE_PASS_TOK2 + N / 33 + 2) : 0;
+    w->pass_job2 = prec == 1 ? (int *)take(c, (size_t)w->max_passes2 * 4) : NULL;
+    w->pass_tp2 = prec == 1 ? (int *)take(c, (size_t)w->max_passes2 * 4) : NULL;
     w->counts = (int *)take(c, 16);
     {
         const size_t gs = k3k_gather_scratch(T, topk, n_experts);
@@ -387,7 +403,8 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
          * the gather runs only when its permutation is asked for */
         if ((perm_out || offsets_out) &&
             k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
-                       w->counts, w->ghist, idx, T, topk, n_experts, bank, pass_tok, stream))
+                       NULL, NULL, w->counts, w->ghist, idx, T, topk, n_experts, bank, pass_tok, 0,
+                       stream))
             return fail("gather");
         k3k_prof_mark(stream, K3D_STAGE_GATHER);
         K3kMxArgs a;
@@ -422,8 +439,10 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
         return 0;
     }
     if (k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
+    const int pass_tok2 = moe_pass_tok2(pass_tok, layout, prec);
     if (k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
-                   w->counts, w->ghist, idx, T, topk, n_experts, bank, pass_tok, stream))
+                   w->pass_job2, w->pass_tp2, w->counts, w->ghist, idx, T, topk, n_experts, bank,
+                   pass_tok, pass_tok2, stream))
         return fail("gather");
     k3k_prof_mark(stream, K3D_STAGE_GATHER);
     K3kMxArgs a;
@@ -452,7 +471,15 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     a.rows = inter;
     a.K = hidden;
     a.n_xrows = T;
+    /* the second pass list: same jobs, the prefill kernel's passes */
+    K3kMxArgs a2 = a;
+    a2.pass_tok = pass_tok2;
+    a2.pass_job = w->pass_job2;
+    a2.pass_tp = w->pass_tp2;
+    a2.n_passes = w->counts + 3;
+    a2.max_passes = w->max_passes2;
     if (k3k_mx_gemm(K3K_MX_GATEUP, &a, stream)) return fail("mx_gemm gateup");
+    if (pass_tok2 && k3k_mx_gemm(K3K_MX_GATEUP, &a2, stream)) return fail("mx_gemm gateup (96)");
     k3k_prof_mark(stream, K3D_STAGE_GATEUP);
     /* down: K = inter, rows = hidden, activations are the assignments */
     a.xhi = w->ahi;
@@ -462,6 +489,15 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     a.K = inter;
     a.n_xrows = T * topk;
     if (k3k_mx_gemm(K3K_MX_DOWN, &a, stream)) return fail("mx_gemm down");
+    if (pass_tok2) {
+        a2.xhi = a.xhi;
+        a2.xlo = a.xlo;
+        a2.out = a.out;
+        a2.rows = a.rows;
+        a2.K = a.K;
+        a2.n_xrows = a.n_xrows;
+        if (k3k_mx_gemm(K3K_MX_DOWN, &a2, stream)) return fail("mx_gemm down (96)");
+    }
     k3k_prof_mark(stream, K3D_STAGE_DOWN);
     if (k3k_combine(out, w->contrib, wt, idx, bank, n_experts, T, topk, hidden, stream)) return fail("combine");
     k3k_prof_mark(stream, K3D_STAGE_COMBINE);

@@ -944,32 +944,37 @@ __device__ __forceinline__ int block_scan_excl(int v, int *wtot, int lane, int w
 }
 
 /* From per-expert counts cnt[] (LDS): offsets[], fill[] (= offsets, in LDS), the jobs,
- * the passes and counts[0..2], as the gather's header describes. Called by all 1024
- * threads; ends with a barrier. */
+ * the passes and counts[0..3], as the gather's header describes. With pass_tok2 > 0 the
+ * experts holding more than pass_tok assignments get passes of pass_tok2 in the second
+ * list instead. Called by all 1024 threads; ends with a barrier. */
 __device__ void gather_plan(const int *cnt, int *fill, int *wtot, int *offsets, int *job_expert,
-                            int *job_off, int *job_cnt, int *pass_job, int *pass_tp, int *counts,
-                            int n_experts, const void *bank, int pass_tok)
+                            int *job_off, int *job_cnt, int *pass_job, int *pass_tp,
+                            int *pass_job2, int *pass_tp2, int *counts, int n_experts,
+                            const void *bank, int pass_tok, int pass_tok2)
 {
+    auto big = [&](int c) { return pass_tok2 > 0 && c > pass_tok; };
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     /* per-thread sums over a contiguous expert range, then workgroup scans */
     const int per = (n_experts + 1023) / 1024;
     const int ea = tid * per, eb = min(n_experts, ea + per);
-    int local = 0, ljobs = 0, lpass = 0, ldrop = 0;
+    int local = 0, ljobs = 0, lpass = 0, lpass2 = 0, ldrop = 0;
     for (int e = ea; e < eb; e++) {
         local += cnt[e];
         if (cnt[e] > 0) {
             if (expert_present(bank, e)) {
                 ljobs++;
-                lpass += (cnt[e] + pass_tok - 1) / pass_tok;
+                if (big(cnt[e])) lpass2 += (cnt[e] + pass_tok2 - 1) / pass_tok2;
+                else lpass += (cnt[e] + pass_tok - 1) / pass_tok;
             } else {
                 ldrop += cnt[e];
             }
         }
     }
-    int tot_a, tot_b, tot_c, tot_d;
+    int tot_a, tot_b, tot_c, tot_d, tot_e;
     int run = block_scan_excl(local, wtot, lane, wv, tot_a);
     int jrun = block_scan_excl(ljobs, wtot, lane, wv, tot_b);
     int prun = block_scan_excl(lpass, wtot, lane, wv, tot_c);
+    int prun2 = block_scan_excl(lpass2, wtot, lane, wv, tot_e);
     (void)block_scan_excl(ldrop, wtot, lane, wv, tot_d);
     for (int e = ea; e < eb; e++) {
         offsets[e] = run;
@@ -978,12 +983,21 @@ __device__ void gather_plan(const int *cnt, int *fill, int *wtot, int *offsets, 
             job_expert[jrun] = e;
             job_off[jrun] = run;
             job_cnt[jrun] = cnt[e];
-            const int np = (cnt[e] + pass_tok - 1) / pass_tok;
-            for (int p = 0; p < np; p++) {
-                pass_job[prun + p] = jrun;
-                pass_tp[prun + p] = p;
+            if (big(cnt[e])) {
+                const int np = (cnt[e] + pass_tok2 - 1) / pass_tok2;
+                for (int p = 0; p < np; p++) {
+                    pass_job2[prun2 + p] = jrun;
+                    pass_tp2[prun2 + p] = p;
+                }
+                prun2 += np;
+            } else {
+                const int np = (cnt[e] + pass_tok - 1) / pass_tok;
+                for (int p = 0; p < np; p++) {
+                    pass_job[prun + p] = jrun;
+                    pass_tp[prun + p] = p;
+                }
+                prun += np;
             }
-            prun += np;
             jrun++;
         }
         run += cnt[e];
@@ -993,15 +1007,17 @@ __device__ void gather_plan(const int *cnt, int *fill, int *wtot, int *offsets, 
         counts[0] = tot_b;
         counts[1] = tot_c;
         counts[2] = tot_d;
+        counts[3] = tot_e;
     }
     __syncthreads();
 }
 
 __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, int *job_expert,
                                                       int *job_off, int *job_cnt, int *pass_job,
-                                                      int *pass_tp, int *counts, const int *idx,
-                                                      int N, int n_experts, const void *bank,
-                                                      int pass_tok)
+                                                      int *pass_tp, int *pass_job2, int *pass_tp2,
+                                                      int *counts, const int *idx, int N,
+                                                      int n_experts, const void *bank,
+                                                      int pass_tok, int pass_tok2)
 {
     __shared__ int cnt[G_MAXE];
     __shared__ int fill[G_MAXE];
@@ -1015,8 +1031,8 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
         if (e >= 0 && e < n_experts) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    gather_plan(cnt, fill, wtot, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp, counts,
-                n_experts, bank, pass_tok);
+    gather_plan(cnt, fill, wtot, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp,
+                pass_job2, pass_tp2, counts, n_experts, bank, pass_tok, pass_tok2);
 
     /* stable placement */
     const bool wide = n_experts > G_WCNT_E;
@@ -1095,8 +1111,10 @@ __global__ __launch_bounds__(GM_C) void gather_hist_kernel(int *hist, const int 
 
 __global__ __launch_bounds__(1024) void gather_scan_kernel(int *hist, int *offsets, int *job_expert,
                                                            int *job_off, int *job_cnt, int *pass_job,
-                                                           int *pass_tp, int *counts, int n_experts,
-                                                           int nchunk, const void *bank, int pass_tok)
+                                                           int *pass_tp, int *pass_job2,
+                                                           int *pass_tp2, int *counts, int n_experts,
+                                                           int nchunk, const void *bank, int pass_tok,
+                                                           int pass_tok2)
 {
     __shared__ int cnt[G_WCNT_E];
     __shared__ int fill[G_WCNT_E];
@@ -1111,8 +1129,8 @@ __global__ __launch_bounds__(1024) void gather_scan_kernel(int *hist, int *offse
         cnt[e] = t;
     }
     __syncthreads();
-    gather_plan(cnt, fill, wtot, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp, counts,
-                n_experts, bank, pass_tok);
+    gather_plan(cnt, fill, wtot, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp,
+                pass_job2, pass_tp2, counts, n_experts, bank, pass_tok, pass_tok2);
     for (int e = tid; e < n_experts; e += 1024) {
         int run = fill[e];
 #pragma unroll 16
@@ -1425,11 +1443,13 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
 }
 
 extern "C" int k3k_gather(int *offsets, int *perm, int *job_expert, int *job_off, int *job_cnt,
-                          int *pass_job, int *pass_tp, int *counts, int *hist, const int *idx,
-                          int T, int topk, int n_experts, const void *bank, int pass_tok,
-                          void *stream)
+                          int *pass_job, int *pass_tp, int *pass_job2, int *pass_tp2, int *counts,
+                          int *hist, const int *idx, int T, int topk, int n_experts,
+                          const void *bank, int pass_tok, int pass_tok2, void *stream)
 {
     if (n_experts > G_MAXE) return k3k_fail("gather: too many experts", hipErrorInvalidValue);
+    if (pass_tok2 > 0 && (!pass_job2 || !pass_tp2))
+        return k3k_fail("gather: second pass list missing", hipErrorInvalidValue);
     hipStream_t st = (hipStream_t)stream;
     const int N = T * topk;
     const size_t need = k3k_gather_scratch(T, topk, n_experts);
@@ -1438,14 +1458,14 @@ extern "C" int k3k_gather(int *offsets, int *perm, int *job_expert, int *job_off
         hipLaunchKernelGGL(gather_hist_kernel, dim3(nchunk), dim3(GM_C), 0, st, hist, idx, N,
                            n_experts, nchunk);
         hipLaunchKernelGGL(gather_scan_kernel, dim3(1), dim3(1024), 0, st, hist, offsets, job_expert,
-                           job_off, job_cnt, pass_job, pass_tp, counts, n_experts, nchunk, bank,
-                           pass_tok);
+                           job_off, job_cnt, pass_job, pass_tp, pass_job2, pass_tp2, counts,
+                           n_experts, nchunk, bank, pass_tok, pass_tok2);
         hipLaunchKernelGGL(gather_place_kernel, dim3(nchunk), dim3(GM_C), 0, st, perm, hist, idx, N,
                            n_experts, nchunk);
     } else {
         hipLaunchKernelGGL(gather_kernel, dim3(1), dim3(1024), 0, st, offsets, perm, job_expert,
-                           job_off, job_cnt, pass_job, pass_tp, counts, idx, N, n_experts, bank,
-                           pass_tok);
+                           job_off, job_cnt, pass_job, pass_tp, pass_job2, pass_tp2, counts, idx, N,
+                           n_experts, bank, pass_tok, pass_tok2);
     }
     K3K_LAUNCH_CHECK("gather launch");
     return 0;

@@ -165,10 +165,13 @@ int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, cons
  *   ascending and (t, j) ascending inside one expert; jobs = experts with at least one
  *   assignment and a present bank entry, ascending: job_expert/job_off/job_cnt; passes
  *   of up to pass_tok tokens of one job: pass_job/pass_tp; counts[0] = n_jobs,
- *   counts[1] = n_passes, counts[2] = assignments whose bank entry is NULL (dropped). */
+ *   counts[1] = n_passes, counts[2] = assignments whose bank entry is NULL (dropped).
+ *   pass_tok2 > 0: jobs of more than pass_tok assignments are split into passes of up to
+ *   pass_tok2 tokens in pass_job2/pass_tp2 instead, counts[3] = their number (else 0). */
 int k3k_gather(int *offsets, int *perm, int *job_expert, int *job_off, int *job_cnt,
-               int *pass_job, int *pass_tp, int *counts, int *hist, const int *idx, int T,
-               int topk, int n_experts, const void *bank, int pass_tok, void *stream);
+               int *pass_job, int *pass_tp, int *pass_job2, int *pass_tp2, int *counts,
+               int *hist, const int *idx, int T, int topk, int n_experts, const void *bank,
+               int pass_tok, int pass_tok2, void *stream);
 /* Ints of scratch (hist) that lets k3k_gather spread a large batch over many workgroups;
  * 0: one workgroup (hist may be NULL). */
 size_t k3k_gather_scratch(int T, int topk, int n_experts);

@@ -456,6 +456,40 @@ def test_moe_device_gather_many_workgroups(gpu, orc, k3, prec):
         assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
 
 
+def test_moe_device_mixed_passes(gpu, orc, k3):
+    """Moderate batches on a tiled bank (8-32 tokens per expert on average) run 32-token
+    passes, except for the experts holding more than 32 assignments, which get the prefill
+    kernel's 96-token passes from a second pass list: three biased experts take every token
+    (100 each: two passes, the second ragged), the rest a few each. Routing exact, outputs
+    within 2e-2 relative of the oracle and equal to the row-major bank's (32-token passes
+    throughout, the same K order per token)."""
+    E, I, N, K, T = 1024, 512, 16, 4, 100
+    say(f"case: mixed pass lists E={E} I={I} N={N} K={K} T={T}")
+    rng = np.random.default_rng(97)
+    bank = [k3.gen_expert(E, I, 101, e) for e in range(N)]
+    W = (rng.standard_normal((N, E)) * 0.05).astype(np.float32)
+    bias = np.zeros(N, np.float32)
+    bias[[0, 6, 13]] = 1.0
+    X = rng.standard_normal((T, E)).astype(np.float32)
+    res = {}
+    for layout in (gpu.K3D_LAYOUT_ROWS, gpu.K3D_LAYOUT_TILED):
+        b = gpu.DevBank(bank, E, I, layout)
+        try:
+            res[layout] = gpu.moe_routed_device(b, X, W, bias, K, prec=1, inter=I)
+        finally:
+            b.free()
+    out, idx, wt, perm, off, drops = res[gpu.K3D_LAYOUT_TILED]
+    o2, i2, w2 = orc.moe_routed(X, W, bias, bank, E, I, K)
+    assert np.array_equal(idx, i2)
+    cnt = np.bincount(idx.ravel(), minlength=N)
+    assert (cnt[[0, 6, 13]] == T).all() and cnt[[e for e in range(N) if e not in (0, 6, 13)]].max() <= 32
+    p2, off2 = stable_gather(i2, N)
+    assert np.array_equal(perm, p2) and np.array_equal(off, off2)
+    assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
+    rows_out = np.asarray(res[gpu.K3D_LAYOUT_ROWS][0])
+    assert np.abs(out - rows_out).max() <= 1e-6 * np.abs(rows_out).max()
+
+
 def test_moe_device_prefill_48_passes(gpu, orc, k3):
     """Large prefill batches on a tiled bank (>= 32 tokens per expert on average) run
     48-token passes with K staged 256 columns at a time: routing exact, outputs within 2e-2
