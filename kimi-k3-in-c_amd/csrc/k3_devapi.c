@@ -414,6 +414,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
         a.idx = idx;
         a.n_assign = T * topk;
         a.drops = w->counts + 2;
+        a.n_experts = n_experts;
         a.topk = topk;
         a.act = act;
         a.b1 = b1;

@@ -464,13 +464,25 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
     const int tw = tg * TPW + wv % TPW, ks = wv / TPW;
     const int tile = min(tw, ntile - 1);                    /* past the last tile: discarded */
     const int c0 = ks * nchunk / KS, c1 = (ks + 1) * nchunk / KS;
-    if (MODE == K3K_MX_GATEUP && blockIdx.x == 0 && tid == 0) {
-        int nd = 0;
-        for (int i = 0; i < a.n_assign; i++)
-            nd += reinterpret_cast<const ExpertQDev *>(a.bank)[a.idx[i]].p1 == nullptr;
-        *a.drops = nd;
+    const ExpertQDev *bank = reinterpret_cast<const ExpertQDev *>(a.bank);
+    auto present = [&](int e) {
+        if (e < 0 || e >= a.n_experts) return false;
+        const ExpertQDev b = bank[e];
+        return b.p1 && b.s1 && b.p3 && b.s3 && b.p2 && b.s2;
+    };
+    if (MODE == K3K_MX_GATEUP) {
+        if (blockIdx.x == 0 && tid == 0) {
+            int nd = 0;
+            for (int i = 0; i < a.n_assign; i++) {
+                const int e = a.idx[i];
+                nd += e >= 0 && e < a.n_experts && !present(e);
+            }
+            *a.drops = nd;
+        }
     }
-    const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[a.idx[asg]];
+    const int eix = a.idx[asg];
+    ExpertQDev q = {};
+    if (eix >= 0 && eix < a.n_experts) q = bank[eix];
     const uint8_t *pm[NM], *sm[NM];
     if (MODE == K3K_MX_GATEUP) {
         pm[0] = q.p1; sm[0] = q.s1;
@@ -478,7 +490,7 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
     } else {
         pm[0] = q.p2; sm[0] = q.s2;
     }
-    if (pm[0] == nullptr) return;                           /* dropped expert */
+    if (pm[0] == nullptr) return;                           /* dropped or out of range */
     /* activation loads first: they return while the weights stream */
     float4 xv[XPT];
     uint4 hv[XPT];

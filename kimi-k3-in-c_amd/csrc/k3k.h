@@ -89,6 +89,7 @@ typedef struct {
     const int *idx;
     int n_assign;
     int *drops;
+    int n_experts;                      /* idx outside [0, n_experts): absent */
 } K3kMxArgs;
 
 int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
