@@ -18,8 +18,10 @@ struct ExpertQDev {
 
 __device__ __forceinline__ bool expert_present(const void *bank, int e)
 {
+    /* all six pointers tested without short-circuit, so they load together */
     const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(bank)[e];
-    return q.p1 && q.s1 && q.p3 && q.s3 && q.p2 && q.s2;
+    return (q.p1 != nullptr) & (q.s1 != nullptr) & (q.p3 != nullptr) & (q.s3 != nullptr) &
+           (q.p2 != nullptr) & (q.s2 != nullptr);
 }
 
 /* ---- fp32 -> bf16 hi/lo ----------------------------------------------------------- */
@@ -1180,35 +1182,30 @@ __global__ __launch_bounds__(GM_C) void gather_place_kernel(int *perm, const int
 /* ---- combine: out[t] = 0 + sum_j wt[t][j] * contrib[t*topk + j], j ascending -------
  * A slot contributes nothing when its expert index is out of range or its bank entry is
  * absent. Every slot's row is loaded (it is valid memory either way) and the sum selects,
- * so that all topk loads are in flight together. */
+ * so that all topk loads are in flight together; the first JB slots' rows are loaded
+ * before the slots' validity (idx, then the bank entry) is known, so the two chains of
+ * loads overlap. */
+template <bool VEC>
 __global__ __launch_bounds__(256) void combine_kernel(float *out, const float *contrib,
                                                      const float *wt, const int *idx,
                                                      const void *bank, int n_experts, int T,
-                                                     int topk, int E, int vec)
+                                                     int topk, int E)
 {
+    constexpr int JB = 8;
     __shared__ float wsl[K3_MAX_TOPK_DEV];
     __shared__ int vsl[K3_MAX_TOPK_DEV];
     const int t = blockIdx.y;
-    if (threadIdx.x < topk) {
-        const int a = t * topk + threadIdx.x;
-        const int e = idx[a];
-        const bool ok = e >= 0 && e < n_experts && (!bank || expert_present(bank, e));
-        vsl[threadIdx.x] = ok;
-        wsl[threadIdx.x] = wt[a];
-    }
-    __syncthreads();
     const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
-    if (i >= E) return;
-    const float *c0 = contrib + (size_t)t * topk * E + i;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    constexpr int JB = 8;
-    for (int j0 = 0; j0 < topk; j0 += JB) {
-        float cv[JB][4];
+    const bool active = i < E;
+    const float *c0 = contrib + (size_t)t * topk * E + (active ? i : 0);
+    float cv[JB][4];
+    auto load = [&](int j0) {
 #pragma unroll
         for (int jj = 0; jj < JB; jj++) {
             const int j = min(j0 + jj, topk - 1);
             const float *c = c0 + (size_t)j * E;
-            if (vec) {
+            if (VEC) {
+                /* unconditional: c0 points at column 0 for threads past the row */
                 const float4 v = *reinterpret_cast<const float4 *>(c);
                 cv[jj][0] = v.x; cv[jj][1] = v.y; cv[jj][2] = v.z; cv[jj][3] = v.w;
             } else {
@@ -1216,6 +1213,24 @@ __global__ __launch_bounds__(256) void combine_kernel(float *out, const float *c
                 for (int q = 0; q < 4; q++) cv[jj][q] = i + q < E ? c[q] : 0.0f;
             }
         }
+    };
+    /* the slot's expert and weight first, then the rows, then the bank entry */
+    int e = -1;
+    float ws = 0.0f;
+    if (threadIdx.x < topk) {
+        e = idx[t * topk + threadIdx.x];
+        ws = wt[t * topk + threadIdx.x];
+    }
+    load(0);
+    if (threadIdx.x < topk) {
+        vsl[threadIdx.x] = e >= 0 && e < n_experts && (!bank || expert_present(bank, e));
+        wsl[threadIdx.x] = ws;
+    }
+    __syncthreads();
+    if (!active) return;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j0 = 0; j0 < topk; j0 += JB) {
+        if (j0 > 0) load(j0);
 #pragma unroll
         for (int jj = 0; jj < JB; jj++) {
             const int j = j0 + jj;
@@ -1227,7 +1242,7 @@ __global__ __launch_bounds__(256) void combine_kernel(float *out, const float *c
         }
     }
     float *o = out + (size_t)t * E + i;
-    if (vec) *reinterpret_cast<float4 *>(o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    if (VEC) *reinterpret_cast<float4 *>(o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     else
         for (int q = 0; q < 4; q++)
             if (i + q < E) o[q] = acc[q];
@@ -1485,8 +1500,12 @@ extern "C" int k3k_combine(float *out, const float *contrib, const float *wt, co
     if (topk > K3_MAX_TOPK_DEV) return k3k_fail("combine: topk too large", hipErrorInvalidValue);
     const int vec = (E % 4 == 0) && ((((uintptr_t)out) | ((uintptr_t)contrib)) % 16 == 0);
     dim3 grid(((E + 3) / 4 + 255) / 256, T);
-    hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, (hipStream_t)stream, out, contrib, wt,
-                       idx, bank, n_experts, T, topk, E, vec);
+    if (vec)
+        hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, out, contrib,
+                           wt, idx, bank, n_experts, T, topk, E);
+    else
+        hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, out, contrib,
+                           wt, idx, bank, n_experts, T, topk, E);
     K3K_LAUNCH_CHECK("combine launch");
     return 0;
 }
