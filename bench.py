@@ -314,11 +314,58 @@ def cpu_baseline(T_sample=8, budget_s=10.0):
         impl.moe_routed(X, W, None, bank, E, I, K)
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
+    one = single_thread_rate(impl, X[:1], W, bank)
     return {"value": round(T_sample / med, 3), "unit": "tokens/s", "cores": threads,
             "kind": kind,
             "sample": f"{T_sample} tokens of the batch-64 decode layer (router + 8 experts each, "
                       f"SiLU), {len(times)} reps, median; spread {min(times):.3f}-{max(times):.3f} s",
-            "ms_per_token": round(med / T_sample * 1e3, 2)}
+            "ms_per_token": round(med / T_sample * 1e3, 2),
+            "one_thread": one, "host": host_description()}
+
+
+def single_thread_rate(impl, X1, W, bank, reps=3):
+    """The same composition on one OpenMP thread (one token, median of reps), through the
+    process's libgomp; the thread count is restored afterwards. None if libgomp cannot be
+    reached."""
+    import ctypes
+    try:
+        gomp = ctypes.CDLL("libgomp.so.1")
+    except OSError:
+        return None
+    prev = gomp.omp_get_max_threads()
+    gomp.omp_set_num_threads(1)
+    try:
+        impl.moe_routed(X1, W, None, bank, E, I, K)           # warm-up
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            impl.moe_routed(X1, W, None, bank, E, I, K)
+            ts.append(time.perf_counter() - t0)
+    finally:
+        gomp.omp_set_num_threads(prev)
+    med = float(np.median(ts))
+    return {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": 1,
+            "sample": f"1 token, {reps} reps, median; spread {min(ts):.3f}-{max(ts):.3f} s"}
+
+
+def host_description():
+    """CPU model, AVX-512 presence and the C library version of the host the CPU numbers
+    come from."""
+    import platform
+    model, avx512 = None, None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if model is None and line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                if avx512 is None and line.startswith("flags"):
+                    avx512 = " avx512f " in f" {line.split(':', 1)[1].strip()} "
+                if model is not None and avx512 is not None:
+                    break
+    except OSError:
+        pass
+    return {"cpu": model, "logical_cpus": os.cpu_count(), "avx512f": avx512,
+            "libc": " ".join(platform.libc_ver())}
 
 
 def measured_traffic():
