@@ -479,8 +479,11 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     a2.pass_tp = w->pass_tp2;
     a2.n_passes = w->counts + 3;
     a2.max_passes = w->max_passes2;
+    /* the second list's gate/up and down run on a side stream beside the first's */
+    void *side = NULL;
+    if (pass_tok2 && k3k_fork(stream, &side)) return fail("fork");
     if (k3k_mx_gemm(K3K_MX_GATEUP, &a, stream)) return fail("mx_gemm gateup");
-    if (pass_tok2 && k3k_mx_gemm(K3K_MX_GATEUP, &a2, stream)) return fail("mx_gemm gateup (96)");
+    if (pass_tok2 && k3k_mx_gemm(K3K_MX_GATEUP, &a2, side)) return fail("mx_gemm gateup (96)");
     k3k_prof_mark(stream, K3D_STAGE_GATEUP);
     /* down: K = inter, rows = hidden, activations are the assignments */
     a.xhi = w->ahi;
@@ -497,7 +500,8 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
         a2.rows = a.rows;
         a2.K = a.K;
         a2.n_xrows = a.n_xrows;
-        if (k3k_mx_gemm(K3K_MX_DOWN, &a2, stream)) return fail("mx_gemm down (96)");
+        if (k3k_mx_gemm(K3K_MX_DOWN, &a2, side)) return fail("mx_gemm down (96)");
+        if (k3k_join(stream)) return fail("join");
     }
     k3k_prof_mark(stream, K3D_STAGE_DOWN);
     if (k3k_combine(out, w->contrib, wt, idx, bank, n_experts, T, topk, hidden, stream)) return fail("combine");

@@ -143,6 +143,40 @@ extern "C" int k3k_stream_destroy(void *stream)
 }
 
 /* ---- HIP graphs: capture the work enqueued on a stream once, replay it with one launch */
+/* A second stream for work that may run beside the caller's (the hot experts' pass list):
+ * created on first use with the default priority, non-blocking, with two events. Work is
+ * forked after what is already queued on the caller's stream and joined back into it; both
+ * are event waits, so a stream being captured into a graph captures the side work too.
+ * Calls that overlap on different caller streams would share it: the library serialises
+ * on one stream per instance. */
+static hipStream_t g_side = nullptr;
+static hipEvent_t g_fork = nullptr, g_join = nullptr;
+
+extern "C" int k3k_fork(void *stream, void **side)
+{
+    if (k3k_init()) return -1;
+    if (!g_side) {
+        hipError_t e = hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking);
+        if (e != hipSuccess) return k3k_fail("fork: hipStreamCreate", e);
+        e = hipEventCreateWithFlags(&g_fork, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&g_join, hipEventDisableTiming);
+        if (e != hipSuccess) return k3k_fail("fork: hipEventCreate", e);
+    }
+    hipError_t e = hipEventRecord(g_fork, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(g_side, g_fork, 0);
+    if (e != hipSuccess) return k3k_fail("fork", e);
+    *side = g_side;
+    return 0;
+}
+
+extern "C" int k3k_join(void *stream)
+{
+    if (!g_side) return k3k_fail("join without fork", hipErrorInvalidValue);
+    hipError_t e = hipEventRecord(g_join, g_side);
+    if (e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)stream, g_join, 0);
+    return e == hipSuccess ? 0 : k3k_fail("join", e);
+}
+
 extern "C" int k3k_graph_begin(void *stream)
 {
     if (!stream) return k3k_fail("graph capture needs a created stream", hipErrorInvalidValue);

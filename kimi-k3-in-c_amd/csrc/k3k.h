@@ -32,6 +32,10 @@ void *k3k_stream_create(void);
 int k3k_stream_destroy(void *stream);
 int k3k_cu_count(void);
 /* Graph capture of the work enqueued on `stream` (a created stream, not NULL). */
+/* k3k_fork: *side = a second stream that first waits for the work queued on stream;
+ * k3k_join: stream waits for the work queued on the side stream since. */
+int k3k_fork(void *stream, void **side);
+int k3k_join(void *stream);
 int k3k_graph_begin(void *stream);
 int k3k_graph_end(void *stream, void **exec);
 int k3k_graph_launch(void *exec, void *stream);

@@ -293,30 +293,25 @@ def test_router_device_uncertified_logits(gpu, orc, hidden, ntok, scale):
         assert rec[0] >= 2      # both crafted logits went through the reference's chain
 
 
-def test_moe_graph_replay_matches_eager(gpu, small_layer):
-    """The layer captured once in a HIP graph (k3d_graph_*) and replayed with new input
-    contents, with eager work and synchronisation between replays: every replay equals
+def _graph_replay(gpu, bank_list, W, bias, E, I, N, K, T, prec, xs):
+    """Capture the layer once in a HIP graph (k3d_graph_*), replay it with new input
+    contents, with eager work and synchronisation between replays: every replay must equal
     the eager call on the same input, bit for bit."""
     import ctypes as C
-    s = small_layer
-    say("case: graph replay vs eager")
     L = gpu.lib()
-    E, I, N, K, T = s["E"], s["I"], s["N"], s["K"], s["T"]
-    bank = gpu.DevBank(s["bank"], E, I, gpu.K3D_LAYOUT_TILED)
-    rng = np.random.default_rng(77)
-    xs = [rng.standard_normal((T, E)).astype(np.float32) for _ in range(3)]
+    bank = gpu.DevBank(bank_list, E, I, gpu.K3D_LAYOUT_TILED)
     dx = gpu.DevBuf(T * E * 4)
-    dw = gpu.DevBuf(s["W"].nbytes).upload(s["W"])
-    db = gpu.DevBuf(N * 4).upload(s["bias"])
+    dw = gpu.DevBuf(W.nbytes).upload(W)
+    db = gpu.DevBuf(N * 4).upload(bias)
     out, idx, wt = gpu.DevBuf(T * E * 4), gpu.DevBuf(T * K * 4), gpu.DevBuf(T * K * 4)
-    wsb = L.k3d_moe_ws(T, E, I, N, K, 0)
+    wsb = L.k3d_moe_ws(T, E, I, N, K, prec)
     ws = gpu.DevBuf(wsb)
     stream = L.k3d_stream_create()
     assert stream
 
     def call(st):
         gpu.check(L.k3d_moe_routed(out.ptr, idx.ptr, wt.ptr, dx.ptr, T, dw.ptr, db.ptr, bank.table.ptr,
-                                   bank.layout, E, I, N, K, 1, 1.0, gpu.K3_ACT_SILU, 4.0, 25.0, 0,
+                                   bank.layout, E, I, N, K, 1, 1.0, gpu.K3_ACT_SILU, 4.0, 25.0, prec,
                                    ws.ptr, wsb, None, None, None, st), "k3d_moe_routed")
 
     def results():
@@ -335,7 +330,7 @@ def test_moe_graph_replay_matches_eager(gpu, small_layer):
         ex = C.c_void_p()
         gpu.check(L.k3d_graph_end(stream, C.byref(ex)), "graph_end")
         for rep in range(6):
-            i = rep % 3
+            i = rep % len(xs)
             dx.upload(xs[i])
             call(None)                                   # eager work between replays
             gpu.check(L.k3d_sync(None), "sync")
@@ -352,6 +347,30 @@ def test_moe_graph_replay_matches_eager(gpu, small_layer):
             b.free()
         bank.free()
 
+
+def test_moe_graph_replay_matches_eager(gpu, small_layer):
+    """The decode-batch layer (8-token passes, two-term activations) captured in a HIP
+    graph: every replay equals the eager call bit for bit."""
+    s = small_layer
+    say("case: graph replay vs eager")
+    rng = np.random.default_rng(77)
+    xs = [rng.standard_normal((s["T"], s["E"])).astype(np.float32) for _ in range(3)]
+    _graph_replay(gpu, s["bank"], s["W"], s["bias"], s["E"], s["I"], s["N"], s["K"], s["T"], 0, xs)
+
+
+def test_moe_graph_replay_mixed_passes(gpu, k3):
+    """The mixed pass lists (hot experts' 96-token passes on a side stream forked from the
+    caller's and joined back) captured in a HIP graph: every replay equals the eager call
+    bit for bit."""
+    E, I, N, K, T = 1024, 512, 16, 4, 100
+    say("case: graph replay vs eager, mixed pass lists")
+    rng = np.random.default_rng(103)
+    bank = [k3.gen_expert(E, I, 107, e) for e in range(N)]
+    W = (rng.standard_normal((N, E)) * 0.05).astype(np.float32)
+    bias = np.zeros(N, np.float32)
+    bias[[1, 9]] = 1.0
+    xs = [rng.standard_normal((T, E)).astype(np.float32) for _ in range(3)]
+    _graph_replay(gpu, bank, W, bias, E, I, N, K, T, 1, xs)
 
 def test_moe_device_prefill_passes(gpu, orc, k3):
     """Prefill batches (>= 8 tokens per expert on average, bf16 activations) run 32-token
