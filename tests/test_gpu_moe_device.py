@@ -550,11 +550,12 @@ def shared_ref(orc, X, w1, w3, w2, hidden, inter):
     return out
 
 
-@pytest.mark.parametrize("T,prec", [(5, 0), (40, 0), (70, 1)])
+@pytest.mark.parametrize("T,prec", [(5, 0), (40, 0), (70, 1), (300, 1)])
 def test_shared_expert_vs_oracle(gpu, orc, k3, T, prec):
     """The bf16 dense shared expert on the matrix cores against the reference's bf16 GEMV
-    composition: 1e-4 * ||ref||inf with two-term activations, 2e-2 relative with one; the
-    accumulate form adds onto the routed output with one fp32 add."""
+    composition: 1e-4 * ||ref||inf with two-term activations, 2e-2 relative with one (32-
+    token passes, the last one ragged); the accumulate form adds onto the routed output with
+    one fp32 add."""
     hidden, inter = 1024, 512
     say(f"case: shared expert T={T} prec={prec}")
     w1 = k3.gen_bf16_normal(inter * hidden, 101, 0.0, 0.02)
