@@ -117,7 +117,9 @@ int k3d_shared_expert(float *y, int accumulate, const float *x, int T, const uin
                       const uint16_t *w3, const uint16_t *w2, int hidden, int inter, int act,
                       float b1, float b2, int prec, void *ws, size_t ws_bytes, void *stream);
 
-/* The expert half of the layer for a routing already in idx/wt (device). */
+/* The expert half of the layer for a routing already in idx/wt (device). Slots whose
+ * expert index lies outside [0, n_experts), or whose bank entry has a NULL pointer,
+ * contribute nothing; drops_out counts the latter. */
 int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x, int T,
                     const void *bank, int layout, int hidden, int inter, int n_experts, int topk,
                     int act, float b1, float b2, int prec, void *ws, size_t ws_bytes,

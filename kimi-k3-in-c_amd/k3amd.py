@@ -450,6 +450,41 @@ def moe_routed_device(bank, x, router_w, bias, topk, renorm=1, routed_scale=1.0,
                 v.free()
 
 
+def moe_experts_device(bank, x, idx, wt, n_experts, act=K3_ACT_SILU, b1=4.0, b2=25.0, prec=0,
+                       hidden=None, inter=None):
+    """The expert half through k3d_moe_experts for a given routing (idx, wt [T][topk]) on a
+    DevBank: host arrays in, (out [T][hidden], offsets [n+1], drops) out."""
+    L = lib()
+    x = _f32(x).reshape(-1, hidden)
+    T = x.shape[0]
+    idx = np.ascontiguousarray(idx, np.int32).reshape(T, -1)
+    topk = idx.shape[1]
+    wt = _f32(wt).reshape(T, topk)
+    bufs = {}
+    try:
+        bufs["x"] = DevBuf(x.nbytes).upload(x)
+        bufs["idx"] = DevBuf(idx.nbytes).upload(idx)
+        bufs["wt"] = DevBuf(wt.nbytes).upload(wt)
+        bufs["out"] = DevBuf(T * hidden * 4)
+        bufs["perm"] = DevBuf(T * topk * 4)
+        bufs["off"] = DevBuf((n_experts + 1) * 4)
+        bufs["drops"] = DevBuf(4)
+        wsb = L.k3d_moe_ws(T, hidden, inter, n_experts, topk, prec)
+        bufs["ws"] = DevBuf(wsb)
+        check(L.k3d_moe_experts(bufs["out"].ptr, bufs["idx"].ptr, bufs["wt"].ptr, bufs["x"].ptr, T,
+                                bank.table.ptr, bank.layout, hidden, inter, n_experts, topk, act, b1,
+                                b2, prec, bufs["ws"].ptr, wsb, bufs["perm"].ptr, bufs["off"].ptr,
+                                bufs["drops"].ptr, None), "k3d_moe_experts")
+        check(L.k3d_sync(None), "sync")
+        out = bufs["out"].download(np.empty((T, hidden), np.float32))
+        off = bufs["off"].download(np.empty(n_experts + 1, np.int32))
+        drops = int(bufs["drops"].download(np.empty(1, np.int32))[0])
+        return out, off, drops
+    finally:
+        for v in bufs.values():
+            v.free()
+
+
 def router_device(x, W, bias, topk, renorm=1, routed_scale=1.0):
     """k3d_router over T tokens on the device: host arrays in, idx/wt [T][topk] out."""
     L = lib()

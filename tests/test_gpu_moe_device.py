@@ -475,6 +475,42 @@ def test_moe_device_gather_many_workgroups(gpu, orc, k3, prec):
         assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
 
 
+@pytest.mark.parametrize("T,K", [(2, 8), (24, 4)])
+def test_moe_experts_given_routing_invalid_slots(gpu, orc, k3, T, K):
+    """k3d_moe_experts with a caller's routing: slots whose expert index lies outside the
+    bank (-1, N, 1000) and slots of an absent expert contribute nothing; drops counts only
+    the absent expert's slots; the rest equals the oracle's per-slot sum in slot order.
+    (2, 8): 16 assignments, the decode kernels; (24, 4): the gather path."""
+    E, I, N = 1024, 512, 12
+    say(f"case: given routing with invalid slots T={T} K={K}")
+    rng = np.random.default_rng(200 + T)
+    bank = [k3.gen_expert(E, I, 211, e) for e in range(N)]
+    holed = list(bank)
+    holed[7] = None
+    X = rng.standard_normal((T, E)).astype(np.float32)
+    idx = rng.integers(0, N, size=(T, K)).astype(np.int32)
+    idx[0, 1] = -1
+    idx[1, 0] = N
+    idx[-1, K - 1] = 1000
+    idx[0, 0] = 7
+    wt = (rng.random((T, K)) + 0.1).astype(np.float32)
+    b = gpu.DevBank(holed, E, I, gpu.K3D_LAYOUT_TILED)
+    try:
+        out, off, drops = gpu.moe_experts_device(b, X, idx, wt, N, prec=0, hidden=E, inter=I)
+    finally:
+        b.free()
+    valid = (idx >= 0) & (idx < N)
+    assert drops == int(((idx == 7) & valid).sum())
+    assert off[N] == int(valid.sum())
+    for tk in range(T):
+        acc = np.zeros(E, np.float32)
+        for j in range(K):
+            e = int(idx[tk, j])
+            if 0 <= e < N and holed[e] is not None:
+                acc = acc + np.float32(wt[tk, j]) * orc.expert_ffn(X[tk], bank[e], E, I, act=1, wt=1.0)
+        assert max_err_rel_inf(out[tk], acc) <= TOL, tk
+
+
 def test_moe_device_mixed_passes(gpu, orc, k3):
     """Moderate batches on a tiled bank (8-32 tokens per expert on average) run 32-token
     passes, except for the experts holding more than 32 assignments, which get the prefill
