@@ -58,30 +58,44 @@ struct ExcTable {
     int n;
 };
 
+/* The word of the exception bitmap that holds v = -logit's magnitude, or 0 outside the
+ * bitmap's range. A buffer load with no branch around it (an offset past the end reads 0),
+ * so that a caller can issue it early and consume it after other work. */
+__device__ __forceinline__ uint32_t exc_word(float logit, const ExcTable &x)
+{
+    const uint32_t key = __float_as_uint(-logit), mag = key & 0x7fffffffu;
+    const uint32_t bi = mag - x.mmin, w = bi >> 5;
+    const bool in = x.n > 0 && mag >= x.mmin && w < x.mwords;
+    const k3_rsrc r = k3_make_rsrc(x.bits, x.n > 0 ? 8u * x.mwords : 0u);
+    return k3_bload4(r, in ? ((key >> 31) * x.mwords + w) * 4u : 0xfffffff0u);
+}
+
 /* libm-exact score 1/(1+expf(v)), v = -logit: the deterministic correctly rounded
  * candidate, replaced where the host libm's expf differs (exception table built at build
- * time from that libm). One bitmap load decides membership; only members search their
- * bucket (key >> 12, at most 17 pairs). */
-__device__ __forceinline__ float router_score(float logit, const ExcTable &x)
+ * time from that libm). The bitmap word (exc_word) decides membership; only members search
+ * their bucket (key >> 12, at most 17 pairs). */
+__device__ __forceinline__ float router_score_w(float logit, uint32_t word, const ExcTable &x)
 {
     const float v = -logit;
     float E = k3_expf_det(v);
     const uint32_t key = __float_as_uint(v);
     const uint32_t mag = key & 0x7fffffffu;
-    if (x.n > 0 && mag >= x.mmin) {
-        const uint32_t bi = mag - x.mmin, w = bi >> 5;
-        if (w < x.mwords && ((x.bits[(key >> 31) * x.mwords + w] >> (bi & 31)) & 1u)) {
-            const uint32_t bkt = (key >> 12) - x.base;
-            int lo = (int)x.index[bkt], hi = (int)x.index[bkt + 1];
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (x.pairs[2 * mid] < key) lo = mid + 1;
-                else hi = mid;
-            }
-            if (lo < x.n && x.pairs[2 * lo] == key) E = __uint_as_float(x.pairs[2 * lo + 1]);
+    if (x.n > 0 && mag >= x.mmin && ((word >> ((mag - x.mmin) & 31)) & 1u)) {
+        const uint32_t bkt = (key >> 12) - x.base;
+        int lo = (int)x.index[bkt], hi = (int)x.index[bkt + 1];
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (x.pairs[2 * mid] < key) lo = mid + 1;
+            else hi = mid;
         }
+        if (lo < x.n && x.pairs[2 * lo] == key) E = __uint_as_float(x.pairs[2 * lo + 1]);
     }
     return 1.0f / (1.0f + E);
+}
+
+__device__ __forceinline__ float router_score(float logit, const ExcTable &x)
+{
+    return router_score_w(logit, exc_word(logit, x), x);
 }
 
 /* ---- router logits, certified ---------------------------------------------------------
@@ -455,17 +469,18 @@ __device__ __forceinline__ void round_interval(float f, double &lo, double &hi)
  * when that range is one float, or two neighbouring floats whose scores are equal (the
  * choice, score + bias, is then certain too); otherwise scmax is the score of the largest
  * float the logit can be. Non-finite sums come from inf/NaN inputs and propagate alike in
- * any order (ok). */
+ * any order (ok). fword = exc_word((float)Q, exc), loaded by the caller. */
 struct Certified {
     float sc, scmax;
     bool ok;
 };
 
-__device__ __forceinline__ Certified certify_score(double Q, double bs, const ExcTable &exc)
+__device__ __forceinline__ Certified certify_score(double Q, double bs, const ExcTable &exc,
+                                                   uint32_t fword)
 {
     const float f = (float)Q;
     Certified r;
-    r.sc = router_score(f, exc);
+    r.sc = router_score_w(f, fword, exc);
     r.scmax = r.sc;
     r.ok = true;
     if (fabs(Q) <= 0x1.fffffffffffffp+1023) {
@@ -494,164 +509,176 @@ __device__ __forceinline__ Certified certify_score(double Q, double bs, const Ex
 }
 
 /* Router logits of a few tokens (T <= RS_T, hidden <= 64 * RS_CH), certified and scored in
- * one kernel: a wave per expert, lane k runs the chain of 128-column chunk k for every
- * token (as router_partial_small_kernel), then one lane per token sums the lanes' partials
- * in k order, certifies (certify_score) and stores pre[t][e] = {score, score of the upper
- * end, uncertified ? 1 : 0, 0}.
- * W is read in full 128-byte lines: for 32-column sub-block sb, lane l loads columns
- * 4(l % 8).. of sub-block sb of chunks l / 8 + 8j (j < 8), and a per-wave LDS buffer turns
- * that into one chunk per lane. The tokens are staged once, rows padded to ks * RS_CH.
- * In both LDS layouts a chunk's 16-byte group q sits at group (q + k) mod (its groups), so
- * the lanes' 16-byte reads of their own chunks fall on distinct banks. */
-template <int NT>
+ * one kernel: a workgroup per expert, lane k of every wave owns 128-column chunk k, and wave
+ * w its 32-column sub-block w.
+ * - Loads cover full 128-byte lines: lane l loads columns 4(l % 8).. of sub-block w of chunks
+ *   l / 8 + 8j (j < 8), for W and for each token, and the wave's LDS buffer turns that into
+ *   one sub-block per lane (a chunk's 16-byte group q at group (q + k) mod 8, so the lanes'
+ *   16-byte reads fall on distinct banks). Every load is a buffer load with no branch
+ *   around it (past the end, or a masked offset, reads 0), all issued at once.
+ * - A chunk's value: each of its four sub-blocks is a chain of its own from 0 (one per wave
+ *   and token), then J = ((c0 + c1) + c2) + c3. Its rounded intermediates are the chains'
+ *   partial sums, each at most ||w||_1 ||x||_inf of the sub-block (times 1 + 32u), and the
+ *   joins, each at most |J before it| + that norm; the reference's own partial sums over
+ *   the chunk are bounded alike. So R_k = sum over sub-blocks of 34 (|J before it| +
+ *   ||w||_1 ||x||_inf) bounds both uses of R_k in the certification (34 >= 33 (1 + 32u) for
+ *   the rounded terms, >= 32 for the reference's).
+ * - Wave t then finishes token t: lane k joins chunk k; every lane runs the chunks' sum in
+ *   k order (Q_{k+1} = Q_k + P_k, the rounding the bound describes) on broadcast LDS reads
+ *   and keeps its own Q_k, Q_{k+1}; lane k forms C_k |Q_k| + 2 R_k + |Q_{k+1}|, the wave
+ *   adds those (any order: bs only bounds); lane 0 certifies (certify_score), its
+ *   exception-bitmap word loaded as soon as the sum is known, and stores pre[t][e] =
+ *   {score, score of the upper end, uncertified ? 1 : 0, 0}. */
+template <bool VEC>
+__device__ __forceinline__ float4 rs_load4(k3_rsrc r, uint32_t col)
+{
+    if (VEC) return __builtin_bit_cast(float4, k3_bload16(r, 4u * col));
+    return make_float4(__uint_as_float(k3_bload4(r, 4u * col)), __uint_as_float(k3_bload4(r, 4u * col + 4u)),
+                       __uint_as_float(k3_bload4(r, 4u * col + 8u)), __uint_as_float(k3_bload4(r, 4u * col + 12u)));
+}
+
+/* a + (a of the lane DPP control CTRL names; 0 in rows outside RM) */
+template <int CTRL, int RM>
+__device__ __forceinline__ double dpp_add_f64(double a)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, a);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, RM, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, RM, 0xf, false);
+    return a + __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+/* Sum of a double over the wave by DPP, returned in every lane: pairs, quads, row halves,
+ * rows, then rows 0-1 / 2-3 (row_bcast15) and 0-3 (row_bcast31) into lane 63. */
+__device__ __forceinline__ double wave_sum_f64(double v)
+{
+    v = dpp_add_f64<0xB1, 0xf>(v);      /* quad_perm [1,0,3,2] */
+    v = dpp_add_f64<0x4E, 0xf>(v);      /* quad_perm [2,3,0,1] */
+    v = dpp_add_f64<0x141, 0xf>(v);     /* row_half_mirror */
+    v = dpp_add_f64<0x140, 0xf>(v);     /* row_mirror */
+    v = dpp_add_f64<0x142, 0xa>(v);     /* row_bcast15 */
+    v = dpp_add_f64<0x143, 0xc>(v);     /* row_bcast31 */
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+template <int NT, bool VEC>
 __global__ __launch_bounds__(256) void router_small_kernel(float4 *pre, const float *x, int T,
                                                            const float *W, int hidden,
-                                                           int n_experts, int vec, ExcTable exc)
+                                                           int n_experts, ExcTable exc)
 {
-    extern __shared__ __attribute__((aligned(16))) float xsf[];   /* [T][ks * RS_CH] */
-    __shared__ __attribute__((aligned(16))) float wsh[4][64 * 32]; /* per wave: 64 chunks x 32 */
-    __shared__ double psh[4][NT][64];
-    __shared__ float rsh[4][NT][64];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int e = blockIdx.x * 4 + wv;
+    __shared__ __attribute__((aligned(16))) float tr[4][64 * 32];  /* per wave: 64 chunks x 32 */
+    __shared__ __attribute__((aligned(16))) double csh[NT][4][64];  /* chain value per sub-block */
+    __shared__ float xmsh[NT][4][64];                               /* ||x||_inf per sub-block */
+    __shared__ float wnsh[4][64];                                   /* ||w||_1 per sub-block */
+    __shared__ __attribute__((aligned(16))) double jsh[NT][64];     /* chunk values P_k */
+    const int tid = threadIdx.x, lane = tid & 63, sb = tid >> 6;
+    const int e = blockIdx.x;
     const int ks = (hidden + RS_CH - 1) / RS_CH;
-    const int kb0 = lane * RS_CH, len = max(0, min(RS_CH, hidden - kb0));
-    const float *wr = W + (size_t)min(e, n_experts - 1) * hidden;
-    /* W loads: sub-block sb, j: chunk l / 8 + 8j, columns 4(l % 8)..4(l % 8) + 3 */
-    float4 wl[4][8];
+    const k3_rsrc wr = k3_make_rsrc(W + (size_t)e * hidden, 4u * (uint32_t)hidden);
+    const k3_rsrc xr = k3_make_rsrc(x, 4u * (uint32_t)(T * hidden));
+    /* loads j: chunk l / 8 + 8j, columns 4(l % 8)..4(l % 8) + 3 of sub-block sb */
     const int lq = lane & 7, lk = lane >> 3;
+    float4 wl[8], xl[NT][8];
 #pragma unroll
-    for (int sb = 0; sb < 4; sb++)
+    for (int j = 0; j < 8; j++) {
+        const int col = (lk + 8 * j) * RS_CH + sb * 32 + 4 * lq;
+        wl[j] = rs_load4<VEC>(wr, (uint32_t)col);
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int col = (lk + 8 * j) * RS_CH + sb * 32 + 4 * lq;
-            if (vec && col + 3 < hidden)
-                wl[sb][j] = *reinterpret_cast<const float4 *>(wr + col);
-            else
-                wl[sb][j] = make_float4(col < hidden ? wr[col] : 0.f, col + 1 < hidden ? wr[col + 1] : 0.f,
-                                        col + 2 < hidden ? wr[col + 2] : 0.f, col + 3 < hidden ? wr[col + 3] : 0.f);
-        }
-    /* stage the tokens: eight loads per thread in flight, then the stores */
-    const int rowp = ks * RS_CH;
-    auto slot = [&](int t, int col) {
-        const int k = col / RS_CH, j = col % RS_CH;
-        return t * rowp + k * RS_CH + ((j + 4 * k) & (RS_CH - 1));
-    };
-    if (vec) {
-        const int nq = T * hidden / 4, rq = hidden / 4;
-        for (int i0 = 0; i0 < nq; i0 += 256 * 8) {
-            float4 v[8];
+        for (int t = 0; t < NT; t++) {
+            /* token t's columns col.. (zero past the row or past T: an offset past the end) */
+            const uint32_t o = (uint32_t)(t * hidden + col);
+            if (VEC) {
+                xl[t][j] = __builtin_bit_cast(float4, k3_bload16(xr, t < T && col < hidden ? 4u * o : 0xfffffff0u));
+            } else {
+                float v[4];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + tid + 256 * j;
-                v[j] = i < nq ? reinterpret_cast<const float4 *>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + tid + 256 * j;
-                if (i < nq) *reinterpret_cast<float4 *>(&xsf[slot(i / rq, 4 * (i % rq))]) = v[j];
-            }
-        }
-    } else {
-        const int n = T * hidden;
-        for (int i0 = 0; i0 < n; i0 += 256 * 8) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + tid + 256 * j;
-                v[j] = i < n ? x[i] : 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + tid + 256 * j;
-                if (i < n) xsf[slot(i / hidden, i % hidden)] = v[j];
+                for (int i = 0; i < 4; i++)
+                    v[i] = __uint_as_float(k3_bload4(xr, t < T && col + i < hidden ? 4u * (o + i) : 0xfffffff0u));
+                xl[t][j] = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
     }
-    __syncthreads();
-    double acc[NT], rb[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) { acc[t] = 0.0; rb[t] = 0.0; }
-    float *wb = wsh[wv];
-    const int xk = lane < ks ? kb0 : 0;             /* lanes past the last chunk read chunk 0 */
-#pragma unroll
-    for (int sb = 0; sb < 4; sb++) {
-        /* this sub-block of every chunk through the wave's buffer: chunk k at 32 k, group q
-         * of it at (q + k) mod 8 */
+    /* through the wave's buffer: a row of 32 per chunk, group q of chunk k at (q + k) mod 8 */
+    float *wb = tr[sb];
+    auto transpose = [&](const float4 (&in)[8], float4 (&out)[8]) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int k = lk + 8 * j;
-            *reinterpret_cast<float4 *>(&wb[k * 32 + 4 * ((lq + k) & 7)]) = wl[sb][j];
+            *reinterpret_cast<float4 *>(&wb[k * 32 + 4 * ((lq + k) & 7)]) = in[j];
         }
         __builtin_amdgcn_wave_barrier();
-        float4 wq[8];
 #pragma unroll
-        for (int q = 0; q < 8; q++) wq[q] = *reinterpret_cast<const float4 *>(&wb[lane * 32 + 4 * ((q + lane) & 7)]);
+        for (int q = 0; q < 8; q++) out[q] = *reinterpret_cast<const float4 *>(&wb[lane * 32 + 4 * ((q + lane) & 7)]);
         __builtin_amdgcn_wave_barrier();
-        float wn = 0.0f;
+    };
+    float4 wq[8];
+    transpose(wl, wq);
+    {
+        /* ||w||_1 as a pairwise sum: relative error under 2^-21 */
+        float s4[8];
 #pragma unroll
-        for (int q = 0; q < 8; q++)
-            wn += fabsf(wq[q].x) + fabsf(wq[q].y) + fabsf(wq[q].z) + fabsf(wq[q].w);
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (t >= T) break;
-            float xv[32];
-            float xm = 0.0f;
-#pragma unroll
-            for (int j4 = 0; j4 < 8; j4++) {
-                const int k = sb * 32 + 4 * j4;
-                const float4 v = *reinterpret_cast<const float4 *>(&xsf[t * rowp + xk + ((k + 4 * lane) & (RS_CH - 1))]);
-                xv[4 * j4] = k < len ? v.x : 0.0f;
-                xv[4 * j4 + 1] = k + 1 < len ? v.y : 0.0f;
-                xv[4 * j4 + 2] = k + 2 < len ? v.z : 0.0f;
-                xv[4 * j4 + 3] = k + 3 < len ? v.w : 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < 32; j++) xm = fmaxf(xm, fabsf(xv[j]));
-            rb[t] = fma(32.0, fabs(acc[t]) + (double)wn * (double)xm, rb[t]);
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                acc[t] = fma((double)wq[q].x, (double)xv[4 * q], acc[t]);
-                acc[t] = fma((double)wq[q].y, (double)xv[4 * q + 1], acc[t]);
-                acc[t] = fma((double)wq[q].z, (double)xv[4 * q + 2], acc[t]);
-                acc[t] = fma((double)wq[q].w, (double)xv[4 * q + 3], acc[t]);
-            }
-        }
+        for (int q = 0; q < 8; q++) s4[q] = (fabsf(wq[q].x) + fabsf(wq[q].y)) + (fabsf(wq[q].z) + fabsf(wq[q].w));
+        wnsh[sb][lane] = ((s4[0] + s4[1]) + (s4[2] + s4[3])) + ((s4[4] + s4[5]) + (s4[6] + s4[7]));
     }
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        psh[wv][t][lane] = acc[t];
-        /* rounded up: the float sums of |w| carry at most a 2^-18 relative error */
-        rsh[wv][t][lane] = bound_up(rb[t], 1.0 + 0x1p-17);
+        if (t >= T) break;
+        float4 xq[8];
+        transpose(xl[t], xq);
+        float m[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            m[q] = fmaxf(fmaxf(fabsf(xq[q].x), fabsf(xq[q].y)), fmaxf(fabsf(xq[q].z), fabsf(xq[q].w)));
+        xmsh[t][sb][lane] = fmaxf(fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3])), fmaxf(fmaxf(m[4], m[5]), fmaxf(m[6], m[7])));
+        double a = 0.0;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            a = fma((double)wq[q].x, (double)xq[q].x, a);
+            a = fma((double)wq[q].y, (double)xq[q].y, a);
+            a = fma((double)wq[q].z, (double)xq[q].z, a);
+            a = fma((double)wq[q].w, (double)xq[q].w, a);
+        }
+        csh[t][sb][lane] = a;
     }
     __syncthreads();
-    if (lane < T && e < n_experts) {
-        const int t = lane;
-        double pv[64];
-        float rv[64];
+    const int t = sb;                               /* wave t finishes token t */
+    if (t >= T) return;
+    /* lane k: chunk k's value and R_k (lanes past the last chunk hold zeros) */
+    double J = csh[t][0][lane];
+    double rb = 34.0 * ((double)wnsh[0][lane] * (double)xmsh[t][0][lane]);
 #pragma unroll
-        for (int k = 0; k < 64; k++) {
-            pv[k] = psh[wv][t][k];
-            rv[k] = rsh[wv][t][k];
-        }
-        /* Q_{k+1} = Q_k + P_k in k order (the rounding the bound describes); bs, the sum of
-         * C_k |Q_k| + 2 R_k + |Q_{k+1}|, only bounds and is added in any order (its own
-         * relative error, under 2^-45, is far inside the bound's 1% slack) */
-        double qk[65];
-        qk[0] = 0.0;
+    for (int s = 1; s < 4; s++) {
+        rb = fma(34.0, fabs(J) + (double)wnsh[s][lane] * (double)xmsh[t][s][lane], rb);
+        J += csh[t][s][lane];
+    }
+    /* rounded up: the float sums of |w| carry at most a 2^-18 relative error */
+    const double R = (double)bound_up(rb, 1.0 + 0x1p-17);
+    jsh[t][lane] = J;
+    __builtin_amdgcn_wave_barrier();
+    /* the sum in k order in every lane (broadcast reads); lane k keeps Q_k and Q_{k+1} */
+    double pk[64];
 #pragma unroll
-        for (int k = 0; k < 64; k++) qk[k + 1] = k < ks ? qk[k] + pv[k] : qk[k];
-        double term[64];
+    for (int k = 0; k < 64; k += 2) {
+        const double2 v = *reinterpret_cast<const double2 *>(&jsh[t][k]);
+        pk[k] = v.x;
+        pk[k + 1] = v.y;
+    }
+    double q = 0.0, q0 = 0.0, q1 = 0.0;
 #pragma unroll
-        for (int k = 0; k < 64; k++) {
-            const int ck = min(RS_CH, hidden - k * RS_CH);
-            term[k] = k < ks ? fma((double)ck, fabs(qk[k]), fma(2.0, (double)rv[k], fabs(qk[k + 1]))) : 0.0;
-        }
-#pragma unroll
-        for (int w = 32; w > 0; w >>= 1)
-#pragma unroll
-            for (int k = 0; k < w; k++) term[k] += term[k + w];
-        const Certified cs = certify_score(qk[64], term[0], exc);
+    for (int k = 0; k < 64; k++) {
+        if (k == lane) q0 = q;
+        if (k < ks) q += pk[k];
+        if (k == lane) q1 = q;
+    }
+    const double S = q;
+    const uint32_t fw = exc_word((float)S, exc);
+    const double ck = (double)min(RS_CH, hidden - min(lane, ks - 1) * RS_CH);
+    const double term = lane < ks ? fma(ck, fabs(q0), fma(2.0, R, fabs(q1))) : 0.0;
+    const double bs = wave_sum_f64(term);
+    if (lane == 0) {
+        const Certified cs = certify_score(S, bs, exc, fw);
         pre[(size_t)t * n_experts + e] = make_float4(cs.sc, cs.scmax, cs.ok ? 0.0f : 1.0f, 0.0f);
     }
 }
@@ -771,7 +798,7 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
                     }
                 }
             }
-            const Certified cs = certify_score(Q, bs, exc);
+            const Certified cs = certify_score(Q, bs, exc, exc_word((float)Q, exc));
             sc[i] = cs.sc;
             const float bb = bias ? bias[e] : 0.0f;
             c[i] = sc[i] + bb;
@@ -1340,15 +1367,11 @@ extern "C" int k3k_router_chunk(int T, int hidden, int n_experts)
     return (int)best_chunk;
 }
 
-/* Up to RS_T tokens and 64 chunks of RS_CH columns whose staged rows fit in LDS beside
- * the kernel's own 45 KB: router_small_kernel certifies and scores the logits itself, and
- * the final kernel starts from its records. */
-constexpr size_t RS_LDS_DYN = 160 * 1024 - 45 * 1024;
-
+/* Up to RS_T tokens and 64 chunks of RS_CH columns: router_small_kernel certifies and
+ * scores the logits itself, and the final kernel starts from its records. */
 static bool router_small_mode(int T, int hidden)
 {
-    const size_t ks = (size_t)(hidden + RS_CH - 1) / RS_CH;
-    return T <= RS_T && ks <= 64 && (size_t)T * ks * RS_CH * 4 <= RS_LDS_DYN;
+    return T <= RS_T && (hidden + RS_CH - 1) / RS_CH <= 64;
 }
 
 static ExcTable exc_view(const K3kExc *exc)
@@ -1380,23 +1403,22 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
     hipStream_t st = (hipStream_t)stream;
     if (router_small_mode(T, hidden)) {
         if (chunk != RS_CH) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
-        const size_t lds = (size_t)T * ks * RS_CH * 4;
+        const size_t lds = 0;
         const ExcTable e = exc_view(exc);
         float4 *pre = reinterpret_cast<float4 *>(part);
-        const dim3 grid((n_experts + 3) / 4);
-        if (T == 1) {
-            hipLaunchKernelGGL(router_small_kernel<1>, grid, dim3(256), lds, st, pre, x, T, W, hidden,
-                               n_experts, vec, e);
-        } else {
-            static bool attr = false;
-            if (!attr) {
-                (void)hipFuncSetAttribute(reinterpret_cast<const void *>(router_small_kernel<RS_T>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)RS_LDS_DYN);
-                attr = true;
-            }
-            hipLaunchKernelGGL(router_small_kernel<RS_T>, grid, dim3(256), lds, st, pre, x, T, W,
-                               hidden, n_experts, vec, e);
-        }
+        const dim3 grid(n_experts);
+        if (T == 1 && vec)
+            hipLaunchKernelGGL((router_small_kernel<1, true>), grid, dim3(256), lds, st, pre, x, T, W,
+                               hidden, n_experts, e);
+        else if (T == 1)
+            hipLaunchKernelGGL((router_small_kernel<1, false>), grid, dim3(256), lds, st, pre, x, T, W,
+                               hidden, n_experts, e);
+        else if (vec)
+            hipLaunchKernelGGL((router_small_kernel<RS_T, true>), grid, dim3(256), lds, st, pre, x, T,
+                               W, hidden, n_experts, e);
+        else
+            hipLaunchKernelGGL((router_small_kernel<RS_T, false>), grid, dim3(256), lds, st, pre, x, T,
+                               W, hidden, n_experts, e);
     } else if (T <= RS_T) {
         if (chunk != RS_CH) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
         dim3 grid((n_experts + 255) / 256, ks);
