@@ -429,12 +429,21 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
         k3k_prof_mark(stream, K3D_STAGE_GATEUP);
         a.xhi = w->ahi;
         a.xlo = w->alo;
-        a.out = w->contrib;
+        a.out = out;
+        a.wt = wt;
         a.rows = hidden;
         a.K = inter;
-        if (k3k_mx_decode(K3K_MX_DOWN, &a, stream)) return fail("mx_decode down");
-        k3k_prof_mark(stream, K3D_STAGE_DOWN);
-        if (k3k_combine(out, w->contrib, wt, idx, bank, n_experts, T, topk, hidden, stream)) return fail("combine");
+        if (k3k_mx_decode_combine_ok(T * topk, topk, a.nsplit, inter, hidden)) {
+            /* down and the combine in one kernel */
+            if (k3k_mx_decode_combine(&a, stream)) return fail("mx_decode down+combine");
+            k3k_prof_mark(stream, K3D_STAGE_DOWN);
+        } else {
+            a.out = w->contrib;
+            if (k3k_mx_decode(K3K_MX_DOWN, &a, stream)) return fail("mx_decode down");
+            k3k_prof_mark(stream, K3D_STAGE_DOWN);
+            if (k3k_combine(out, w->contrib, wt, idx, bank, n_experts, T, topk, hidden, stream))
+                return fail("combine");
+        }
         k3k_prof_mark(stream, K3D_STAGE_COMBINE);
         if (drops_out && k3k_d2d(drops_out, w->counts + 2, 4, stream)) return fail("drops");
         return 0;

@@ -490,7 +490,7 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
     } else {
         pm[0] = q.p2; sm[0] = q.s2;
     }
-    if (pm[0] == nullptr) return;                           /* dropped or out of range */
+    if (!(q.p1 && q.s1 && q.p3 && q.s3 && q.p2 && q.s2)) return;   /* dropped or out of range */
     /* activation loads first: they return while the weights stream */
     float4 xv[XPT];
     uint4 hv[XPT];
@@ -632,6 +632,149 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
             for (int jj = 0; jj < 4; jj++)
                 if (base + jj < rows) a.out[(size_t)asg * rows + base + jj] = sum[0][jj];
         }
+    }
+}
+
+/* mx_decode_combine_kernel: DOWN and the weighted combine of the decode path in one
+ * kernel. A workgroup takes one (token t, 16-row tile) and all of the token's topk slots:
+ * wave w = (slot j = w % topk, K share ks = w / topk) streams the tile's rows of slot j's
+ * down matrix over its share of the 512-column chunks, like mx_decode_kernel with one tile
+ * per wave. The slots' activation terms are staged in LDS once per workgroup. Then the
+ * shares of a slot are added in share order (the sums mx_decode_kernel writes to contrib)
+ * and out[t][row] = 0 + sum_j wt[t][j] * slot j's sum, j ascending, over the slots whose
+ * expert is in range and present in the bank -- the combine's rule and order
+ * (k3_ops.c:641-642). An absent slot's wave reads through an empty descriptor (zeros) and
+ * its sum is left out. */
+template <int NS, int LAYOUT>
+__global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* [topk][NS][K], zeros[512] */
+    __shared__ float red[16 * 16];                                  /* [slot, share][16 rows] */
+    __shared__ int vsh[16];
+    __shared__ float wsh[16];
+    constexpr int WPOL = LAYOUT == 1 ? K3_LD_NT : K3_LD_DEFAULT;
+    const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int topk = a.topk, KS = nthr / (64 * topk);
+    const int j = wv % topk, ks = wv / topk;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int K = a.K, nblk = K >> 5, rows = a.rows, ntile = (rows + 15) >> 4, nchunk = K >> 9;
+    const int t = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+    const int c0 = ks * nchunk / KS, c1 = (ks + 1) * nchunk / KS;
+    const ExpertQDev *bank = reinterpret_cast<const ExpertQDev *>(a.bank);
+    const int eix = a.idx[t * topk + j];
+    const float wj = a.wt[t * topk + j];                    /* in flight with the rest */
+    ExpertQDev q = {};
+    if (eix >= 0 && eix < a.n_experts) q = bank[eix];
+    const bool valid = q.p1 && q.s1 && q.p3 && q.s3 && q.p2 && q.s2;
+    const uint32_t prow = LAYOUT == 1 ? (uint32_t)ntile * 16u : (uint32_t)rows;
+    const k3_rsrc rp = k3_make_rsrc(q.p2, valid ? prow * (uint32_t)(K >> 1) : 0u);
+    const k3_rsrc rs = k3_make_rsrc(q.s2, valid ? prow * (uint32_t)nblk : 0u);
+    const int row = min(tile * 16 + r16, rows - 1);
+    uint4 qa[2][4];
+    uint4 sq[2];
+    auto load = [&](int c, auto slot) {
+        constexpr int S = decltype(slot)::value;
+        if (LAYOUT == 1) {
+            const uint32_t tc = (uint32_t)tile * (uint32_t)nchunk + (uint32_t)c;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                qa[S][i] = k3_bload16<WPOL>(rp, tc * 4096u + (uint32_t)i * 1024u + (uint32_t)lane * 16u);
+            sq[S].x = k3_bload4<WPOL>(rs, tc * 256u + (uint32_t)lane * 4u);
+        } else {
+            const uint32_t pb = (uint32_t)row * (uint32_t)(K >> 1) + (uint32_t)c * 256u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) qa[S][i] = k3_bload16<WPOL>(rp, pb + (uint32_t)(4 * i + g) * 16u);
+            sq[S] = k3_bload16<WPOL>(rs, (uint32_t)row * (uint32_t)nblk + (uint32_t)c * 16u);
+        }
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    if (c0 < c1) load(c0, P0{});
+    if (c0 + 1 < c1) load(c0 + 1, P1{});
+    /* this wave's slot and columns of the activation terms into [slot][term][K] (the waves
+     * of one slot stage disjoint column ranges), and the row of zeros (every wave writes the
+     * same zeros): no workgroup barrier before the products */
+    {
+        const int nq = (c1 - c0) * 64;                      /* 16-byte pieces per term */
+        const uint32_t bytes = (uint32_t)a.n_assign * (uint32_t)K * 2u;
+        const uint32_t src = (uint32_t)(t * topk + j) * (uint32_t)K + (uint32_t)c0 * 512u;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const k3_rsrc rx = k3_make_rsrc(s == 0 ? a.xhi : a.xlo, bytes);
+            for (int i0 = 0; i0 < nq; i0 += 256) {
+                uint4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[u] = k3_bload16(rx, (src + 8u * (uint32_t)(i0 + lane + 64 * u)) * 2u);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int i = i0 + lane + 64 * u;
+                    if (i < nq)
+                        *reinterpret_cast<uint4 *>(&xs[((size_t)j * NS + s) * K + c0 * 512 + 8 * i]) = v[u];
+                }
+            }
+        }
+        reinterpret_cast<uint4 *>(&xs[(size_t)topk * NS * K])[lane] = make_uint4(0, 0, 0, 0);
+    }
+    if (ks == 0 && lane == 0) {
+        vsh[j] = valid ? 1 : 0;
+        wsh[j] = wj;
+    }
+    __builtin_amdgcn_wave_barrier();
+    k3_f32x4 acc[2] = {k3_f32x4{0.f, 0.f, 0.f, 0.f}, k3_f32x4{0.f, 0.f, 0.f, 0.f}};
+    const uint16_t *zb = &xs[(size_t)topk * NS * K + g * 32];
+    auto comp = [&](int c, auto slot) {
+        constexpr int S = decltype(slot)::value;
+        const uint16_t *hb = r16 == 0 ? &xs[(size_t)j * NS * K + c * 512 + g * 32] : zb;
+        const uint16_t *lb = r16 == 0 ? &xs[((size_t)j * NS + 1) * K + c * 512 + g * 32] : zb;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t sw = LAYOUT == 1 ? sq[S].x >> (8 * i)
+                              : (i == 0 ? sq[S].x : i == 1 ? sq[S].y : i == 2 ? sq[S].z : sq[S].w) >> (8 * g);
+            uint32_t ss = sw & 0xffu;
+            uint4 qm = qa[S][i];
+            if (ss == 255u) {                               /* NaN byte: the block is 0 */
+                qm = make_uint4(0, 0, 0, 0);
+                ss = 127u;
+            }
+            const float so = k3_e8m0_operand(ss);
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const uint4 bh = *reinterpret_cast<const uint4 *>(hb + 128 * i + 8 * p);
+                const uint32_t codes = p == 0 ? qm.x : p == 1 ? qm.y : p == 2 ? qm.z : qm.w;
+                const k3_bf16x8 av = k3_dequant8_bf16(codes, so);
+                acc[p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh), acc[p & 1], 0, 0, 0);
+                if (NS == 2) {
+                    const uint4 bl = *reinterpret_cast<const uint4 *>(lb + 128 * i + 8 * p);
+                    acc[p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl), acc[p & 1], 0, 0, 0);
+                }
+            }
+        }
+    };
+    for (int c = c0; c < c1; c += 2) {
+        comp(c, P0{});
+        if (c + 2 < c1) load(c + 2, P0{});
+        if (c + 1 < c1) {
+            comp(c + 1, P1{});
+            if (c + 3 < c1) load(c + 3, P1{});
+        }
+    }
+    /* lanes of token column 0 hold the tile's 16 rows, four each */
+    if (r16 == 0) {
+        const k3_f32x4 sum = acc[0] + acc[1];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) red[(j * KS + ks) * 16 + 4 * g + jj] = sum[jj];
+    }
+    __syncthreads();
+    if (tid < 16 && tile * 16 + tid < rows) {
+        float o = 0.0f;
+        for (int jj = 0; jj < topk; jj++) {
+            if (!vsh[jj]) continue;
+            float d = red[(jj * KS) * 16 + tid];
+            for (int k2 = 1; k2 < KS; k2++) d += red[(jj * KS + k2) * 16 + tid];
+            o = __fadd_rn(o, __fmul_rn(wsh[jj], d));
+        }
+        a.out[(size_t)t * rows + tile * 16 + tid] = o;
     }
 }
 
@@ -1460,6 +1603,51 @@ extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
 #undef K3_DEC
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * tpw * ks), lds, (hipStream_t)stream, *a);
     K3K_LAUNCH_CHECK("mx_decode launch");
+    return 0;
+}
+
+/* The fused kernel is used where it is faster than mx_decode_kernel DOWN + the combine
+ * kernel (measured: one or two assignments, 7168 x 2048 -- 18.3 against 20.3 us for one
+ * expert's FFN; at eight it is slower, 24 against 19 us) and the slots' activation terms
+ * of one token fit in its LDS. */
+extern "C" int k3k_mx_decode_combine_ok(int n_assign, int topk, int nsplit, int K, int rows)
+{
+    const long ntile = (rows + 15) / 16;
+    const bool wide = (long)n_assign * ((ntile + 3) / 4) >= 256 || K / 512 < 4;
+    return !wide && topk >= 1 && topk <= 16 && (size_t)topk * nsplit * K * 2 + 1024 <= 160 * 1024 - 2048;
+}
+
+extern "C" int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream)
+{
+    if (a->n_assign <= 0) return 0;
+    if (a->K % 512 || a->K > 16 * 512 || a->n_assign > 16 || a->layout > 1 || a->topk < 1 ||
+        a->n_assign % a->topk || !a->wt ||
+        (size_t)((a->rows + 15) / 16 * 16) * (a->K / 2) >= 0x80000000u)
+        return k3k_fail("mx_decode_combine: shape", hipErrorInvalidValue);
+    /* waves: topk slots x K shares, at most 16 */
+    const int nchunk = a->K / 512;
+    int ks = 16 / a->topk;
+    if (ks > nchunk) ks = nchunk;
+    const int T = a->n_assign / a->topk, ntile = (a->rows + 15) / 16;
+    if ((size_t)a->topk * a->nsplit * a->K * 2 + 1024 > 160 * 1024 - 2048)
+        return k3k_fail("mx_decode_combine: LDS", hipErrorInvalidValue);
+    const size_t lds = (size_t)a->topk * a->nsplit * a->K * 2 + 1024;
+    void (*kern)(K3kMxArgs);
+    const bool ns2 = a->nsplit == 2, tiled = a->layout == 1;
+    kern = tiled ? (ns2 ? mx_decode_combine_kernel<2, 1> : mx_decode_combine_kernel<1, 1>)
+                 : (ns2 ? mx_decode_combine_kernel<2, 0> : mx_decode_combine_kernel<1, 0>);
+    static bool attr = false;
+    if (!attr) {
+        const void *ks4[4] = {reinterpret_cast<const void *>(mx_decode_combine_kernel<2, 1>),
+                              reinterpret_cast<const void *>(mx_decode_combine_kernel<1, 1>),
+                              reinterpret_cast<const void *>(mx_decode_combine_kernel<2, 0>),
+                              reinterpret_cast<const void *>(mx_decode_combine_kernel<1, 0>)};
+        for (int i = 0; i < 4; i++)
+            (void)hipFuncSetAttribute(ks4[i], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 2048);
+        attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(T * ntile), dim3(64 * a->topk * ks), lds, (hipStream_t)stream, *a);
+    K3K_LAUNCH_CHECK("mx_decode_combine launch");
     return 0;
 }
 

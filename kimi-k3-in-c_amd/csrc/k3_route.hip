@@ -691,6 +691,7 @@ __global__ __launch_bounds__(256) void router_small_kernel(float4 *pre, const fl
  * (k3_ops.c:469-475). nrecomp[t] (optional) counts recomputes. KB: chunk partials loaded
  * per batch (64 for up to 512 experts, one batch at decode sizes). */
 constexpr int RF_MAXE = 2048, RF_MAXW = 16, RF_KB = 32;
+constexpr int RS_SEL = 8;           /* router_select_kernel: up to 64 x 8 experts */
 
 /* unsigned order of a non-NaN float that matches its numeric order (-0 as +0) */
 __device__ __forceinline__ uint32_t choice_order(float v)
@@ -731,6 +732,159 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t k)
     const uint32_t hi = wave_reduce_u32<true>((uint32_t)(k >> 32));
     const uint32_t lo = wave_reduce_u32<true>((uint32_t)(k >> 32) == hi ? (uint32_t)k : 0u);
     return ((uint64_t)hi << 32) | lo;
+}
+
+/* The wave's largest key as wave_max_key, with the second reduction only on a tie of the
+ * high words (choices): otherwise the one lane holding the largest choice gives its key. */
+__device__ __forceinline__ uint64_t wave_max_key_fast(uint64_t k)
+{
+    const uint32_t hi = wave_reduce_u32<true>((uint32_t)(k >> 32));
+    const uint64_t at = __ballot((uint32_t)(k >> 32) == hi);
+    uint32_t lo;
+    if (__popcll(at) == 1)
+        lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, (int)(__ffsll((unsigned long long)at) - 1));
+    else
+        lo = wave_reduce_u32<true>((uint32_t)(k >> 32) == hi ? (uint32_t)k : 0u);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+/* The choice a selection key carries (choice_order inverted; -0 comes back as +0). */
+__device__ __forceinline__ float key_choice(uint64_t key)
+{
+    const uint32_t h = (uint32_t)(key >> 32);
+    return __uint_as_float((h & 0x80000000u) ? (h & 0x7fffffffu) : ~h);
+}
+
+/* The selection of a few tokens from router_small_kernel's scored records, one wave per
+ * token (up to 64 SL experts): the same rule and the same recompute rounds as
+ * router_final_kernel (k3_ops.c:459-475), with every step inside one wave. Lane l holds
+ * experts l + 64 i and the largest of its keys; each of the topk extractions is one wave
+ * maximum over those (wave_max_key_fast), after which the lane that held it drops the key
+ * and takes its next largest. Lane j keeps the j-th selected key. Uncertified logits that
+ * matter are listed by ballots and recomputed with the reference's chain (chain_block on
+ * this wave); the selection is redone until none is left. */
+template <int SL>
+__global__ __launch_bounds__(64) void router_select_kernel(int *idx, float *wt, int *nrecomp,
+                                                           const float4 *pre, const float *x,
+                                                           const float *W, const float *bias,
+                                                           int hidden, int n_experts, int topk,
+                                                           int renorm, float routed_scale,
+                                                           ExcTable exc)
+{
+    __shared__ __attribute__((aligned(16))) double prod_sh[2][RF_BLK];
+    __shared__ float ssh[64 * SL];
+    __shared__ int list_sh[RF_LIST];
+    __shared__ double res_sh[RF_LIST];
+    const int lane = threadIdx.x, t = blockIdx.x;
+    float c[SL], cmax[SL], sc[SL];
+    bool unc[SL];
+    float4 pr[SL];
+    float bb[SL];
+#pragma unroll
+    for (int i = 0; i < SL; i++) {
+        const int e = lane + 64 * i;
+        pr[i] = e < n_experts ? pre[(size_t)t * n_experts + e] : make_float4(0.f, 0.f, 0.f, 0.f);
+        bb[i] = (bias && e < n_experts) ? bias[e] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < SL; i++) {
+        const int e = lane + 64 * i;
+        sc[i] = pr[i].x;
+        c[i] = e < n_experts ? sc[i] + bb[i] : -INFINITY;
+        unc[i] = e < n_experts && pr[i].z != 0.0f;
+        cmax[i] = unc[i] ? pr[i].y + bb[i] : c[i];          /* choice is monotone in logit */
+        ssh[lane + 64 * i] = sc[i];
+    }
+    int nre = 0;
+    uint64_t mysel = 0ull;                          /* lane j: the j-th selected key */
+    for (int round = 0; round <= n_experts; round++) {
+        uint64_t key[SL];
+        uint64_t head = 0ull;
+#pragma unroll
+        for (int i = 0; i < SL; i++) {
+            const int e = lane + 64 * i;
+            key[i] = c[i] > -INFINITY ? ((uint64_t)choice_order(c[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e)
+                                      : 0ull;
+            head = head > key[i] ? head : key[i];
+        }
+        uint32_t taken = 0u;                        /* bit i: key i was selected */
+        int nsel = 0;
+        uint64_t last = 0ull;
+        mysel = 0ull;
+        for (int j = 0; j < topk; j++) {
+            const uint64_t m = wave_max_key_fast(head);
+            if (m == 0ull) break;                   /* no finite choice left */
+            nsel++;
+            last = m;
+            if (lane == j) mysel = m;
+            if (head == m) {
+                uint64_t h2 = 0ull;
+#pragma unroll
+                for (int i = 0; i < SL; i++) {
+                    if (key[i] == m) {
+                        key[i] = 0ull;
+                        taken |= 1u << i;
+                    }
+                    h2 = h2 > key[i] ? h2 : key[i];
+                }
+                head = h2;
+            }
+        }
+        const float ckth = nsel > 0 ? key_choice(last) : -INFINITY;
+        /* uncertified logits that matter: selected, or able to reach the selection */
+        bool need[SL];
+        bool any = false;
+#pragma unroll
+        for (int i = 0; i < SL; i++) {
+            need[i] = unc[i] && (((taken >> i) & 1u) || nsel < topk || cmax[i] >= ckth);
+            any |= need[i];
+        }
+        if (__ballot(any) == 0ull) break;
+        /* list up to RF_LIST of them (ballot order); the rest wait for the next round */
+        int slot[SL];
+        int base = 0;
+#pragma unroll
+        for (int i = 0; i < SL; i++) {
+            const uint64_t m = __ballot(need[i]);
+            const int below = __popcll(m & ((1ull << lane) - 1ull));
+            slot[i] = need[i] ? base + below : RF_LIST;
+            if (slot[i] >= RF_LIST) slot[i] = RF_LIST;
+            base += __popcll(m);
+            if (slot[i] < RF_LIST) list_sh[slot[i]] = lane + 64 * i;
+        }
+        const int nl = min(base, RF_LIST);
+        __syncthreads();
+        for (int j = 0; j < nl; j++) {
+            const double a = chain_block(prod_sh, W + (size_t)list_sh[j] * hidden, x + (size_t)t * hidden, hidden);
+            if (lane == 0) res_sh[j] = a;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < SL; i++)
+            if (slot[i] < RF_LIST) {
+                sc[i] = router_score((float)res_sh[slot[i]], exc);
+                c[i] = sc[i] + bb[i];
+                cmax[i] = c[i];
+                unc[i] = false;
+                ssh[lane + 64 * i] = sc[i];
+            }
+        nre += nl;
+        __syncthreads();
+    }
+    const int id = mysel != 0ull ? (int)(0xffffffffu - (uint32_t)mysel) : -1;
+    __syncthreads();
+    float w = (lane < topk && id >= 0) ? ssh[id] : 0.0f;
+    if (renorm && topk > 1) {
+        double s = 0.0;
+        for (int j = 0; j < topk; j++) s += (double)__shfl(w, j, 64);   /* j ascending */
+        const float inv = (float)(1.0 / (s + 1e-20));
+        w = w * inv;
+    }
+    if (lane < topk) {
+        idx[(size_t)t * topk + lane] = id >= 0 ? id : 0;
+        wt[(size_t)t * topk + lane] = w * routed_scale;
+    }
+    if (nrecomp && lane == 0) nrecomp[t] = nre;
 }
 
 template <int SL, int KB, bool PRE>
@@ -1455,7 +1609,11 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
      * experts (<= 8 waves) in one batch of up to 64 loads (more registers, fewer waves per
      * CU: only while the tokens do not fill the chip) */
     const bool pre = router_small_mode(T, hidden);
-    if (pre && n_experts <= 64 * RF_MAXW)
+    if (pre && n_experts <= 64 * RS_SEL)
+        hipLaunchKernelGGL((router_select_kernel<RS_SEL>), dim3(T), dim3(64), 0, st, idx, wt, nrecomp,
+                           reinterpret_cast<const float4 *>(part), x, W, bias, hidden, n_experts,
+                           topk, renorm, routed_scale, e);
+    else if (pre && n_experts <= 64 * RF_MAXW)
         hipLaunchKernelGGL((router_final_kernel<1, RF_KB, true>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
                            nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
                            renorm, routed_scale, e);

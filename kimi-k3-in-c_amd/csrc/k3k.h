@@ -94,6 +94,7 @@ typedef struct {
     int n_assign;
     int *drops;
     int n_experts;                      /* idx outside [0, n_experts): absent */
+    const float *wt;                    /* k3k_mx_decode_combine: weights [n_assign] */
 } K3kMxArgs;
 
 int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
@@ -101,6 +102,12 @@ int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
 /* GATEUP / DOWN for at most 16 assignments without the gather: one workgroup per
  * (assignment, 16-row tile), K % 512 == 0 and K <= 8192, row-major or tiled bank. */
 int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream);
+/* DOWN and the weighted combine of the decode path in one launch: out [T][rows] =
+ * 0 + sum_j wt[t][j] * (slot j's down projection), j ascending, over slots whose expert is
+ * in range and present (k3k_combine's rule); activation terms xhi/xlo [n_assign][K]. */
+int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream);
+/* where k3k_mx_decode_combine is used (faster than the two kernels, LDS fits) */
+int k3k_mx_decode_combine_ok(int n_assign, int topk, int nsplit, int K, int rows);
 
 /* Whether PLAIN may take fp32 activations (xf32): one or two tokens whose bf16 terms fit in
  * 64 KB of LDS, K <= 16384, x 16-byte aligned, the packed matrix under 2 GiB. */

@@ -133,12 +133,16 @@ def test_moe_device_layouts_vs_oracle(gpu, orc, small_layer, prec):
 @pytest.mark.parametrize("T,K,prec,E,I", [(1, 8, 0, 1024, 1536), (2, 8, 0, 1024, 1536),
                                          (1, 8, 1, 1024, 1536), (3, 5, 0, 1024, 1536),
                                          (2, 7, 1, 1024, 1536), (1, 1, 0, 1024, 1536),
-                                         (2, 8, 0, 2048, 4096), (2, 8, 1, 2048, 4096)])
+                                         (2, 8, 0, 2048, 4096), (2, 8, 1, 2048, 4096),
+                                         (1, 2, 1, 1024, 2048), (2, 1, 0, 1024, 2048),
+                                         (1, 1, 0, 1024, 2048)])
 def test_moe_device_decode_path(gpu, orc, k3, T, K, prec, E, I):
     """At most 16 assignments (T * topk) take the decode kernels straight from the router's
     idx, without the gather: one tile per workgroup with K over up to 16 waves for few
     assignments, four tiles with K over two waves when they fill the chip (the 2048 x 4096
-    cases). Outputs against the oracle's per-slot sum (1e-4 * ||ref||inf with two-term
+    cases); down and the combine in one kernel for one or two assignments (the 1-slot
+    case), else down into per-slot rows and the combine kernel. Outputs
+    against the oracle's per-slot sum (1e-4 * ||ref||inf with two-term
     activations, 2e-2 relative with one), row-major and tiled banks bit-identical, a
     NaN-scaled expert, and a dropped expert that contributes nothing and is counted."""
     N = 12
@@ -477,24 +481,28 @@ def test_moe_device_gather_many_workgroups(gpu, orc, k3, prec):
         assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
 
 
-@pytest.mark.parametrize("T,K", [(2, 8), (24, 4)])
-def test_moe_experts_given_routing_invalid_slots(gpu, orc, k3, T, K):
+@pytest.mark.parametrize("T,K,I", [(2, 8, 512), (24, 4, 512), (1, 2, 2048)])
+def test_moe_experts_given_routing_invalid_slots(gpu, orc, k3, T, K, I):
     """k3d_moe_experts with a caller's routing: slots whose expert index lies outside the
     bank (-1, N, 1000) and slots of an absent expert contribute nothing; drops counts only
     the absent expert's slots; the rest equals the oracle's per-slot sum in slot order.
-    (2, 8): 16 assignments, the decode kernels; (24, 4): the gather path."""
-    E, I, N = 1024, 512, 12
-    say(f"case: given routing with invalid slots T={T} K={K}")
+    (2, 8): 16 assignments, the decode kernels; (1, 2): down and the combine in one
+    kernel; (24, 4): the gather path."""
+    E, N = 1024, 12
+    say(f"case: given routing with invalid slots T={T} K={K} I={I}")
     rng = np.random.default_rng(200 + T)
     bank = [k3.gen_expert(E, I, 211, e) for e in range(N)]
     holed = list(bank)
     holed[7] = None
     X = rng.standard_normal((T, E)).astype(np.float32)
     idx = rng.integers(0, N, size=(T, K)).astype(np.int32)
-    idx[0, 1] = -1
-    idx[1, 0] = N
-    idx[-1, K - 1] = 1000
-    idx[0, 0] = 7
+    if T > 1:
+        idx[0, 1] = -1
+        idx[1, 0] = N
+        idx[-1, K - 1] = 1000
+        idx[0, 0] = 7
+    else:                       # one token: an absent slot beside a valid one
+        idx[0] = [3, 7]
     wt = (rng.random((T, K)) + 0.1).astype(np.float32)
     b = gpu.DevBank(holed, E, I, gpu.K3D_LAYOUT_TILED)
     try:
