@@ -683,15 +683,8 @@ __global__ __launch_bounds__(256) void router_small_kernel(float4 *pre, const fl
     }
 }
 
-/* One workgroup per token, one lane per expert (SL experts per lane past 1024): certify
- * the logit, score, then the reference's rule topk times -- largest choice, lowest index
- * among equals, strictly above -inf, none left: idx 0, weight 0 (k3_ops.c:459-467) -- as
- * topk extractions of a wave maximum (DPP) per wave, then over the waves' candidates in
- * wave 0, one barrier between; recompute what matters and repeat; renormalise and scale
- * (k3_ops.c:469-475). nrecomp[t] (optional) counts recomputes. KB: chunk partials loaded
- * per batch (64 for up to 512 experts, one batch at decode sizes). */
+/* router_final_kernel: up to RF_MAXE experts, RF_MAXW waves; RF_KB chunk partials per load batch. */
 constexpr int RF_MAXE = 2048, RF_MAXW = 16, RF_KB = 32;
-constexpr int RS_SEL = 8;           /* router_select_kernel: up to 64 x 8 experts */
 
 /* unsigned order of a non-NaN float that matches its numeric order (-0 as +0) */
 __device__ __forceinline__ uint32_t choice_order(float v)
@@ -755,139 +748,19 @@ __device__ __forceinline__ float key_choice(uint64_t key)
     return __uint_as_float((h & 0x80000000u) ? (h & 0x7fffffffu) : ~h);
 }
 
-/* The selection of a few tokens from router_small_kernel's scored records, one wave per
- * token (up to 64 SL experts): the same rule and the same recompute rounds as
- * router_final_kernel (k3_ops.c:459-475), with every step inside one wave. Lane l holds
- * experts l + 64 i and the largest of its keys; each of the topk extractions is one wave
+/* One workgroup per token: every thread certifies and scores SL experts (tid + nthr i) --
+ * from router_small_kernel's scored records (PRE) or from the chunk partials, summed in
+ * k order and certified here (certify_score) -- into LDS; then wave 0 applies the
+ * reference's rule topk times (largest choice, lowest index among equals, strictly above
+ * -inf, none left: idx 0, weight 0; k3_ops.c:459-467). Lane l of wave 0 holds the keys of
+ * experts l + 64 i (SW of them) and the largest of its keys; each extraction is one wave
  * maximum over those (wave_max_key_fast), after which the lane that held it drops the key
- * and takes its next largest. Lane j keeps the j-th selected key. Uncertified logits that
- * matter are listed by ballots and recomputed with the reference's chain (chain_block on
- * this wave); the selection is redone until none is left. */
-template <int SL>
-__global__ __launch_bounds__(64) void router_select_kernel(int *idx, float *wt, int *nrecomp,
-                                                           const float4 *pre, const float *x,
-                                                           const float *W, const float *bias,
-                                                           int hidden, int n_experts, int topk,
-                                                           int renorm, float routed_scale,
-                                                           ExcTable exc)
-{
-    __shared__ __attribute__((aligned(16))) double prod_sh[2][RF_BLK];
-    __shared__ float ssh[64 * SL];
-    __shared__ int list_sh[RF_LIST];
-    __shared__ double res_sh[RF_LIST];
-    const int lane = threadIdx.x, t = blockIdx.x;
-    float c[SL], cmax[SL], sc[SL];
-    bool unc[SL];
-    float4 pr[SL];
-    float bb[SL];
-#pragma unroll
-    for (int i = 0; i < SL; i++) {
-        const int e = lane + 64 * i;
-        pr[i] = e < n_experts ? pre[(size_t)t * n_experts + e] : make_float4(0.f, 0.f, 0.f, 0.f);
-        bb[i] = (bias && e < n_experts) ? bias[e] : 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < SL; i++) {
-        const int e = lane + 64 * i;
-        sc[i] = pr[i].x;
-        c[i] = e < n_experts ? sc[i] + bb[i] : -INFINITY;
-        unc[i] = e < n_experts && pr[i].z != 0.0f;
-        cmax[i] = unc[i] ? pr[i].y + bb[i] : c[i];          /* choice is monotone in logit */
-        ssh[lane + 64 * i] = sc[i];
-    }
-    int nre = 0;
-    uint64_t mysel = 0ull;                          /* lane j: the j-th selected key */
-    for (int round = 0; round <= n_experts; round++) {
-        uint64_t key[SL];
-        uint64_t head = 0ull;
-#pragma unroll
-        for (int i = 0; i < SL; i++) {
-            const int e = lane + 64 * i;
-            key[i] = c[i] > -INFINITY ? ((uint64_t)choice_order(c[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e)
-                                      : 0ull;
-            head = head > key[i] ? head : key[i];
-        }
-        uint32_t taken = 0u;                        /* bit i: key i was selected */
-        int nsel = 0;
-        uint64_t last = 0ull;
-        mysel = 0ull;
-        for (int j = 0; j < topk; j++) {
-            const uint64_t m = wave_max_key_fast(head);
-            if (m == 0ull) break;                   /* no finite choice left */
-            nsel++;
-            last = m;
-            if (lane == j) mysel = m;
-            if (head == m) {
-                uint64_t h2 = 0ull;
-#pragma unroll
-                for (int i = 0; i < SL; i++) {
-                    if (key[i] == m) {
-                        key[i] = 0ull;
-                        taken |= 1u << i;
-                    }
-                    h2 = h2 > key[i] ? h2 : key[i];
-                }
-                head = h2;
-            }
-        }
-        const float ckth = nsel > 0 ? key_choice(last) : -INFINITY;
-        /* uncertified logits that matter: selected, or able to reach the selection */
-        bool need[SL];
-        bool any = false;
-#pragma unroll
-        for (int i = 0; i < SL; i++) {
-            need[i] = unc[i] && (((taken >> i) & 1u) || nsel < topk || cmax[i] >= ckth);
-            any |= need[i];
-        }
-        if (__ballot(any) == 0ull) break;
-        /* list up to RF_LIST of them (ballot order); the rest wait for the next round */
-        int slot[SL];
-        int base = 0;
-#pragma unroll
-        for (int i = 0; i < SL; i++) {
-            const uint64_t m = __ballot(need[i]);
-            const int below = __popcll(m & ((1ull << lane) - 1ull));
-            slot[i] = need[i] ? base + below : RF_LIST;
-            if (slot[i] >= RF_LIST) slot[i] = RF_LIST;
-            base += __popcll(m);
-            if (slot[i] < RF_LIST) list_sh[slot[i]] = lane + 64 * i;
-        }
-        const int nl = min(base, RF_LIST);
-        __syncthreads();
-        for (int j = 0; j < nl; j++) {
-            const double a = chain_block(prod_sh, W + (size_t)list_sh[j] * hidden, x + (size_t)t * hidden, hidden);
-            if (lane == 0) res_sh[j] = a;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < SL; i++)
-            if (slot[i] < RF_LIST) {
-                sc[i] = router_score((float)res_sh[slot[i]], exc);
-                c[i] = sc[i] + bb[i];
-                cmax[i] = c[i];
-                unc[i] = false;
-                ssh[lane + 64 * i] = sc[i];
-            }
-        nre += nl;
-        __syncthreads();
-    }
-    const int id = mysel != 0ull ? (int)(0xffffffffu - (uint32_t)mysel) : -1;
-    __syncthreads();
-    float w = (lane < topk && id >= 0) ? ssh[id] : 0.0f;
-    if (renorm && topk > 1) {
-        double s = 0.0;
-        for (int j = 0; j < topk; j++) s += (double)__shfl(w, j, 64);   /* j ascending */
-        const float inv = (float)(1.0 / (s + 1e-20));
-        w = w * inv;
-    }
-    if (lane < topk) {
-        idx[(size_t)t * topk + lane] = id >= 0 ? id : 0;
-        wt[(size_t)t * topk + lane] = w * routed_scale;
-    }
-    if (nrecomp && lane == 0) nrecomp[t] = nre;
-}
-
-template <int SL, int KB, bool PRE>
+ * and takes its next largest; lane j keeps the j-th selected key. Uncertified logits that
+ * matter (selected, or able to reach the selection) are listed by ballots, recomputed by
+ * the workgroup with the reference's chain (chain_block) and the selection is redone
+ * until none is left; then renormalise and scale (k3_ops.c:469-475). nrecomp[t]
+ * (optional) counts recomputes. KB: chunk partials loaded per batch. */
+template <int SL, int SW, int KB, bool PRE>
 __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int *idx, float *wt, int *nrecomp,
                                                             const double *part,
                                                             const float *rbound, int ksplit,
@@ -897,37 +770,29 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
                                                             int topk, int renorm,
                                                             float routed_scale, ExcTable exc)
 {
-    __shared__ uint64_t candk[RF_MAXW][64];
-    __shared__ uint64_t selk[64];
-    __shared__ float csh[RF_MAXE], ssh[RF_MAXE];
-    __shared__ int nre_sh, nlist_sh;
+    __shared__ float csh[64 * SW], cmsh[64 * SW], ssh[64 * SW];
+    __shared__ int ush[64 * SW];
+    __shared__ int nlist_sh;
     __shared__ int list_sh[RF_LIST];
     __shared__ double res_sh[RF_LIST];
     __shared__ __attribute__((aligned(16))) double prod_sh[2][RF_BLK];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nthr = blockDim.x;
     const int t = blockIdx.x;
-    if (tid == 0) nre_sh = 0;
-    float c[SL], cmax[SL], sc[SL];
-    bool unc[SL];
 #pragma unroll
     for (int i = 0; i < SL; i++) {
         const int e = tid + nthr * i;
-        c[i] = -INFINITY;
-        cmax[i] = -INFINITY;
-        sc[i] = 0.0f;
-        unc[i] = false;
+        if (e >= 64 * SW) break;
+        float c = -INFINITY, cmax = -INFINITY, sc = 0.0f;
+        bool unc = false;
         if (e < n_experts && PRE) {
             /* scored by router_small_kernel: {score, score of the upper end, uncertified} */
             const float4 pr = reinterpret_cast<const float4 *>(part)[(size_t)t * n_experts + e];
-            sc[i] = pr.x;
             const float bb = bias ? bias[e] : 0.0f;
-            c[i] = sc[i] + bb;
-            cmax[i] = c[i];
-            if (pr.z != 0.0f) {
-                unc[i] = true;
-                cmax[i] = pr.y + bb;
-            }
+            sc = pr.x;
+            c = sc + bb;
+            unc = pr.z != 0.0f;
+            cmax = unc ? pr.y + bb : c;                     /* choice is monotone in logit */
         } else if (e < n_experts) {
             double Q = 0.0, bs = 0.0;
             for (int k0 = 0; k0 < ksplit; k0 += KB) {
@@ -953,136 +818,99 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
                 }
             }
             const Certified cs = certify_score(Q, bs, exc, exc_word((float)Q, exc));
-            sc[i] = cs.sc;
             const float bb = bias ? bias[e] : 0.0f;
-            c[i] = sc[i] + bb;
-            cmax[i] = c[i];
-            if (!cs.ok) {
-                unc[i] = true;
-                cmax[i] = cs.scmax + bb;                    /* choice is monotone in logit */
-            }
+            sc = cs.sc;
+            c = sc + bb;
+            unc = !cs.ok;
+            cmax = unc ? cs.scmax + bb : c;
         }
+        csh[e] = c;
+        cmsh[e] = cmax;
+        ssh[e] = sc;
+        ush[e] = unc ? 1 : 0;
     }
     __syncthreads();
+    int nre = 0;
+    uint64_t mysel = 0ull;                          /* wave 0, lane j: the j-th selected key */
     for (int round = 0; round <= n_experts; round++) {
-        /* Selection keys: (order-preserving bits of the choice, ~expert) as one 64-bit
-         * integer, so that "larger choice, then lower index" is a plain unsigned max; a
-         * choice that is not > -inf (NaN, -inf) is the key 0 and is never selected. */
-        uint64_t key[SL];
-#pragma unroll
-        for (int i = 0; i < SL; i++) {
-            const int e = tid + nthr * i;
-            csh[min(e, RF_MAXE - 1)] = e < n_experts ? c[i] : 0.0f;
-            ssh[min(e, RF_MAXE - 1)] = e < n_experts ? sc[i] : 0.0f;
-            key[i] = (e < n_experts && c[i] > -INFINITY)
-                         ? ((uint64_t)choice_order(c[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e)
-                         : 0ull;
-        }
-        /* 1. each wave extracts its topk largest keys, largest first (topk rounds of a
-         *    wave max; a key taken is zeroed); 2. wave 0 does the same over the waves'
-         *    candidates. Keys are distinct (the expert index is part of the key). */
-        for (int j = 0; j < topk; j++) {
-            uint64_t b = key[0];
-#pragma unroll
-            for (int i = 1; i < SL; i++) b = b > key[i] ? b : key[i];
-            const uint64_t m = wave_max_key(b);
-#pragma unroll
-            for (int i = 0; i < SL; i++)
-                if (key[i] == m) key[i] = 0ull;
-            if (lane == 0) candk[wv][j] = m;
-        }
-        __syncthreads();
         if (wv == 0) {
-            const int ncand = nw * topk;
-            if (ncand <= 64) {
-                uint64_t mk = lane < ncand ? candk[lane / topk][lane % topk] : 0ull;
-                for (int j = 0; j < topk; j++) {
-                    const uint64_t m = wave_max_key(mk);
-                    if (mk == m) mk = 0ull;
-                    if (lane == 0) selk[j] = m;
-                }
-            } else {
-                uint64_t mk[RF_MAXW];
+            uint64_t key[SW];
+            uint64_t head = 0ull;
 #pragma unroll
-                for (int q = 0; q < RF_MAXW; q++) {
-                    const int ci = lane + 64 * q;
-                    mk[q] = ci < ncand ? candk[ci / topk][ci % topk] : 0ull;
-                }
-                for (int j = 0; j < topk; j++) {
-                    uint64_t b = 0ull;
-#pragma unroll
-                    for (int q = 0; q < RF_MAXW; q++) b = b > mk[q] ? b : mk[q];
-                    const uint64_t m = wave_max_key(b);
-#pragma unroll
-                    for (int q = 0; q < RF_MAXW; q++)
-                        if (mk[q] == m) mk[q] = 0ull;
-                    if (lane == 0) selk[j] = m;
-                }
+            for (int i = 0; i < SW; i++) {
+                const int e = lane + 64 * i;
+                const float c = csh[e];
+                key[i] = (e < n_experts && c > -INFINITY)
+                             ? ((uint64_t)choice_order(c) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e)
+                             : 0ull;
+                head = head > key[i] ? head : key[i];
             }
-        }
-        __syncthreads();
-        bool sel[SL];
-#pragma unroll
-        for (int i = 0; i < SL; i++) sel[i] = false;
-        int nsel = 0;
-        float ckth = -INFINITY;
-        for (int j = 0; j < topk; j++) {
-            const uint64_t kj = selk[j];
-            if (kj != 0ull) {
-                const int id = (int)(0xffffffffu - (uint32_t)kj);
+            uint32_t taken = 0u;                    /* bit i: key i was selected */
+            int nsel = 0;
+            uint64_t last = 0ull;
+            mysel = 0ull;
+            for (int j = 0; j < topk; j++) {
+                const uint64_t m = wave_max_key_fast(head);
+                if (m == 0ull) break;               /* no finite choice left */
                 nsel++;
-                ckth = csh[id];
+                last = m;
+                if (lane == j) mysel = m;
+                if (head == m) {
+                    uint64_t h2 = 0ull;
 #pragma unroll
-                for (int i = 0; i < SL; i++)
-                    if (id == tid + nthr * i) sel[i] = true;
+                    for (int i = 0; i < SW; i++) {
+                        if (key[i] == m) {
+                            key[i] = 0ull;
+                            taken |= 1u << i;
+                        }
+                        h2 = h2 > key[i] ? h2 : key[i];
+                    }
+                    head = h2;
+                }
             }
+            const float ckth = nsel > 0 ? key_choice(last) : -INFINITY;
+            /* uncertified logits that matter, listed in ballot order (up to RF_LIST; the
+             * rest wait for the next round) */
+            int base = 0;
+#pragma unroll
+            for (int i = 0; i < SW; i++) {
+                const int e = lane + 64 * i;
+                const bool need = e < n_experts && ush[e] &&
+                                  (((taken >> i) & 1u) || nsel < topk || cmsh[e] >= ckth);
+                const uint64_t m = __ballot(need);
+                const int slot = base + __popcll(m & ((1ull << lane) - 1ull));
+                if (need && slot < RF_LIST) list_sh[slot] = e;
+                base += __popcll(m);
+            }
+            if (lane == 0) nlist_sh = min(base, RF_LIST);
         }
-        /* uncertified logits that matter: selected, or able to reach the selection */
-        bool need_any = false;
-        bool need[SL];
-#pragma unroll
-        for (int i = 0; i < SL; i++) {
-            need[i] = unc[i] && (sel[i] || nsel < topk || cmax[i] >= ckth);
-            need_any |= need[i];
-        }
-        if (tid == 0) nlist_sh = 0;
-        if (!__syncthreads_or(need_any)) break;
-        /* list up to RF_LIST of them; the rest wait for the next round */
-        int slot[SL];
-#pragma unroll
-        for (int i = 0; i < SL; i++) slot[i] = need[i] ? atomicAdd(&nlist_sh, 1) : RF_LIST;
         __syncthreads();
-        const int nl = min(nlist_sh, RF_LIST);
-#pragma unroll
-        for (int i = 0; i < SL; i++)
-            if (slot[i] < RF_LIST) list_sh[slot[i]] = tid + nthr * i;
-        __syncthreads();
+        const int nl = nlist_sh;
+        if (nl == 0) break;
         for (int j = 0; j < nl; j++) {
-            const double a = chain_block(prod_sh, W + (size_t)list_sh[j] * hidden,
-                                         x + (size_t)t * hidden, hidden);
+            const double a = chain_block(prod_sh, W + (size_t)list_sh[j] * hidden, x + (size_t)t * hidden, hidden);
             if (tid == 0) res_sh[j] = a;
         }
         __syncthreads();
-#pragma unroll
-        for (int i = 0; i < SL; i++)
-            if (slot[i] < RF_LIST) {
-                const int e = tid + nthr * i;
-                sc[i] = router_score((float)res_sh[slot[i]], exc);
-                c[i] = sc[i] + (bias ? bias[e] : 0.0f);
-                cmax[i] = c[i];
-                unc[i] = false;
-            }
-        if (tid == 0) nre_sh += nl;
+        if (tid < nl) {
+            const int e = list_sh[tid];
+            const float sc = router_score((float)res_sh[tid], exc);
+            const float c = sc + (bias ? bias[e] : 0.0f);
+            csh[e] = c;
+            cmsh[e] = c;
+            ssh[e] = sc;
+            ush[e] = 0;
+        }
+        nre += nl;
         __syncthreads();
     }
-    __syncthreads();
     if (wv == 0) {
-        const uint64_t kj = lane < topk ? selk[lane] : 0ull;
-        const int id = kj != 0ull ? (int)(0xffffffffu - (uint32_t)kj) : -1;
-        float w = id >= 0 ? ssh[id] : 0.0f;
+        const int id = mysel != 0ull ? (int)(0xffffffffu - (uint32_t)mysel) : -1;
+        float w = (lane < topk && id >= 0) ? ssh[id] : 0.0f;
         if (renorm && topk > 1) {
             double s = 0.0;
-            for (int j = 0; j < topk; j++) s += (double)__shfl(w, j, 64);   /* j ascending */
+            for (int j = 0; j < topk; j++)                  /* j ascending */
+                s += (double)__uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(w), j));
             const float inv = (float)(1.0 / (s + 1e-20));
             w = w * inv;
         }
@@ -1090,7 +918,7 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
             idx[(size_t)t * topk + lane] = id >= 0 ? id : 0;
             wt[(size_t)t * topk + lane] = w * routed_scale;
         }
-        if (nrecomp && lane == 0) nrecomp[t] = nre_sh;
+        if (nrecomp && lane == 0) nrecomp[t] = nre;
     }
 }
 
@@ -1605,34 +1433,22 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
     int nw = (n_experts + 63) / 64;
     if (nw > RF_MAXW) nw = RF_MAXW;
     hipStream_t st = (hipStream_t)stream;
-    /* scored records (a few tokens), else the chunk partials: for up to 64 tokens and 512
-     * experts (<= 8 waves) in one batch of up to 64 loads (more registers, fewer waves per
-     * CU: only while the tokens do not fill the chip) */
     const bool pre = router_small_mode(T, hidden);
-    if (pre && n_experts <= 64 * RS_SEL)
-        hipLaunchKernelGGL((router_select_kernel<RS_SEL>), dim3(T), dim3(64), 0, st, idx, wt, nrecomp,
-                           reinterpret_cast<const float4 *>(part), x, W, bias, hidden, n_experts,
-                           topk, renorm, routed_scale, e);
-    else if (pre && n_experts <= 64 * RF_MAXW)
-        hipLaunchKernelGGL((router_final_kernel<1, RF_KB, true>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
-                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
-                           renorm, routed_scale, e);
-    else if (pre)
-        hipLaunchKernelGGL((router_final_kernel<2, RF_KB, true>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
-                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
-                           renorm, routed_scale, e);
-    else if (n_experts <= 512 && ks <= 64 && T <= 64)
-        hipLaunchKernelGGL((router_final_kernel<1, 64, false>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
-                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
-                           renorm, routed_scale, e);
-    else if (n_experts <= 64 * RF_MAXW)
-        hipLaunchKernelGGL((router_final_kernel<1, RF_KB, false>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
-                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
-                           renorm, routed_scale, e);
-    else
-        hipLaunchKernelGGL((router_final_kernel<2, RF_KB, false>), dim3(T), dim3(64 * nw), 0, st, idx, wt,
-                           nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk,
-                           renorm, routed_scale, e);
+    /* scored records (a few tokens): one wave loads them all; else the chunk partials, a lane
+     * per expert, up to 64 of a lane's partials per load batch for up to 64 tokens and 512
+     * experts (more registers, fewer waves per CU: only while the tokens do not fill the
+     * chip). Wave 0 selects over SW keys per lane: 8 up to 512 experts, else 32. */
+#define K3_RF(SL, SW, KB, PRE, NT)                                                                  \
+    hipLaunchKernelGGL((router_final_kernel<SL, SW, KB, PRE>), dim3(T), dim3(NT), 0, st, idx, wt, nrecomp, \
+                       part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm,        \
+                       routed_scale, e)
+    if (pre && n_experts <= 512) K3_RF(8, 8, RF_KB, true, 64);
+    else if (pre) K3_RF(32, 32, RF_KB, true, 64);
+    else if (n_experts <= 512 && ks <= 64 && T <= 64) K3_RF(1, 8, 64, false, 64 * nw);
+    else if (n_experts <= 512) K3_RF(1, 8, RF_KB, false, 64 * nw);
+    else if (n_experts <= 64 * RF_MAXW) K3_RF(1, 32, RF_KB, false, 64 * nw);
+    else K3_RF(2, 32, RF_KB, false, 64 * nw);
+#undef K3_RF
     K3K_LAUNCH_CHECK("router_final launch");
     return 0;
 }

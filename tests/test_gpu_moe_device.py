@@ -209,7 +209,8 @@ def test_moe_device_tiled_decode_golden(gpu, wl, gold):
     (3, 7168, 384, 8, True), (4, 8192, 96, 8, False), (2, 8200, 64, 4, True),
     (7, 7168, 384, 8, True), (31, 1001, 70, 5, True),
     (33, 1000, 70, 5, False), (64, 7168, 384, 8, False), (100, 520, 131, 16, True),
-    (129, 7168, 384, 8, False), (300, 1000, 200, 5, True)])
+    (129, 7168, 384, 8, False), (300, 1000, 200, 5, True),
+    (2, 1024, 1000, 8, True), (40, 512, 1500, 8, False), (20, 256, 2048, 16, True)])
 def test_router_device_bit_exact(gpu, orc, T, hidden, N, K, biased):
     """Every partial kernel (a workgroup per expert for a few tokens up to 64 chunks of 128
     columns, one lane per chunk past that, the matrix cores for more tokens), widths that
