@@ -445,7 +445,8 @@ __global__ __launch_bounds__(1024) void mx_gemv_small_kernel(K3kMxArgs a, int kw
  * columns > 0 read the zeros, so the B operands need no masking. The K shares are added
  * in order, then GATEUP writes act(gate, up) of assignment a as bf16 terms and DOWN writes
  * contrib[a]. A dropped expert (NULL weights) is skipped; the combine leaves it out.
- * GATEUP's block 0 stores the number of dropped assignments in *a.drops. */
+ * GATEUP's block 0 stores the number of dropped assignments in *a.drops. Two activation
+ * terms share one MFMA: column 0 is the hi term, column 1 the lo term, added at the end. */
 template <int MODE, int NS, int LAYOUT, int TPW>
 __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxArgs a)
 {
@@ -558,8 +559,10 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
     for (int m = 0; m < NM; m++) acc[m][0] = acc[m][1] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
     auto comp = [&](int c, auto slot) {
         constexpr int S = decltype(slot)::value;
-        const uint16_t *hb = r16 == 0 ? &xs[c * 512 + g * 32] : &xs[(size_t)NS * K + g * 32];
-        const uint16_t *lb = r16 == 0 ? &xs[(size_t)K + c * 512 + g * 32] : hb;
+        /* column 0: the hi term, column 1 (two terms): the lo term, the rest: zeros */
+        const uint16_t *hb = r16 == 0            ? &xs[c * 512 + g * 32]
+                             : (NS == 2 && r16 == 1) ? &xs[(size_t)K + c * 512 + g * 32]
+                                                     : &xs[(size_t)NS * K + g * 32];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             uint4 qm[NM];
@@ -579,15 +582,11 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
 #pragma unroll
             for (int p = 0; p < 4; p++) {
                 const uint4 bh = *reinterpret_cast<const uint4 *>(hb + 128 * i + 8 * p);
-                uint4 bl = make_uint4(0, 0, 0, 0);
-                if (NS == 2) bl = *reinterpret_cast<const uint4 *>(lb + 128 * i + 8 * p);
 #pragma unroll
                 for (int m = 0; m < NM; m++) {
                     const uint32_t codes = p == 0 ? qm[m].x : p == 1 ? qm[m].y : p == 2 ? qm[m].z : qm[m].w;
                     const k3_bf16x8 av = k3_dequant8_bf16(codes, so[m]);
                     acc[m][p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh), acc[m][p & 1], 0, 0, 0);
-                    if (NS == 2)
-                        acc[m][p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl), acc[m][p & 1], 0, 0, 0);
                 }
             }
         }
@@ -600,7 +599,8 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
             if (c + 3 < c1) load(c + 3, P1{});
         }
     }
-    /* K shares in order: share 0 adds those of shares 1.. (LDS reused after the products) */
+    /* K shares in order: share 0 adds those of shares 1.. (LDS reused after the products);
+     * then column 0 (hi) + column 1 (lo) */
     k3_f32x4 *red = reinterpret_cast<k3_f32x4 *>(xs);
     if (KS > 1) {
         __syncthreads();
@@ -610,12 +610,24 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
                 red[(((ks - 1) * TPW + wv % TPW) * NM + m) * 64 + lane] = acc[m][0] + acc[m][1];
         __syncthreads();
     }
+    k3_f32x4 own[NM], nxt[NM];                      /* this lane's column, and lane + 1's */
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        own[m] = acc[m][0] + acc[m][1];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) nxt[m][jj] = __shfl_down(own[m][jj], 1, 16);
+    }
     if (ks == 0 && r16 == 0 && tw < ntile) {
         k3_f32x4 sum[NM];
 #pragma unroll
         for (int m = 0; m < NM; m++) {
-            sum[m] = acc[m][0] + acc[m][1];
+            sum[m] = own[m];
             for (int k2 = 1; k2 < KS; k2++) sum[m] += red[(((k2 - 1) * TPW + wv % TPW) * NM + m) * 64 + lane];
+            if (NS == 2) {
+                k3_f32x4 lo = nxt[m];
+                for (int k2 = 1; k2 < KS; k2++) lo += red[(((k2 - 1) * TPW + wv % TPW) * NM + m) * 64 + lane + 1];
+                sum[m] += lo;
+            }
         }
         const int base = tw * 16 + 4 * g;
         if (MODE == K3K_MX_GATEUP) {
@@ -644,12 +656,13 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
  * and out[t][row] = 0 + sum_j wt[t][j] * slot j's sum, j ascending, over the slots whose
  * expert is in range and present in the bank -- the combine's rule and order
  * (k3_ops.c:641-642). An absent slot's wave reads through an empty descriptor (zeros) and
- * its sum is left out. */
+ * its sum is left out. Two activation terms share one MFMA (columns 0 and 1), each term's
+ * shares are added in order, then hi + lo. */
 template <int NS, int LAYOUT>
 __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* [topk][NS][K], zeros[512] */
-    __shared__ float red[16 * 16];                                  /* [slot, share][16 rows] */
+    __shared__ float red[16 * 2 * 16];                              /* [slot, share][term][16 rows] */
     __shared__ int vsh[16];
     __shared__ float wsh[16];
     constexpr int WPOL = LAYOUT == 1 ? K3_LD_NT : K3_LD_DEFAULT;
@@ -725,8 +738,10 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
     const uint16_t *zb = &xs[(size_t)topk * NS * K + g * 32];
     auto comp = [&](int c, auto slot) {
         constexpr int S = decltype(slot)::value;
-        const uint16_t *hb = r16 == 0 ? &xs[(size_t)j * NS * K + c * 512 + g * 32] : zb;
-        const uint16_t *lb = r16 == 0 ? &xs[((size_t)j * NS + 1) * K + c * 512 + g * 32] : zb;
+        /* column 0: the hi term, column 1 (two terms): the lo term, the rest: zeros */
+        const uint16_t *hb = r16 == 0              ? &xs[(size_t)j * NS * K + c * 512 + g * 32]
+                             : (NS == 2 && r16 == 1) ? &xs[((size_t)j * NS + 1) * K + c * 512 + g * 32]
+                                                     : zb;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t sw = LAYOUT == 1 ? sq[S].x >> (8 * i)
@@ -744,10 +759,6 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
                 const uint32_t codes = p == 0 ? qm.x : p == 1 ? qm.y : p == 2 ? qm.z : qm.w;
                 const k3_bf16x8 av = k3_dequant8_bf16(codes, so);
                 acc[p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh), acc[p & 1], 0, 0, 0);
-                if (NS == 2) {
-                    const uint4 bl = *reinterpret_cast<const uint4 *>(lb + 128 * i + 8 * p);
-                    acc[p & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl), acc[p & 1], 0, 0, 0);
-                }
             }
         }
     };
@@ -759,19 +770,25 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
             if (c + 3 < c1) load(c + 3, P1{});
         }
     }
-    /* lanes of token column 0 hold the tile's 16 rows, four each */
-    if (r16 == 0) {
+    /* lanes of token column 0 (hi) and 1 (lo) hold the tile's 16 rows, four each */
+    if (r16 < NS) {
         const k3_f32x4 sum = acc[0] + acc[1];
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) red[(j * KS + ks) * 16 + 4 * g + jj] = sum[jj];
+        for (int jj = 0; jj < 4; jj++) red[((j * KS + ks) * 2 + r16) * 16 + 4 * g + jj] = sum[jj];
     }
     __syncthreads();
     if (tid < 16 && tile * 16 + tid < rows) {
         float o = 0.0f;
         for (int jj = 0; jj < topk; jj++) {
             if (!vsh[jj]) continue;
-            float d = red[(jj * KS) * 16 + tid];
-            for (int k2 = 1; k2 < KS; k2++) d += red[(jj * KS + k2) * 16 + tid];
+            /* each term's shares in order, then hi + lo */
+            float d = red[((jj * KS) * 2) * 16 + tid];
+            for (int k2 = 1; k2 < KS; k2++) d += red[((jj * KS + k2) * 2) * 16 + tid];
+            if (NS == 2) {
+                float l = red[((jj * KS) * 2 + 1) * 16 + tid];
+                for (int k2 = 1; k2 < KS; k2++) l += red[((jj * KS + k2) * 2 + 1) * 16 + tid];
+                d += l;
+            }
             o = __fadd_rn(o, __fmul_rn(wsh[jj], d));
         }
         a.out[(size_t)t * rows + tile * 16 + tid] = o;
@@ -798,12 +815,16 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
  * While chunk c is multiplied, the weight/scale loads and the activation loads of chunk
  * c+1 are in flight (activations issued first, so waiting for them leaves the weight
  * loads outstanding).
+ * Passes of up to 8 tokens with two activation terms put both terms in one MFMA column
+ * block (PACK): column t is token t's hi term, column 8 + t its lo term, so each weight
+ * fragment takes one MFMA instead of two; the epilogue adds column 8 + t to column t.
  */
 template <int MODE, int MT, int NS, int PT, int NB, int NW, int WPE, int LAYOUT, int DEPTH>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
 void mx_moe_kernel(K3kMxArgs a)
 {
     static_assert(PT <= 16 * NB, "a pass fits the MFMA column blocks");
+    constexpr bool PACK = NS == 2 && PT <= 8 && NB == 1;     /* hi and lo in one column block */
     constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
     constexpr int KC = 512, SPC = 4, LDT = KC + 8;           /* LDS row: 16-byte pad */
     /* tiled MXFP4 weights are streamed once per pass and non-temporal; row-major ones keep
@@ -886,10 +907,15 @@ void mx_moe_kernel(K3kMxArgs a)
                 gsrc[i] = ((uint32_t)xr * (uint32_t)K + (uint32_t)lane * 8u) * 2u;
             }
         }
-        /* B operand rows: token column nb*16 + r16 of the pass, or the zero row */
+        /* B operand rows: token column nb*16 + r16 of the pass, or the zero row; PACK: token
+         * r16 % 8 of term r16 / 8 */
         int brow[NB];
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++) brow[nb] = nb * 16 + r16 < ntok ? nb * 16 + r16 : PT;
+        for (int nb = 0; nb < NB; nb++) {
+            const int tk = PACK ? (r16 & 7) : nb * 16 + r16;
+            brow[nb] = tk < ntok ? tk : PT;
+        }
+        const int bterm = PACK ? (r16 >> 3) : 0;
 
         k3_f32x4 acc[MT][NB];
 #pragma unroll
@@ -976,12 +1002,12 @@ void mx_moe_kernel(K3kMxArgs a)
                 uint4 bh[NB][4], bl[NB][4];
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++) {
-                    const uint4 *bp = reinterpret_cast<const uint4 *>(&bsh[buf][0][brow[nb]][(4 * d + g) * 32]);
+                    const uint4 *bp = reinterpret_cast<const uint4 *>(&bsh[buf][bterm][brow[nb]][(4 * d + g) * 32]);
                     const uint4 *bq = reinterpret_cast<const uint4 *>(&bsh[buf][NS - 1][brow[nb]][(4 * d + g) * 32]);
 #pragma unroll
                     for (int pp = 0; pp < 4; pp++) {
                         bh[nb][pp] = bp[pp];
-                        if (NS == 2) bl[nb][pp] = bq[pp];
+                        if (NS == 2 && !PACK) bl[nb][pp] = bq[pp];
                     }
                 }
                 uint4 qq[MT];
@@ -1014,7 +1040,7 @@ void mx_moe_kernel(K3kMxArgs a)
 #pragma unroll
                         for (int nb = 0; nb < NB; nb++) {
                             acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh[nb][pp]), acc[m][nb], 0, 0, 0);
-                            if (NS == 2)
+                            if (NS == 2 && !PACK)
                                 acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl[nb][pp]), acc[m][nb], 0, 0, 0);
                         }
                     }
@@ -1033,11 +1059,18 @@ void mx_moe_kernel(K3kMxArgs a)
             if (NSLOT == 2 && c + 1 < nchunk) chunk(c + 1, I1{});
         }
 
-        /* epilogue: lane holds token column nb*16 + r16, rows 4g..4g+3 of each tile */
+        /* epilogue: lane holds token column nb*16 + r16, rows 4g..4g+3 of each tile; PACK:
+         * column t gains column 8 + t (hi + lo) */
+        if (PACK) {
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) acc[m][0][jj] += __shfl_down(acc[m][0][jj], 8, 16);
+        }
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) {
             const int tk = nb * 16 + r16;
-            if (tk >= ntok) continue;
+            if (tk >= ntok || (PACK && r16 >= 8)) continue;
             const int orow = a.perm[off + tok0 + tk];
             for (int m = 0; m < RT; m++) {
                 const int base = rb * rpg + wv * rpw + 16 * m + 4 * g;
@@ -1606,6 +1639,9 @@ extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
     return 0;
 }
 
+/* dynamic LDS of mx_decode_combine_kernel: all of the CU's 160 KB but its 4 KB of static arrays */
+#define K3_DC_LDS_MAX (160 * 1024 - 4096)
+
 /* The fused kernel is used where it is faster than mx_decode_kernel DOWN + the combine
  * kernel (measured: one or two assignments, 7168 x 2048 -- 18.3 against 20.3 us for one
  * expert's FFN; at eight it is slower, 24 against 19 us) and the slots' activation terms
@@ -1614,7 +1650,7 @@ extern "C" int k3k_mx_decode_combine_ok(int n_assign, int topk, int nsplit, int 
 {
     const long ntile = (rows + 15) / 16;
     const bool wide = (long)n_assign * ((ntile + 3) / 4) >= 256 || K / 512 < 4;
-    return !wide && topk >= 1 && topk <= 16 && (size_t)topk * nsplit * K * 2 + 1024 <= 160 * 1024 - 2048;
+    return !wide && topk >= 1 && topk <= 16 && (size_t)topk * nsplit * K * 2 + 1024 <= K3_DC_LDS_MAX;
 }
 
 extern "C" int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream)
@@ -1629,7 +1665,7 @@ extern "C" int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream)
     int ks = 16 / a->topk;
     if (ks > nchunk) ks = nchunk;
     const int T = a->n_assign / a->topk, ntile = (a->rows + 15) / 16;
-    if ((size_t)a->topk * a->nsplit * a->K * 2 + 1024 > 160 * 1024 - 2048)
+    if ((size_t)a->topk * a->nsplit * a->K * 2 + 1024 > K3_DC_LDS_MAX)
         return k3k_fail("mx_decode_combine: LDS", hipErrorInvalidValue);
     const size_t lds = (size_t)a->topk * a->nsplit * a->K * 2 + 1024;
     void (*kern)(K3kMxArgs);
@@ -1642,8 +1678,10 @@ extern "C" int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream)
                               reinterpret_cast<const void *>(mx_decode_combine_kernel<1, 1>),
                               reinterpret_cast<const void *>(mx_decode_combine_kernel<2, 0>),
                               reinterpret_cast<const void *>(mx_decode_combine_kernel<1, 0>)};
-        for (int i = 0; i < 4; i++)
-            (void)hipFuncSetAttribute(ks4[i], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 2048);
+        for (int i = 0; i < 4; i++) {
+            const hipError_t e = hipFuncSetAttribute(ks4[i], hipFuncAttributeMaxDynamicSharedMemorySize, K3_DC_LDS_MAX);
+            if (e != hipSuccess) return k3k_fail("mx_decode_combine: LDS attribute", e);
+        }
         attr = true;
     }
     hipLaunchKernelGGL(kern, dim3(T * ntile), dim3(64 * a->topk * ks), lds, (hipStream_t)stream, *a);
