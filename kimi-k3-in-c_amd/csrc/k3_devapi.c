@@ -390,10 +390,24 @@ static int moe_check(const char *fn, int hidden, int inter, int n_experts, int t
     return 0;
 }
 
+/* The router's selection done inside the decode gate/up kernel (a few tokens): the scored
+ * records of k3k_router_partial and what the selection needs; idx / wt are written there. */
+typedef struct {
+    const void *pre;
+    const float *rw, *rbias;
+    int renorm;
+    float rscale;
+    const K3kExc *exc;
+    int *nrecomp;
+    int *idx;
+    float *wt;
+} RouterSel;
+
 static int moe_experts_ws(float *out, const int *idx, const float *wt, const float *x, int T,
                           const void *bank, int layout, int hidden, int inter, int n_experts,
                           int topk, int act, float b1, float b2, int prec, const MoeWs *w,
-                          int *perm_out, int *offsets_out, int *drops_out, void *stream)
+                          int *perm_out, int *offsets_out, int *drops_out, const RouterSel *sel,
+                          void *stream)
 {
     int *perm = perm_out ? perm_out : w->perm;
     int *offsets = offsets_out ? offsets_out : w->offsets;
@@ -425,7 +439,20 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
         a.alo = w->alo;
         a.rows = inter;
         a.K = hidden;
+        if (sel) {
+            a.sel = 1;
+            a.pre = sel->pre;
+            a.rw = sel->rw;
+            a.rbias = sel->rbias;
+            a.renorm = sel->renorm;
+            a.rscale = sel->rscale;
+            a.exc = *sel->exc;
+            a.idx_out = sel->idx;
+            a.wt_out = sel->wt;
+            a.nrecomp = sel->nrecomp;
+        }
         if (k3k_mx_decode(K3K_MX_GATEUP, &a, stream)) return fail("mx_decode gateup");
+        a.sel = 0;
         k3k_prof_mark(stream, K3D_STAGE_GATEUP);
         a.xhi = w->ahi;
         a.xlo = w->alo;
@@ -534,7 +561,7 @@ int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x,
     moe_layout(&c, &w, T, hidden, inter, n_experts, topk, prec);
     k3k_prof_mark(stream, K3D_STAGE_BEGIN);
     return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
-                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, stream);
+                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, stream);
 }
 
 int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const float *router_w,
@@ -554,12 +581,26 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
     moe_layout(&c, &w, T, hidden, inter, n_experts, topk, prec);
     router_layout(&c, &r, T, hidden, n_experts);
     k3k_prof_mark(stream, K3D_STAGE_BEGIN);
+    if (moe_decode_ok(T, hidden, inter, topk, x) && k3k_router_small(T, hidden) && n_experts <= 512 &&
+        !perm_out && !offsets_out) {
+        /* a few tokens: the scored logits, then the decode gate/up kernel selects the
+         * experts itself (no selection kernel) and writes idx / wt */
+        const K3kExc *exc;
+        rc = exc_table(&exc);
+        if (rc) return rc;
+        if (k3k_router_partial(r.part, r.rbound, x, T, router_w, hidden, n_experts, r.chunk, exc, stream))
+            return fail("router_partial");
+        k3k_prof_mark(stream, K3D_STAGE_ROUTER);
+        const RouterSel sel = {r.part, router_w, bias, renorm, routed_scale, exc, r.nrecomp, idx, wt};
+        return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
+                              b1, b2, prec, &w, NULL, NULL, drops_out, &sel, stream);
+    }
     rc = router_run(idx, wt, x, T, router_w, bias, hidden, n_experts, topk, renorm, routed_scale,
                     &r, stream);
     if (rc) return rc;
     k3k_prof_mark(stream, K3D_STAGE_ROUTER);
     return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
-                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, stream);
+                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, stream);
 }
 
 /* ---- tiled expert layout ---------------------------------------------------------------- */

@@ -43,6 +43,7 @@
  *   DOWN   expert jobs; activation rows are assignments; contrib[assignment][hidden].
  */
 #include "k3_common.h"
+#include "k3_select.h"
 
 #include <type_traits>
 #include "k3k.h"
@@ -445,9 +446,11 @@ __global__ __launch_bounds__(1024) void mx_gemv_small_kernel(K3kMxArgs a, int kw
  * columns > 0 read the zeros, so the B operands need no masking. The K shares are added
  * in order, then GATEUP writes act(gate, up) of assignment a as bf16 terms and DOWN writes
  * contrib[a]. A dropped expert (NULL weights) is skipped; the combine leaves it out.
- * GATEUP's block 0 stores the number of dropped assignments in *a.drops. Two activation
+ * DOWN's block 0 stores the number of dropped assignments in *a.drops. SEL (gate/up of a
+ * few tokens): the workgroup first selects its token's experts from the router's scored
+ * records (select_rounds), so no separate selection kernel runs. Two activation
  * terms share one MFMA: column 0 is the hi term, column 1 the lo term, added at the end. */
-template <int MODE, int NS, int LAYOUT, int TPW>
+template <int MODE, int NS, int LAYOUT, int TPW, bool SEL = false>
 __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* [NS][K], zeros[512] */
@@ -471,7 +474,8 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
         const ExpertQDev b = bank[e];
         return b.p1 && b.s1 && b.p3 && b.s3 && b.p2 && b.s2;
     };
-    if (MODE == K3K_MX_GATEUP) {
+    /* the dropped assignments, counted by DOWN's block 0 (the slots are final by then) */
+    if (MODE == K3K_MX_DOWN && a.drops) {
         if (blockIdx.x == 0 && tid == 0) {
             int nd = 0;
             for (int i = 0; i < a.n_assign; i++) {
@@ -481,18 +485,7 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
             *a.drops = nd;
         }
     }
-    const int eix = a.idx[asg];
-    ExpertQDev q = {};
-    if (eix >= 0 && eix < a.n_experts) q = bank[eix];
-    const uint8_t *pm[NM], *sm[NM];
-    if (MODE == K3K_MX_GATEUP) {
-        pm[0] = q.p1; sm[0] = q.s1;
-        pm[NM - 1] = q.p3; sm[NM - 1] = q.s3;
-    } else {
-        pm[0] = q.p2; sm[0] = q.s2;
-    }
-    if (!(q.p1 && q.s1 && q.p3 && q.s3 && q.p2 && q.s2)) return;   /* dropped or out of range */
-    /* activation loads first: they return while the weights stream */
+    /* activation loads first: they return while the selection runs and the weights stream */
     float4 xv[XPT];
     uint4 hv[XPT];
     const int nq = MODE == K3K_MX_GATEUP ? K >> 2 : NS * (K >> 3);
@@ -507,6 +500,59 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
                                                                 8 * (i % (K >> 3)))
                            : make_uint4(0, 0, 0, 0);
     }
+    int eix;
+    if constexpr (SEL) {
+        /* the token's experts: the router's selection from router_small's scored records,
+         * the same in every workgroup of the token; its first workgroup writes idx / wt */
+        __shared__ SelSmem<8> ssm;
+        __shared__ int sel_id[64];
+        const int t = asg / a.topk, j = asg % a.topk;
+        ExcTable exc;
+        exc.pairs = a.exc.pairs;
+        exc.index = a.exc.index;
+        exc.bits = a.exc.bits;
+        exc.kmin = a.exc.kmin;
+        exc.kmax = a.exc.kmax;
+        exc.base = a.exc.base;
+        exc.mmin = a.exc.mmin;
+        exc.mwords = a.exc.mwords;
+        exc.n = a.exc.n;
+        const float4 *pre = reinterpret_cast<const float4 *>(a.pre);
+        for (int e = tid; e < 64 * 8; e += nthr)
+            select_put_record(ssm, e, e < a.n_experts ? pre[(size_t)t * a.n_experts + e] : make_float4(0.f, 0.f, 0.f, 0.f),
+                              e < a.n_experts ? (a.rbias ? a.rbias[e] : 0.0f) : -INFINITY);
+        __syncthreads();
+        int nre;
+        const uint64_t mysel = select_rounds<8>(ssm, a.xf32 + (size_t)t * K, a.rw, a.rbias, K, a.n_experts,
+                                                a.topk, exc, nre);
+        if (wv == 0) {
+            int id;
+            float w;
+            select_weight<8>(ssm, mysel, a.topk, a.renorm, a.rscale, id, w);
+            if (lane < a.topk) {
+                sel_id[lane] = id >= 0 ? id : 0;            /* none left: expert 0, weight 0 */
+                if (j == 0 && tg == 0) {
+                    a.idx_out[(size_t)t * a.topk + lane] = id >= 0 ? id : 0;
+                    a.wt_out[(size_t)t * a.topk + lane] = w;
+                }
+            }
+            if (j == 0 && tg == 0 && lane == 0 && a.nrecomp) a.nrecomp[t] = nre;
+        }
+        __syncthreads();
+        eix = sel_id[j];
+    } else {
+        eix = a.idx[asg];
+    }
+    ExpertQDev q = {};
+    if (eix >= 0 && eix < a.n_experts) q = bank[eix];
+    const uint8_t *pm[NM], *sm[NM];
+    if (MODE == K3K_MX_GATEUP) {
+        pm[0] = q.p1; sm[0] = q.s1;
+        pm[NM - 1] = q.p3; sm[NM - 1] = q.s3;
+    } else {
+        pm[0] = q.p2; sm[0] = q.s2;
+    }
+    if (!(q.p1 && q.s1 && q.p3 && q.s3 && q.p2 && q.s2)) return;   /* dropped or out of range */
     const uint32_t prow = LAYOUT == 1 ? (uint32_t)ntile * 16u : (uint32_t)rows;
     k3_rsrc rp[NM], rs[NM];
 #pragma unroll
@@ -675,6 +721,17 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
     const int t = blockIdx.x / ntile, tile = blockIdx.x % ntile;
     const int c0 = ks * nchunk / KS, c1 = (ks + 1) * nchunk / KS;
     const ExpertQDev *bank = reinterpret_cast<const ExpertQDev *>(a.bank);
+    if (a.drops && blockIdx.x == 0 && tid == 0) {          /* dropped assignments */
+        int nd = 0;
+        for (int i = 0; i < a.n_assign; i++) {
+            const int e = a.idx[i];
+            if (e >= 0 && e < a.n_experts) {
+                const ExpertQDev b = bank[e];
+                nd += !(b.p1 && b.s1 && b.p3 && b.s3 && b.p2 && b.s2);
+            }
+        }
+        *a.drops = nd;
+    }
     const int eix = a.idx[t * topk + j];
     const float wj = a.wt[t * topk + j];                    /* in flight with the rest */
     ExpertQDev q = {};
@@ -1626,7 +1683,18 @@ extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
 #define K3_DEC(MODE, TPW)                                                                          \
     kern = tiled ? (ns2 ? mx_decode_kernel<MODE, 2, 1, TPW> : mx_decode_kernel<MODE, 1, 1, TPW>)     \
                  : (ns2 ? mx_decode_kernel<MODE, 2, 0, TPW> : mx_decode_kernel<MODE, 1, 0, TPW>)
-    if (mode == K3K_MX_GATEUP) {
+#define K3_DEC_SEL(TPW)                                                                            \
+    kern = tiled ? (ns2 ? mx_decode_kernel<K3K_MX_GATEUP, 2, 1, TPW, true>                           \
+                        : mx_decode_kernel<K3K_MX_GATEUP, 1, 1, TPW, true>)                          \
+                 : (ns2 ? mx_decode_kernel<K3K_MX_GATEUP, 2, 0, TPW, true>                           \
+                        : mx_decode_kernel<K3K_MX_GATEUP, 1, 0, TPW, true>)
+    if (mode == K3K_MX_GATEUP && a->sel) {
+        if (!a->pre || !a->rw || !a->idx_out || !a->wt_out || a->n_experts > 512 || a->topk > 64 ||
+            a->n_assign % a->topk)
+            return k3k_fail("mx_decode: selection arguments", hipErrorInvalidValue);
+        if (wide) K3_DEC_SEL(4);
+        else K3_DEC_SEL(1);
+    } else if (mode == K3K_MX_GATEUP) {
         if (wide) K3_DEC(K3K_MX_GATEUP, 4);
         else K3_DEC(K3K_MX_GATEUP, 1);
     } else {
@@ -1634,6 +1702,7 @@ extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
         else K3_DEC(K3K_MX_DOWN, 1);
     }
 #undef K3_DEC
+#undef K3_DEC_SEL
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * tpw * ks), lds, (hipStream_t)stream, *a);
     K3K_LAUNCH_CHECK("mx_decode launch");
     return 0;

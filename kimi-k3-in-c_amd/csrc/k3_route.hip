@@ -6,6 +6,7 @@
  */
 #include "k3_common.h"
 #include "k3_expf.h"
+#include "k3_select.h"
 #include "k3k.h"
 
 #include <string.h>
@@ -38,65 +39,10 @@ __global__ void split_kernel(uint16_t *hi, uint16_t *lo, const float *x, size_t 
 
 /* ---- router scores ------------------------------------------------------------------
  * logit[t][e] = the reference's own fp64 chain: acc = 0; for k ascending: acc += (double)
- * W[e][k] * (double)x[t][k] (k3_ops.c:446-450). A product of two floats is exact in fp64,
- * so fma(w, x, acc) rounds exactly like the separate multiply and add; one lane runs one
- * (token, expert) chain in the reference's order, so the logit is bit-identical to the
- * reference's by construction. Then score = 1/(1+expf(-(float)acc)) with the host libm's
- * expf (k3_ops.c:451) and choice = score + bias (k3_ops.c:452).
- *
- * A workgroup covers EB experts x TB tokens (EB*TB = 256 lanes): EB = 4, TB = 64 (a wave
- * is 64 tokens of one expert) when there are many tokens, EB = 64, TB = 4 (a wave is 64
- * experts of one token) when there are few. K walks in chunks of RC columns; W and x of the
- * chunk are staged in LDS (double buffered) and each lane reads its W row and x row 4
- * columns at a time. */
-
-struct ExcTable {
-    const uint32_t *pairs;      /* sorted (key bits of v, libm expf(v) bits) */
-    const uint32_t *index;      /* index[b] = first pair with (key >> 12) - base >= b */
-    const uint32_t *bits;       /* membership bitmap over |key| in [mmin, mmax], per sign */
-    uint32_t kmin, kmax, base, mmin, mwords;
-    int n;
-};
-
-/* The word of the exception bitmap that holds v = -logit's magnitude, or 0 outside the
- * bitmap's range. A buffer load with no branch around it (an offset past the end reads 0),
- * so that a caller can issue it early and consume it after other work. */
-__device__ __forceinline__ uint32_t exc_word(float logit, const ExcTable &x)
-{
-    const uint32_t key = __float_as_uint(-logit), mag = key & 0x7fffffffu;
-    const uint32_t bi = mag - x.mmin, w = bi >> 5;
-    const bool in = x.n > 0 && mag >= x.mmin && w < x.mwords;
-    const k3_rsrc r = k3_make_rsrc(x.bits, x.n > 0 ? 8u * x.mwords : 0u);
-    return k3_bload4(r, in ? ((key >> 31) * x.mwords + w) * 4u : 0xfffffff0u);
-}
-
-/* libm-exact score 1/(1+expf(v)), v = -logit: the deterministic correctly rounded
- * candidate, replaced where the host libm's expf differs (exception table built at build
- * time from that libm). The bitmap word (exc_word) decides membership; only members search
- * their bucket (key >> 12, at most 17 pairs). */
-__device__ __forceinline__ float router_score_w(float logit, uint32_t word, const ExcTable &x)
-{
-    const float v = -logit;
-    float E = k3_expf_det(v);
-    const uint32_t key = __float_as_uint(v);
-    const uint32_t mag = key & 0x7fffffffu;
-    if (x.n > 0 && mag >= x.mmin && ((word >> ((mag - x.mmin) & 31)) & 1u)) {
-        const uint32_t bkt = (key >> 12) - x.base;
-        int lo = (int)x.index[bkt], hi = (int)x.index[bkt + 1];
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (x.pairs[2 * mid] < key) lo = mid + 1;
-            else hi = mid;
-        }
-        if (lo < x.n && x.pairs[2 * lo] == key) E = __uint_as_float(x.pairs[2 * lo + 1]);
-    }
-    return 1.0f / (1.0f + E);
-}
-
-__device__ __forceinline__ float router_score(float logit, const ExcTable &x)
-{
-    return router_score_w(logit, exc_word(logit, x), x);
-}
+ * W[e][k] * (double)x[t][k] (k3_ops.c:446-450), score = 1/(1+expf(-(float)acc)) with the
+ * host libm's expf (k3_ops.c:451) and choice = score + bias (k3_ops.c:452). The exact
+ * score (router_score), the reference's chain (chain_block) and the selection
+ * (select_rounds) are in k3_select.h, shared with the decode kernels. */
 
 /* ---- router logits, certified ---------------------------------------------------------
  * The reference's logit is one sequential fp64 chain per (token, expert):
@@ -396,55 +342,6 @@ __global__ __launch_bounds__(256) void router_partial_small_kernel(double *part,
         }
 }
 
-/* The reference's own chain for one logit (the fallback of the certification), computed
- * by a whole workgroup: acc = 0; for k ascending: acc = fma(w_k, x_k, acc). The chain is one dependent fp64 add per column, so one thread runs it
- * (thread 0), adding the exact products w_k x_k (a product of two floats is exact in
- * fp64, so acc + w_k x_k rounds like fma(w_k, x_k, acc)) that the other waves write into
- * an LDS ring of two RF_BLK-column blocks one block ahead. Every thread of the workgroup
- * calls it; the result is valid in thread 0. */
-constexpr int RF_BLK = 512, RF_LIST = 64;
-
-__device__ double chain_block(double (*ring)[RF_BLK], const float *w, const float *x, int hidden)
-{
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    const bool many = nthr > 64;                 /* producers: waves 1.., else every lane */
-    const int p0 = many ? tid - 64 : tid, np = many ? nthr - 64 : nthr;
-    const int nb = (hidden + RF_BLK - 1) / RF_BLK;
-    auto produce = [&](int b) {
-        if (p0 < 0) return;
-        double *dst = ring[b & 1];
-        for (int i = p0; i < RF_BLK; i += np) {
-            const int k = b * RF_BLK + i;
-            dst[i] = k < hidden ? (double)w[k] * (double)x[k] : 0.0;
-        }
-    };
-    double acc = 0.0;
-    produce(0);
-    __syncthreads();
-    for (int b = 0; b < nb; b++) {
-        if (b + 1 < nb) produce(b + 1);
-        if (tid == 0) {
-            const double2 *p2 = reinterpret_cast<const double2 *>(ring[b & 1]);
-            const int n = min(RF_BLK, hidden - b * RF_BLK);
-            int i = 0;
-            for (; i + 8 <= n; i += 8) {
-                const double2 a0 = p2[i / 2], a1 = p2[i / 2 + 1], a2 = p2[i / 2 + 2], a3 = p2[i / 2 + 3];
-                acc += a0.x;
-                acc += a0.y;
-                acc += a1.x;
-                acc += a1.y;
-                acc += a2.x;
-                acc += a2.y;
-                acc += a3.x;
-                acc += a3.y;
-            }
-            for (; i < n; i++) acc += ring[b & 1][i];
-        }
-        __syncthreads();
-    }
-    return acc;
-}
-
 /* The float next to finite f towards +inf (up) or -inf (down). */
 __device__ __forceinline__ float next_float(float f, bool up)
 {
@@ -686,80 +583,12 @@ __global__ __launch_bounds__(256) void router_small_kernel(float4 *pre, const fl
 /* router_final_kernel: up to RF_MAXE experts, RF_MAXW waves; RF_KB chunk partials per load batch. */
 constexpr int RF_MAXE = 2048, RF_MAXW = 16, RF_KB = 32;
 
-/* unsigned order of a non-NaN float that matches its numeric order (-0 as +0) */
-__device__ __forceinline__ uint32_t choice_order(float v)
-{
-    const uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-/* 32-bit max / min of the wave by DPP, the same in every lane: pairs, quads (quad_perm),
- * 8 (row half mirror), 16 (row mirror), then rows 0-1 and 2-3 (row_bcast15 into rows 1,
- * 3) and rows 0-3 (row_bcast31 into rows 2, 3), so lane 63 holds the result. */
-/* (rows outside RM read the identity of the operation, so each step is one DPP max/min) */
-template <int CTRL, int RM, uint32_t ID>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v)
-{
-    return (uint32_t)__builtin_amdgcn_update_dpp((int)ID, (int)v, CTRL, RM, 0xf, false);
-}
-
-template <bool MAX>
-__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v)
-{
-    constexpr uint32_t ID = MAX ? 0u : 0xffffffffu;
-    auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
-    v = op(v, dpp_u32<0xB1, 0xf, ID>(v));      /* quad_perm [1,0,3,2] */
-    v = op(v, dpp_u32<0x4E, 0xf, ID>(v));      /* quad_perm [2,3,0,1] */
-    v = op(v, dpp_u32<0x141, 0xf, ID>(v));     /* row_half_mirror */
-    v = op(v, dpp_u32<0x140, 0xf, ID>(v));     /* row_mirror */
-    v = op(v, dpp_u32<0x142, 0xa, ID>(v));     /* row_bcast15 */
-    v = op(v, dpp_u32<0x143, 0xc, ID>(v));     /* row_bcast31 */
-    return __builtin_amdgcn_readlane(v, 63);
-}
-
-/* Selection key (order-preserving bits of the choice) << 32 | ~expert: the largest key is
- * the largest choice, then the lowest expert. The wave's largest key, in every lane: the
- * largest high word, then the largest low word among the lanes holding it. */
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k)
-{
-    const uint32_t hi = wave_reduce_u32<true>((uint32_t)(k >> 32));
-    const uint32_t lo = wave_reduce_u32<true>((uint32_t)(k >> 32) == hi ? (uint32_t)k : 0u);
-    return ((uint64_t)hi << 32) | lo;
-}
-
-/* The wave's largest key as wave_max_key, with the second reduction only on a tie of the
- * high words (choices): otherwise the one lane holding the largest choice gives its key. */
-__device__ __forceinline__ uint64_t wave_max_key_fast(uint64_t k)
-{
-    const uint32_t hi = wave_reduce_u32<true>((uint32_t)(k >> 32));
-    const uint64_t at = __ballot((uint32_t)(k >> 32) == hi);
-    uint32_t lo;
-    if (__popcll(at) == 1)
-        lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, (int)(__ffsll((unsigned long long)at) - 1));
-    else
-        lo = wave_reduce_u32<true>((uint32_t)(k >> 32) == hi ? (uint32_t)k : 0u);
-    return ((uint64_t)hi << 32) | lo;
-}
-
-/* The choice a selection key carries (choice_order inverted; -0 comes back as +0). */
-__device__ __forceinline__ float key_choice(uint64_t key)
-{
-    const uint32_t h = (uint32_t)(key >> 32);
-    return __uint_as_float((h & 0x80000000u) ? (h & 0x7fffffffu) : ~h);
-}
-
 /* One workgroup per token: every thread certifies and scores SL experts (tid + nthr i) --
  * from router_small_kernel's scored records (PRE) or from the chunk partials, summed in
- * k order and certified here (certify_score) -- into LDS; then wave 0 applies the
- * reference's rule topk times (largest choice, lowest index among equals, strictly above
- * -inf, none left: idx 0, weight 0; k3_ops.c:459-467). Lane l of wave 0 holds the keys of
- * experts l + 64 i (SW of them) and the largest of its keys; each extraction is one wave
- * maximum over those (wave_max_key_fast), after which the lane that held it drops the key
- * and takes its next largest; lane j keeps the j-th selected key. Uncertified logits that
- * matter (selected, or able to reach the selection) are listed by ballots, recomputed by
- * the workgroup with the reference's chain (chain_block) and the selection is redone
- * until none is left; then renormalise and scale (k3_ops.c:469-475). nrecomp[t]
- * (optional) counts recomputes. KB: chunk partials loaded per batch. */
+ * k order and certified here (certify_score) -- into LDS; then select_rounds (wave 0
+ * selects, the workgroup recomputes what matters) and select_weight; renormalise and
+ * scale (k3_ops.c:459-475). nrecomp[t] (optional) counts recomputes. KB: chunk partials
+ * loaded per batch. */
 template <int SL, int SW, int KB, bool PRE>
 __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int *idx, float *wt, int *nrecomp,
                                                             const double *part,
@@ -770,12 +599,7 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
                                                             int topk, int renorm,
                                                             float routed_scale, ExcTable exc)
 {
-    __shared__ float csh[64 * SW], cmsh[64 * SW], ssh[64 * SW];
-    __shared__ int ush[64 * SW];
-    __shared__ int nlist_sh;
-    __shared__ int list_sh[RF_LIST];
-    __shared__ double res_sh[RF_LIST];
-    __shared__ __attribute__((aligned(16))) double prod_sh[2][RF_BLK];
+    __shared__ SelSmem<SW> sm;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nthr = blockDim.x;
     const int t = blockIdx.x;
@@ -783,17 +607,13 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
     for (int i = 0; i < SL; i++) {
         const int e = tid + nthr * i;
         if (e >= 64 * SW) break;
-        float c = -INFINITY, cmax = -INFINITY, sc = 0.0f;
-        bool unc = false;
-        if (e < n_experts && PRE) {
-            /* scored by router_small_kernel: {score, score of the upper end, uncertified} */
-            const float4 pr = reinterpret_cast<const float4 *>(part)[(size_t)t * n_experts + e];
-            const float bb = bias ? bias[e] : 0.0f;
-            sc = pr.x;
-            c = sc + bb;
-            unc = pr.z != 0.0f;
-            cmax = unc ? pr.y + bb : c;                     /* choice is monotone in logit */
-        } else if (e < n_experts) {
+        if (e >= n_experts) {
+            select_put_record(sm, e, make_float4(0.f, 0.f, 0.f, 0.f), -INFINITY);
+        } else if (PRE) {
+            /* scored by router_small_kernel */
+            select_put_record(sm, e, reinterpret_cast<const float4 *>(part)[(size_t)t * n_experts + e],
+                              bias ? bias[e] : 0.0f);
+        } else {
             double Q = 0.0, bs = 0.0;
             for (int k0 = 0; k0 < ksplit; k0 += KB) {
                 /* one batch of chunk loads in flight together */
@@ -818,105 +638,20 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
                 }
             }
             const Certified cs = certify_score(Q, bs, exc, exc_word((float)Q, exc));
-            const float bb = bias ? bias[e] : 0.0f;
-            sc = cs.sc;
-            c = sc + bb;
-            unc = !cs.ok;
-            cmax = unc ? cs.scmax + bb : c;
+            select_put_record(sm, e, make_float4(cs.sc, cs.scmax, cs.ok ? 0.0f : 1.0f, 0.0f),
+                              bias ? bias[e] : 0.0f);
         }
-        csh[e] = c;
-        cmsh[e] = cmax;
-        ssh[e] = sc;
-        ush[e] = unc ? 1 : 0;
     }
     __syncthreads();
-    int nre = 0;
-    uint64_t mysel = 0ull;                          /* wave 0, lane j: the j-th selected key */
-    for (int round = 0; round <= n_experts; round++) {
-        if (wv == 0) {
-            uint64_t key[SW];
-            uint64_t head = 0ull;
-#pragma unroll
-            for (int i = 0; i < SW; i++) {
-                const int e = lane + 64 * i;
-                const float c = csh[e];
-                key[i] = (e < n_experts && c > -INFINITY)
-                             ? ((uint64_t)choice_order(c) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e)
-                             : 0ull;
-                head = head > key[i] ? head : key[i];
-            }
-            uint32_t taken = 0u;                    /* bit i: key i was selected */
-            int nsel = 0;
-            uint64_t last = 0ull;
-            mysel = 0ull;
-            for (int j = 0; j < topk; j++) {
-                const uint64_t m = wave_max_key_fast(head);
-                if (m == 0ull) break;               /* no finite choice left */
-                nsel++;
-                last = m;
-                if (lane == j) mysel = m;
-                if (head == m) {
-                    uint64_t h2 = 0ull;
-#pragma unroll
-                    for (int i = 0; i < SW; i++) {
-                        if (key[i] == m) {
-                            key[i] = 0ull;
-                            taken |= 1u << i;
-                        }
-                        h2 = h2 > key[i] ? h2 : key[i];
-                    }
-                    head = h2;
-                }
-            }
-            const float ckth = nsel > 0 ? key_choice(last) : -INFINITY;
-            /* uncertified logits that matter, listed in ballot order (up to RF_LIST; the
-             * rest wait for the next round) */
-            int base = 0;
-#pragma unroll
-            for (int i = 0; i < SW; i++) {
-                const int e = lane + 64 * i;
-                const bool need = e < n_experts && ush[e] &&
-                                  (((taken >> i) & 1u) || nsel < topk || cmsh[e] >= ckth);
-                const uint64_t m = __ballot(need);
-                const int slot = base + __popcll(m & ((1ull << lane) - 1ull));
-                if (need && slot < RF_LIST) list_sh[slot] = e;
-                base += __popcll(m);
-            }
-            if (lane == 0) nlist_sh = min(base, RF_LIST);
-        }
-        __syncthreads();
-        const int nl = nlist_sh;
-        if (nl == 0) break;
-        for (int j = 0; j < nl; j++) {
-            const double a = chain_block(prod_sh, W + (size_t)list_sh[j] * hidden, x + (size_t)t * hidden, hidden);
-            if (tid == 0) res_sh[j] = a;
-        }
-        __syncthreads();
-        if (tid < nl) {
-            const int e = list_sh[tid];
-            const float sc = router_score((float)res_sh[tid], exc);
-            const float c = sc + (bias ? bias[e] : 0.0f);
-            csh[e] = c;
-            cmsh[e] = c;
-            ssh[e] = sc;
-            ush[e] = 0;
-        }
-        nre += nl;
-        __syncthreads();
-    }
+    int nre;
+    const uint64_t mysel = select_rounds<SW>(sm, x + (size_t)t * hidden, W, bias, hidden, n_experts, topk, exc, nre);
     if (wv == 0) {
-        const int id = mysel != 0ull ? (int)(0xffffffffu - (uint32_t)mysel) : -1;
-        float w = (lane < topk && id >= 0) ? ssh[id] : 0.0f;
-        if (renorm && topk > 1) {
-            double s = 0.0;
-            for (int j = 0; j < topk; j++)                  /* j ascending */
-                s += (double)__uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(w), j));
-            const float inv = (float)(1.0 / (s + 1e-20));
-            w = w * inv;
-        }
+        int id;
+        float w;
+        select_weight<SW>(sm, mysel, topk, renorm, routed_scale, id, w);
         if (lane < topk) {
             idx[(size_t)t * topk + lane] = id >= 0 ? id : 0;
-            wt[(size_t)t * topk + lane] = w * routed_scale;
+            wt[(size_t)t * topk + lane] = w;
         }
         if (nrecomp && lane == 0) nrecomp[t] = nre;
     }
@@ -1354,6 +1089,11 @@ extern "C" int k3k_router_chunk(int T, int hidden, int n_experts)
 static bool router_small_mode(int T, int hidden)
 {
     return T <= RS_T && (hidden + RS_CH - 1) / RS_CH <= 64;
+}
+
+extern "C" int k3k_router_small(int T, int hidden)
+{
+    return router_small_mode(T, hidden) ? 1 : 0;
 }
 
 static ExcTable exc_view(const K3kExc *exc)

@@ -58,6 +58,16 @@ int k3k_split_bf16(uint16_t *hi, uint16_t *lo, const float *x, size_t n, void *s
  * of activation rows: out[row_of(tok)][r] = sum_k W[r][k] * act[row_of(tok)][k].
  * Jobs come either from the expert gather (mode GATEUP / DOWN) or from a single matrix
  * (mode PLAIN). Activations arrive pre-split as bf16 hi (+ lo when nsplit == 2). */
+/* The libm expf exception table on the device: sorted (key, value) bit pairs and a bucket
+ * index by key >> 12 over [kmin, kmax] (index[b] = first pair whose (key >> 12) - base >= b),
+ * and a membership bitmap so that a miss costs one load. */
+typedef struct {
+    const uint32_t *pairs, *index;
+    const uint32_t *bits;      /* membership bits of |key| - mmin: [2 signs][mwords] words */
+    uint32_t kmin, kmax, base, mmin, mwords;
+    int n;
+} K3kExc;
+
 enum { K3K_MX_PLAIN = 0, K3K_MX_GATEUP = 1, K3K_MX_DOWN = 2 };
 
 typedef struct {
@@ -95,6 +105,19 @@ typedef struct {
     int *drops;
     int n_experts;                      /* idx outside [0, n_experts): absent */
     const float *wt;                    /* k3k_mx_decode_combine: weights [n_assign] */
+    /* k3k_mx_decode GATEUP with sel = 1 (a few tokens, k3k_router_small): the kernel selects
+     * the tokens' experts itself from router_small's scored records pre [T][n_experts]
+     * (router weights rw [n_experts][K], bias rbias or NULL, renorm, rscale, the exception
+     * table exc) and writes idx_out / wt_out [T][topk] and nrecomp [T]; idx is unused. */
+    int sel;
+    const void *pre;
+    const float *rw, *rbias;
+    int renorm;
+    float rscale;
+    K3kExc exc;
+    int *idx_out;
+    float *wt_out;
+    int *nrecomp;
 } K3kMxArgs;
 
 int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
@@ -146,16 +169,6 @@ int k3k_gemv_q8(float *y, const float *x, const void *W, int in, int out, int nt
                 void *stream);
 
 /* ---- router ----------------------------------------------------------------------- */
-/* The libm expf exception table on the device: sorted (key, value) bit pairs and a bucket
- * index by key >> 12 over [kmin, kmax] (index[b] = first pair whose (key >> 12) - base >= b),
- * and a membership bitmap so that a miss costs one load. */
-typedef struct {
-    const uint32_t *pairs, *index;
-    const uint32_t *bits;      /* membership bits of |key| - mmin: [2 signs][mwords] words */
-    uint32_t kmin, kmax, base, mmin, mwords;
-    int n;
-} K3kExc;
-
 /* Router in two launches. k3k_router_partial: per K chunk of `chunk` columns (a multiple
  * of 64, from k3k_router_chunk), the chunk's fp64 chain part[k][t][e] and a bound
  * rbound[k][t][e] on its intermediate magnitudes. k3k_router_final: the certified logit
@@ -164,6 +177,9 @@ typedef struct {
  * first-strict-max top-k, renorm, scale -> idx/wt [T][topk]; nrecomp [T] (may be NULL)
  * receives the number of recomputed logits per token. */
 int k3k_router_chunk(int T, int hidden, int n_experts);
+/* 1 when k3k_router_partial scores and certifies the logits itself (a few tokens): its
+ * part then holds one 16-byte record per logit, which a selecting decode gate/up reads. */
+int k3k_router_small(int T, int hidden);
 int k3k_router_partial(double *part, float *rbound, const float *x, int T, const float *W,
                        int hidden, int n_experts, int chunk, const K3kExc *exc, void *stream);
 int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, const float *rbound,

@@ -408,9 +408,12 @@ class DevBank:
 
 
 def moe_routed_device(bank, x, router_w, bias, topk, renorm=1, routed_scale=1.0,
-                      act=K3_ACT_SILU, b1=4.0, b2=25.0, prec=0, hidden=None, inter=None):
+                      act=K3_ACT_SILU, b1=4.0, b2=25.0, prec=0, hidden=None, inter=None,
+                      want_perm=True):
     """The routed layer through k3d_moe_routed on a DevBank: host arrays in, host arrays
-    out (out [T][hidden], idx, wt [T][topk], perm [T*topk], offsets [n+1], drops)."""
+    out (out [T][hidden], idx, wt [T][topk], perm [T*topk], offsets [n+1], drops). With
+    want_perm False no permutation is asked for (perm and offsets come back None): a few
+    tokens then take the path whose decode gate/up kernel selects the experts itself."""
     L = lib()
     router_w = _f32(router_w)
     n_experts, hid = router_w.shape
@@ -425,8 +428,8 @@ def moe_routed_device(bank, x, router_w, bias, topk, renorm=1, routed_scale=1.0,
         bufs["out"] = DevBuf(T * hidden * 4)
         bufs["idx"] = DevBuf(T * topk * 4)
         bufs["wt"] = DevBuf(T * topk * 4)
-        bufs["perm"] = DevBuf(T * topk * 4)
-        bufs["off"] = DevBuf((n_experts + 1) * 4)
+        bufs["perm"] = DevBuf(T * topk * 4) if want_perm else None
+        bufs["off"] = DevBuf((n_experts + 1) * 4) if want_perm else None
         bufs["drops"] = DevBuf(4)
         wsb = L.k3d_moe_ws(T, hidden, inter, n_experts, topk, prec)
         bufs["ws"] = DevBuf(wsb)
@@ -434,14 +437,15 @@ def moe_routed_device(bank, x, router_w, bias, topk, renorm=1, routed_scale=1.0,
         check(L.k3d_moe_routed(bufs["out"].ptr, bufs["idx"].ptr, bufs["wt"].ptr, bufs["x"].ptr, T,
                                bufs["w"].ptr, b, bank.table.ptr, bank.layout, hidden, inter,
                                n_experts, topk, renorm, routed_scale, act, b1, b2, prec,
-                               bufs["ws"].ptr, wsb, bufs["perm"].ptr, bufs["off"].ptr,
+                               bufs["ws"].ptr, wsb, bufs["perm"].ptr if want_perm else None,
+                               bufs["off"].ptr if want_perm else None,
                                bufs["drops"].ptr, None), "k3d_moe_routed")
         check(L.k3d_sync(None), "sync")
         out = bufs["out"].download(np.empty((T, hidden), np.float32))
         idx = bufs["idx"].download(np.empty((T, topk), np.int32))
         wt = bufs["wt"].download(np.empty((T, topk), np.float32))
-        perm = bufs["perm"].download(np.empty(T * topk, np.int32))
-        off = bufs["off"].download(np.empty(n_experts + 1, np.int32))
+        perm = bufs["perm"].download(np.empty(T * topk, np.int32)) if want_perm else None
+        off = bufs["off"].download(np.empty(n_experts + 1, np.int32)) if want_perm else None
         drops = int(bufs["drops"].download(np.empty(1, np.int32))[0])
         return out, idx, wt, perm, off, drops
     finally:

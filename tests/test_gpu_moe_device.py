@@ -162,8 +162,12 @@ def test_moe_device_decode_path(gpu, orc, k3, T, K, prec, E, I):
         b = gpu.DevBank(holed, E, I, layout)
         try:
             res[layout] = gpu.moe_routed_device(b, X, W, None, K, prec=prec, inter=I)
+            # no permutation asked for: the decode gate/up kernel selects the experts itself
+            fused = gpu.moe_routed_device(b, X, W, None, K, prec=prec, inter=I, want_perm=False)
         finally:
             b.free()
+        for i in (0, 1, 2, 5):                      # out, idx, wt, drops
+            assert np.array_equal(np.asarray(fused[i]), np.asarray(res[layout][i])), (layout, i)
     r, t = res[gpu.K3D_LAYOUT_ROWS], res[gpu.K3D_LAYOUT_TILED]
     for a, b in zip(r, t):
         assert np.array_equal(np.asarray(a), np.asarray(b))
@@ -298,6 +302,45 @@ def test_router_device_uncertified_logits(gpu, orc, hidden, ntok, scale):
     assert list(idx[0][:3]) == [2, 5, 11]
     if scale < 0:
         assert rec[0] >= 2      # both crafted logits went through the reference's chain
+
+
+@pytest.mark.parametrize("ntok", [1, 2])
+def test_moe_selection_in_gateup_uncertified(gpu, orc, k3, ntok):
+    """The routed layer of a few tokens with no permutation asked for: the decode gate/up
+    kernel selects the experts itself from the router's scored records. The crafted rows of
+    test_router_device_uncertified_logits at scale -16 (two logits whose candidate floats'
+    scores differ, so the reference's chain must run inside that kernel): idx and weight
+    bits equal to the oracle's router, the output to the oracle's per-slot sum."""
+    say(f"case: selection inside gate/up, uncertified logits, ntok={ntok}")
+    E, I, N, K = 1024, 512, 16, 4
+    rng = np.random.default_rng(77 + ntok)
+    W = (rng.standard_normal((N, E)) * 1e-3).astype(np.float32)
+    crafted = np.full(E, 2.0 ** -53, np.float32)
+    crafted[:3] = [1.0, 2.0 ** -24, -2.0 ** -52]
+    for e in (5, 11):
+        W[e] = crafted * np.float32(-16.0)
+    W[2] = 0.0
+    W[2, 0] = -16.0
+    bias = np.zeros(N, np.float32)
+    bias[[2, 5, 11]] = 1.0
+    X = np.stack([np.ones(E, np.float32)] +
+                 [rng.standard_normal(E).astype(np.float32) for _ in range(ntok - 1)])
+    bank = [k3.gen_expert(E, I, 91, e) for e in range(N)]
+    b = gpu.DevBank(bank, E, I, gpu.K3D_LAYOUT_TILED)
+    try:
+        out, idx, wt, _, _, drops = gpu.moe_routed_device(b, X, W, bias, K, inter=I, want_perm=False)
+    finally:
+        b.free()
+    assert drops == 0
+    for t in range(ntok):
+        i2, w2 = orc.router(X[t], W, bias, K)
+        assert np.array_equal(idx[t], i2), (t, idx[t], i2)
+        assert np.array_equal(bits(wt[t]), bits(w2)), t
+        acc = np.zeros(E, np.float32)
+        for j in range(K):
+            acc = acc + np.float32(wt[t, j]) * orc.expert_ffn(X[t], bank[int(idx[t, j])], E, I, act=1, wt=1.0)
+        assert max_err_rel_inf(out[t], acc) <= TOL, t
+    assert list(idx[0][:3]) == [2, 5, 11]
 
 
 def _graph_replay(gpu, bank_list, W, bias, E, I, N, K, T, prec, xs):
