@@ -620,32 +620,24 @@ int k3d_mxfp4_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
     return k3k_mx_tile(tpacked, tscales, packed, scales, rows, in, stream) ? fail("mx_tile") : 0;
 }
 
-/* ---- dense (bf16) shared expert on the matrix cores -------------------------------------- */
+/* ---- dense (bf16) shared expert ------------------------------------------------------------
+ * Plain dense GEMMs (rocBLAS, bf16 in, fp32 accumulation): gate and up into the halves of one
+ * [T][2 inter] fp32 buffer, act + bf16 split in one elementwise kernel, then down. Two-term
+ * activations (prec 0) add the lo term's product as a second GEMM with beta 1. The
+ * accumulating form adds the finished output onto y with one fp32 add per element. */
 typedef struct {
     uint16_t *xhi, *xlo, *ahi, *alo;
-    float *tmp;
-    int *job_expert, *job_off, *job_cnt, *pass_job, *pass_tp, *counts, *perm;
-    void *slot;
-    int pass_tok, max_passes;
+    float *gu, *tmp;
 } ShWs;
 
 static size_t shared_layout(Carve *c, ShWs *w, int T, int hidden, int inter, int prec)
 {
-    w->pass_tok = prec == 1 ? 32 : 16;
-    w->max_passes = (T + w->pass_tok - 1) / w->pass_tok;
     w->xhi = (uint16_t *)take(c, (size_t)T * hidden * 2);
     w->xlo = prec == 0 ? (uint16_t *)take(c, (size_t)T * hidden * 2) : NULL;
     w->ahi = (uint16_t *)take(c, (size_t)T * inter * 2);
     w->alo = prec == 0 ? (uint16_t *)take(c, (size_t)T * inter * 2) : NULL;
+    w->gu = (float *)take(c, (size_t)T * 2 * inter * 4);
     w->tmp = (float *)take(c, (size_t)T * hidden * 4);
-    w->job_expert = (int *)take(c, 4);
-    w->job_off = (int *)take(c, 4);
-    w->job_cnt = (int *)take(c, 4);
-    w->pass_job = (int *)take(c, (size_t)w->max_passes * 4);
-    w->pass_tp = (int *)take(c, (size_t)w->max_passes * 4);
-    w->counts = (int *)take(c, 16);
-    w->perm = (int *)take(c, (size_t)T * 4);
-    w->slot = take(c, 64);
     return c->off;
 }
 
@@ -667,43 +659,20 @@ int k3d_shared_expert(float *y, int accumulate, const float *x, int T, const uin
     Carve c = {(char *)ws, 0};
     ShWs w;
     shared_layout(&c, &w, T, hidden, inter, prec);
+    const int ld = 2 * inter;
     if (k3k_split_bf16(w.xhi, w.xlo, x, (size_t)T * hidden, stream)) return fail("split");
-    if (k3k_dense_jobs(w.slot, w1, w3, w2, w.job_expert, w.job_off, w.job_cnt, w.pass_job,
-                       w.pass_tp, w.counts, w.perm, T, w.pass_tok, stream))
-        return fail("dense_jobs");
-    K3kMxArgs a;
-    memset(&a, 0, sizeof a);
-    a.bank = w.slot;
-    a.pass_tok = w.pass_tok;
-    a.layout = 2;
-    a.job_expert = w.job_expert;
-    a.job_off = w.job_off;
-    a.job_cnt = w.job_cnt;
-    a.pass_job = w.pass_job;
-    a.pass_tp = w.pass_tp;
-    a.n_passes = w.counts + 1;
-    a.perm = w.perm;
-    a.topk = 1;
-    a.act = act;
-    a.b1 = b1;
-    a.b2 = b2;
-    a.nsplit = prec == 0 ? 2 : 1;
-    a.max_passes = w.max_passes;
-    a.xhi = w.xhi;
-    a.xlo = w.xlo;
-    a.ahi = w.ahi;
-    a.alo = w.alo;
-    a.rows = inter;
-    a.K = hidden;
-    a.n_xrows = T;
-    if (k3k_mx_gemm(K3K_MX_GATEUP, &a, stream)) return fail("shared gate/up");
-    a.xhi = w.ahi;
-    a.xlo = w.alo;
-    a.out = accumulate ? w.tmp : y;
-    a.rows = hidden;
-    a.K = inter;
-    a.n_xrows = T;
-    if (k3k_mx_gemm(K3K_MX_DOWN, &a, stream)) return fail("shared down");
+    if (k3k_gemm_bf16_nt(w.gu, ld, w1, w.xhi, inter, T, hidden, 0.0f, stream) ||
+        k3k_gemm_bf16_nt(w.gu + inter, ld, w3, w.xhi, inter, T, hidden, 0.0f, stream))
+        return fail("shared gate/up");
+    if (prec == 0 && (k3k_gemm_bf16_nt(w.gu, ld, w1, w.xlo, inter, T, hidden, 1.0f, stream) ||
+                      k3k_gemm_bf16_nt(w.gu + inter, ld, w3, w.xlo, inter, T, hidden, 1.0f, stream)))
+        return fail("shared gate/up (lo)");
+    if (k3k_act_split(w.ahi, w.alo, w.gu, inter, T, act, b1, b2, stream)) return fail("shared act");
+    float *dst = accumulate ? w.tmp : y;
+    if (k3k_gemm_bf16_nt(dst, hidden, w2, w.ahi, hidden, T, inter, 0.0f, stream))
+        return fail("shared down");
+    if (prec == 0 && k3k_gemm_bf16_nt(dst, hidden, w2, w.alo, hidden, T, inter, 1.0f, stream))
+        return fail("shared down (lo)");
     if (accumulate && k3k_axpy_rows(y, w.tmp, (size_t)T * hidden, stream)) return fail("shared add");
     k3k_prof_mark(stream, K3D_STAGE_SHARED);
     return 0;

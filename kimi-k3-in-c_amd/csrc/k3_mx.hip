@@ -885,8 +885,7 @@ void mx_moe_kernel(K3kMxArgs a)
     constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
     constexpr int KC = 512, SPC = 4, LDT = KC + 8;           /* LDS row: 16-byte pad */
     /* tiled MXFP4 weights are streamed once per pass and non-temporal; row-major ones keep
-     * the default policy (a 128-byte line is consumed by two steps' loads), as do bf16
-     * (dense) weights, which every pass of the batch re-reads */
+     * the default policy (a 128-byte line is consumed by two steps' loads) */
     constexpr int WPOL = LAYOUT == 1 ? K3_LD_NT : K3_LD_DEFAULT;
     constexpr int NRH = PT * NS;                             /* staged row-halves per chunk */
     constexpr int PPW = (NRH + NW - 1) / NW;                 /* row-halves per wave */
@@ -919,16 +918,15 @@ void mx_moe_kernel(K3kMxArgs a)
         const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[e];
         /* one buffer descriptor per matrix (wave-uniform); per-lane byte offsets */
         const uint32_t prow = LAYOUT == 1 ? (uint32_t)((rows + 15) & ~15) : (uint32_t)rows;
-        /* LAYOUT 2: bf16 weights [rows][K], 2 bytes per element, no scales */
-        const uint32_t pbytes = LAYOUT == 2 ? prow * (uint32_t)K * 2u : prow * rstride;
-        const uint32_t sbytes = LAYOUT == 2 ? 16u : prow * nblk;
+        const uint32_t pbytes = prow * rstride;
+        const uint32_t sbytes = prow * nblk;
         k3_rsrc rp0, rp1, rs0, rs1;
         if (MODE == K3K_MX_GATEUP) {
-            rp0 = k3_make_rsrc(q.p1, pbytes); rs0 = k3_make_rsrc(LAYOUT == 2 ? q.p1 : q.s1, sbytes);
-            rp1 = k3_make_rsrc(q.p3, pbytes); rs1 = k3_make_rsrc(LAYOUT == 2 ? q.p3 : q.s3, sbytes);
+            rp0 = k3_make_rsrc(q.p1, pbytes); rs0 = k3_make_rsrc(q.s1, sbytes);
+            rp1 = k3_make_rsrc(q.p3, pbytes); rs1 = k3_make_rsrc(q.s3, sbytes);
         } else {
             rp0 = rp1 = k3_make_rsrc(q.p2, pbytes);
-            rs0 = rs1 = k3_make_rsrc(LAYOUT == 2 ? q.p2 : q.s2, sbytes);
+            rs0 = rs1 = k3_make_rsrc(q.s2, sbytes);
         }
         uint32_t poff[MT], soff[MT];
         const int ntile = (rows + 15) >> 4;
@@ -939,10 +937,6 @@ void mx_moe_kernel(K3kMxArgs a)
                 const int r = min(rb * rpg + wv * rpw + 16 * mt + r16, rows - 1);
                 poff[m] = (uint32_t)r * rstride + (uint32_t)g * 16u;
                 soff[m] = (uint32_t)r * (uint32_t)nblk;
-            } else if (LAYOUT == 2) {
-                const int r = min(rb * rpg + wv * rpw + 16 * mt + r16, rows - 1);
-                poff[m] = ((uint32_t)r * (uint32_t)K + (uint32_t)g * 32u) * 2u;
-                soff[m] = 0;
             } else {
                 const int t = min((rb * rpg + wv * rpw) / 16 + mt, ntile - 1);
                 poff[m] = (uint32_t)t * (uint32_t)nchunk * 4096u + (uint32_t)lane * 16u;
@@ -986,8 +980,7 @@ void mx_moe_kernel(K3kMxArgs a)
          * chunk c+2 is loaded into chunk c's slot. Scales follow one chunk behind. */
         constexpr int NSLOT = DEPTH == 2 ? 2 : 1;
         constexpr int SQN = MT * (LAYOUT == 0 ? 4 : 1);
-        constexpr int WQ = LAYOUT == 2 ? 4 : 1;             /* 16-byte loads per block */
-        uint4 qa[NSLOT][SPC][MT][WQ];
+        uint4 qa[NSLOT][SPC][MT];
         uint32_t sq[SQN], sqn[SQN], sqnn[SQN];
         uint4 bst[PPW];
 
@@ -1009,18 +1002,13 @@ void mx_moe_kernel(K3kMxArgs a)
         };
         auto load_step = [&](int c, int d, auto slot) {
             constexpr int S = decltype(slot)::value;
-            const uint32_t bo = LAYOUT == 0   ? (uint32_t)c * 256u + (uint32_t)d * 64u
-                                : LAYOUT == 2 ? (uint32_t)c * 1024u + (uint32_t)d * 256u
-                                              : ((uint32_t)c * 4u + (uint32_t)d) * 1024u;
+            const uint32_t bo = LAYOUT == 0 ? (uint32_t)c * 256u + (uint32_t)d * 64u
+                                            : ((uint32_t)c * 4u + (uint32_t)d) * 1024u;
 #pragma unroll
             for (int m = 0; m < MT; m++)
-#pragma unroll
-                for (int w = 0; w < WQ; w++)
-                    qa[S][d][m][w] = k3_bload16<WPOL>(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1,
-                                                poff[m] + bo + 16u * w);
+                qa[S][d][m] = k3_bload16<WPOL>(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo);
         };
         auto load_scales = [&](int c, uint32_t *ss) {
-            if (LAYOUT == 2) return;
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 const k3_rsrc rs = m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1;
@@ -1069,31 +1057,24 @@ void mx_moe_kernel(K3kMxArgs a)
                 }
                 uint4 qq[MT];
                 float so[MT];
-                if (LAYOUT != 2) {
 #pragma unroll
-                    for (int m = 0; m < MT; m++) {
-                        const uint32_t sraw = LAYOUT == 0 ? (sq[4 * m + d] >> (8 * g)) & 0xFFu
-                                                          : (sq[m] >> (8 * d)) & 0xFFu;
-                        const bool nanb = sraw == 255u;          /* NaN byte: the block is 0 */
-                        qq[m] = qa[S][d][m][0];
-                        qq[m].x = nanb ? 0u : qq[m].x;
-                        qq[m].y = nanb ? 0u : qq[m].y;
-                        qq[m].z = nanb ? 0u : qq[m].z;
-                        qq[m].w = nanb ? 0u : qq[m].w;
-                        so[m] = k3_e8m0_operand(nanb ? 127u : sraw);
-                    }
+                for (int m = 0; m < MT; m++) {
+                    const uint32_t sraw = LAYOUT == 0 ? (sq[4 * m + d] >> (8 * g)) & 0xFFu
+                                                      : (sq[m] >> (8 * d)) & 0xFFu;
+                    const bool nanb = sraw == 255u;              /* NaN byte: the block is 0 */
+                    qq[m] = qa[S][d][m];
+                    qq[m].x = nanb ? 0u : qq[m].x;
+                    qq[m].y = nanb ? 0u : qq[m].y;
+                    qq[m].z = nanb ? 0u : qq[m].z;
+                    qq[m].w = nanb ? 0u : qq[m].w;
+                    so[m] = k3_e8m0_operand(nanb ? 127u : sraw);
                 }
 #pragma unroll
                 for (int m = 0; m < MT; m++)
 #pragma unroll
                     for (int pp = 0; pp < 4; pp++) {
-                        k3_bf16x8 av;
-                        if (LAYOUT == 2) {
-                            av = k3_as_bf16x8(qa[S][d][m][WQ == 4 ? pp : 0]);
-                        } else {
-                            const uint32_t codes = pp == 0 ? qq[m].x : pp == 1 ? qq[m].y : pp == 2 ? qq[m].z : qq[m].w;
-                            av = k3_dequant8_bf16(codes, so[m]);
-                        }
+                        const uint32_t codes = pp == 0 ? qq[m].x : pp == 1 ? qq[m].y : pp == 2 ? qq[m].z : qq[m].w;
+                        const k3_bf16x8 av = k3_dequant8_bf16(codes, so[m]);
 #pragma unroll
                         for (int nb = 0; nb < NB; nb++) {
                             acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bh[nb][pp]), acc[m][nb], 0, 0, 0);
@@ -1170,8 +1151,7 @@ int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
 
 /* ---- prefill: large token passes, one-term activations --------------------------------
  * mx_prefill_kernel: GATEUP / DOWN for passes of up to 16*NB tokens with the activations
- * as single bf16 terms (the prefill precision), weights tiled MXFP4 (LAYOUT 1) or bf16
- * (LAYOUT 2). Same item = (pass, row block) and K order as mx_moe_kernel, but K is staged
+ * as single bf16 terms (the prefill precision), weights tiled MXFP4. Same item = (pass, row block) and K order as mx_moe_kernel, but K is staged
  * 128 * SPC columns at a time so that the pass's tokens fit in LDS: each expert's weights
  * are streamed once per pass of up to 16*NB tokens, and every dequantized weight fragment
  * feeds MT x NB MFMAs. Stage c covers steps c SPC .. c SPC + SPC - 1 (128 columns each).
@@ -1187,7 +1167,6 @@ void mx_prefill_kernel(K3kMxArgs a)
     constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
     constexpr int NPC = PT * PR;                              /* 16-byte pieces per stage */
     constexpr int PPT = (NPC + NTH - 1) / NTH;
-    constexpr int WQ = LAYOUT == 2 ? 4 : 1;
     __shared__ __attribute__((aligned(16))) uint16_t bsh[2][PT + 1][LDT];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1223,30 +1202,24 @@ void mx_prefill_kernel(K3kMxArgs a)
         const int nbu = (ntok + 15) >> 4;             /* token blocks holding tokens */
         const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[e];
         const uint32_t prow = LAYOUT == 1 ? (uint32_t)((rows + 15) & ~15) : (uint32_t)rows;
-        const uint32_t pbytes = LAYOUT == 2 ? prow * (uint32_t)K * 2u : prow * rstride;
-        const uint32_t sbytes = LAYOUT == 2 ? 16u : prow * nblk;
+        const uint32_t pbytes = prow * rstride;
+        const uint32_t sbytes = prow * nblk;
         k3_rsrc rp0, rp1, rs0, rs1;
         if (MODE == K3K_MX_GATEUP) {
-            rp0 = k3_make_rsrc(q.p1, pbytes); rs0 = k3_make_rsrc(LAYOUT == 2 ? q.p1 : q.s1, sbytes);
-            rp1 = k3_make_rsrc(q.p3, pbytes); rs1 = k3_make_rsrc(LAYOUT == 2 ? q.p3 : q.s3, sbytes);
+            rp0 = k3_make_rsrc(q.p1, pbytes); rs0 = k3_make_rsrc(q.s1, sbytes);
+            rp1 = k3_make_rsrc(q.p3, pbytes); rs1 = k3_make_rsrc(q.s3, sbytes);
         } else {
             rp0 = rp1 = k3_make_rsrc(q.p2, pbytes);
-            rs0 = rs1 = k3_make_rsrc(LAYOUT == 2 ? q.p2 : q.s2, sbytes);
+            rs0 = rs1 = k3_make_rsrc(q.s2, sbytes);
         }
         uint32_t poff[MT], soff[MT];
         const int ntile = (rows + 15) >> 4;
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             const int mt = (MODE == K3K_MX_GATEUP) ? (m % RT) : m;
-            if (LAYOUT == 2) {
-                const int r = min(rb * rpg + wv * rpw + 16 * mt + r16, rows - 1);
-                poff[m] = ((uint32_t)r * (uint32_t)K + (uint32_t)g * 32u) * 2u;
-                soff[m] = 0;
-            } else {
-                const int t = min((rb * rpg + wv * rpw) / 16 + mt, ntile - 1);
-                poff[m] = (uint32_t)t * (uint32_t)nchunk * 4096u + (uint32_t)lane * 16u;
-                soff[m] = (uint32_t)t * (uint32_t)nchunk * 256u + (uint32_t)lane * 4u;
-            }
+            const int t = min((rb * rpg + wv * rpw) / 16 + mt, ntile - 1);
+            poff[m] = (uint32_t)t * (uint32_t)nchunk * 4096u + (uint32_t)lane * 16u;
+            soff[m] = (uint32_t)t * (uint32_t)nchunk * 256u + (uint32_t)lane * 4u;
         }
         /* staging pieces: token row p = pc / PR, 16-byte column piece o = pc % PR */
         const uint32_t xbytes = (uint32_t)a.n_xrows * (uint32_t)K * 2u;
@@ -1273,7 +1246,7 @@ void mx_prefill_kernel(K3kMxArgs a)
             for (int nb = 0; nb < NB; nb++) acc[m][nb] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
 
         /* weights two stages ahead: stages alternate between the two register slots */
-        uint4 qa[2][SPC][MT][WQ];
+        uint4 qa[2][SPC][MT];
         uint32_t sq[MT], sqn[MT], sqnn[MT];
         uint4 bst[PPT];
         auto load_b = [&](int c) {
@@ -1287,17 +1260,13 @@ void mx_prefill_kernel(K3kMxArgs a)
         };
         auto load_step = [&](int c, int d, auto slot) {
             constexpr int S = decltype(slot)::value;
-            /* step s = c SPC + d: 128 columns, 1 KB per tile (tiled MXFP4), 256 B per row (bf16) */
-            const uint32_t st = (uint32_t)(c * SPC + d);
-            const uint32_t bo = LAYOUT == 2 ? st * 256u : st * 1024u;
+            /* step s = c SPC + d: 128 columns, 1 KB per tile */
+            const uint32_t bo = (uint32_t)(c * SPC + d) * 1024u;
 #pragma unroll
             for (int m = 0; m < MT; m++)
-#pragma unroll
-                for (int w = 0; w < WQ; w++)
-                    qa[S][d][m][w] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo + 16u * w);
+                qa[S][d][m] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo);
         };
         auto load_scales = [&](int c, uint32_t *ss) {
-            if (LAYOUT == 2) return;
 #pragma unroll
             for (int m = 0; m < MT; m++)
                 ss[m] = k3_bload4(m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1, soff[m] + (uint32_t)((c * SPC) >> 2) * 256u);
@@ -1341,13 +1310,9 @@ void mx_prefill_kernel(K3kMxArgs a)
                     k3_bf16x8 av[MT];
 #pragma unroll
                     for (int m = 0; m < MT; m++) {
-                        if (LAYOUT == 2) {
-                            av[m] = k3_as_bf16x8(qa[S][d][m][WQ == 4 ? pp : 0]);
-                        } else {
-                            const uint4 qv = qa[S][d][m][0];
-                            const uint32_t codes = pp == 0 ? qv.x : pp == 1 ? qv.y : pp == 2 ? qv.z : qv.w;
-                            av[m] = k3_dequant8_bf16(nanb[m] ? 0u : codes, so[m]);
-                        }
+                        const uint4 qv = qa[S][d][m];
+                        const uint32_t codes = pp == 0 ? qv.x : pp == 1 ? qv.y : pp == 2 ? qv.z : qv.w;
+                        av[m] = k3_dequant8_bf16(nanb[m] ? 0u : codes, so[m]);
                     }
 #pragma unroll
                     for (int nb = 0; nb < NB; nb++) {
@@ -1479,48 +1444,7 @@ __global__ void mx_tile_kernel(uint8_t *tpacked, uint8_t *tscales, const uint8_t
     }
 }
 
-/* One job over all T tokens (the shared expert): identity permutation, passes of
- * pass_tok tokens, and the job's bank entry from three weight pointers. */
-__global__ void dense_jobs_kernel(ExpertQDev *slot, const uint8_t *w1, const uint8_t *w3,
-                                  const uint8_t *w2, int *job_expert, int *job_off, int *job_cnt,
-                                  int *pass_job, int *pass_tp, int *counts, int *perm, int T,
-                                  int pass_tok)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    const int np = (T + pass_tok - 1) / pass_tok;
-    if (i < T) perm[i] = i;
-    if (i < np) {
-        pass_job[i] = 0;
-        pass_tp[i] = i;
-    }
-    if (i == 0) {
-        slot->p1 = w1; slot->s1 = w1;
-        slot->p3 = w3; slot->s3 = w3;
-        slot->p2 = w2; slot->s2 = w2;
-        job_expert[0] = 0;
-        job_off[0] = 0;
-        job_cnt[0] = T;
-        counts[0] = 1;
-        counts[1] = np;
-        counts[2] = 0;
-    }
-}
-
 }  // namespace
-
-extern "C" int k3k_dense_jobs(void *slot, const void *w1, const void *w3, const void *w2,
-                              int *job_expert, int *job_off, int *job_cnt, int *pass_job,
-                              int *pass_tp, int *counts, int *perm, int T, int pass_tok,
-                              void *stream)
-{
-    if (T <= 0) return 0;
-    hipLaunchKernelGGL(dense_jobs_kernel, dim3((T + 255) / 256), dim3(256), 0, (hipStream_t)stream,
-                       (ExpertQDev *)slot, (const uint8_t *)w1, (const uint8_t *)w3,
-                       (const uint8_t *)w2, job_expert, job_off, job_cnt, pass_job, pass_tp,
-                       counts, perm, T, pass_tok);
-    K3K_LAUNCH_CHECK("dense_jobs launch");
-    return 0;
-}
 
 extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
 {
@@ -1578,25 +1502,6 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
                       : launch_prefill<K3K_MX_DOWN, 4, 6, 1, 1, 8>(a, grid, st);
         return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 1, 2, 8>(a, grid, st)
                   : launch_prefill<K3K_MX_DOWN, 4, 3, 1, 2, 8>(a, grid, st);
-    }
-    if (a->layout == 2) {
-        /* bf16 weights (the dense shared expert): 2 tiles of 16 rows per wave, 32-token
-         * passes with one-term activations or 16-token passes with one or two terms */
-        if (a->K % 512) return k3k_fail("mx_moe bf16: K % 512 != 0", hipErrorInvalidValue);
-        const bool gu = mode == K3K_MX_GATEUP;
-        const int rpg = gu ? 64 : 128;
-        const long items = (long)a->max_passes * ((a->rows + rpg - 1) / rpg);
-        const int grid = (int)(items < (long)cus * 4 ? (items > 0 ? items : 1) : (long)cus * 4);
-        if (a->pass_tok == 32 && a->nsplit == 1)
-            return gu ? launch_moe<K3K_MX_GATEUP, 2, 1, 32, 4, 2, 2, 1, 2>(a, grid, st)
-                      : launch_moe<K3K_MX_DOWN, 2, 1, 32, 4, 2, 2, 1, 2>(a, grid, st);
-        if (a->pass_tok == 16)
-            return a->nsplit == 2
-                       ? (gu ? launch_moe<K3K_MX_GATEUP, 2, 2, 16, 4, 2, 2, 1, 1>(a, grid, st)
-                             : launch_moe<K3K_MX_DOWN, 2, 2, 16, 4, 2, 2, 1, 1>(a, grid, st))
-                       : (gu ? launch_moe<K3K_MX_GATEUP, 2, 1, 16, 4, 2, 2, 1, 1>(a, grid, st)
-                             : launch_moe<K3K_MX_DOWN, 2, 1, 16, 4, 2, 2, 1, 1>(a, grid, st));
-        return k3k_fail("mx_moe bf16: pass size", hipErrorInvalidValue);
     }
     if (a->pass_tok == 32) {
         /* prefill: 32-token passes, two MFMA column blocks per weight fragment, activations

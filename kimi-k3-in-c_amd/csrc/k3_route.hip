@@ -993,6 +993,21 @@ __global__ __launch_bounds__(256) void combine_kernel(float *out, const float *c
 }
 
 /* ---- elementwise --------------------------------------------------------------------- */
+__global__ void act_split_kernel(uint16_t *hi, uint16_t *lo, const float *gu, int n, int rows, int act,
+                                 float b1, float b2)
+{
+    const size_t total = (size_t)n * rows;
+    for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < total;
+         k += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = k / n, i = k % n;
+        const float *x = gu + r * 2 * (size_t)n;
+        uint16_t h, l;
+        k3_split2(k3_act_pair(x[i], x[n + i], act, b1, b2), h, l);
+        hi[k] = h;
+        if (lo) lo[k] = l;
+    }
+}
+
 __global__ void act_kernel(float *y, const float *gu, int n, int rows, int act, float b1, float b2)
 {
     const size_t total = (size_t)n * rows;
@@ -1243,6 +1258,17 @@ extern "C" int k3k_combine(float *out, const float *contrib, const float *wt, co
         hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, out, contrib,
                            wt, idx, bank, n_experts, T, topk, E);
     K3K_LAUNCH_CHECK("combine launch");
+    return 0;
+}
+
+extern "C" int k3k_act_split(uint16_t *hi, uint16_t *lo, const float *gu, int n, int rows, int act,
+                             float b1, float b2, void *stream)
+{
+    const size_t total = (size_t)n * rows;
+    if (!total) return 0;
+    hipLaunchKernelGGL(act_split_kernel, dim3(grid1d(total, 256)), dim3(256), 0, (hipStream_t)stream, hi, lo,
+                       gu, n, rows, act, b1, b2);
+    K3K_LAUNCH_CHECK("act_split launch");
     return 0;
 }
 

@@ -83,8 +83,7 @@ typedef struct {
      * kernel). */
     const void *bank;                   /* device K3ExpertQ[n_experts] */
     int pass_tok;
-    int layout;                         /* 0: row-major MXFP4, 1: tiled MXFP4 (k3k_mx_tile),
-                                           2: bf16 weights [rows][K] (p1/p3/p2 only) */
+    int layout;                         /* 0: row-major MXFP4, 1: tiled MXFP4 (k3k_mx_tile) */
     const int *job_expert, *job_off, *job_cnt;
     const int *pass_job, *pass_tp, *n_passes;
     const int *perm;                    /* sorted position -> assignment a = t*topk + j */
@@ -140,12 +139,6 @@ static inline int k3k_mx_small_ok(int ntok, int K, int nsplit, int rows, const v
     return ntok >= 1 && ntok <= 2 && K % 32 == 0 && (long)nsplit * ntok * K * 2 <= 65536 &&
            nsteps <= 128 && ((uintptr_t)x % 16) == 0 && (unsigned long long)rows * (K / 2) < 0x80000000ull;
 }
-
-/* The job arrays of one dense expert over T tokens (the shared expert): slot receives the
- * bank entry {w1, w3, w2}, perm is the identity, passes of pass_tok tokens. */
-int k3k_dense_jobs(void *slot, const void *w1, const void *w3, const void *w2, int *job_expert,
-                   int *job_off, int *job_cnt, int *pass_job, int *pass_tp, int *counts,
-                   int *perm, int T, int pass_tok, void *stream);
 
 /* Row-major MXFP4 matrix [rows][K] (K % 512 == 0) -> the tiled layout of the expert kernel:
  * tpacked [ceil(rows/16)*16][K/2] bytes, tscales [ceil(rows/16)*16][K/32] bytes. */
@@ -212,6 +205,16 @@ int k3k_combine(float *out, const float *contrib, const float *wt, const int *id
 /* ---- elementwise -------------------------------------------------------------------- */
 int k3k_act(float *y, const float *gu, int n, int rows, int act, float b1, float b2,
             void *stream);
+/* act over gu [rows][2n] (gate | up) straight into its bf16 split: hi [rows][n], and lo when
+ * not NULL (k3k_split_bf16's rounding of the fp32 value k3k_act would write). */
+int k3k_act_split(uint16_t *hi, uint16_t *lo, const float *gu, int n, int rows, int act,
+                  float b1, float b2, void *stream);
+
+/* ---- plain dense GEMM (rocBLAS) ---------------------------------------------------- */
+/* y[t][r] = beta * y[t][r] + sum_k W[r][k] * x[t][k], t < T, r < R (row stride ldy): W bf16
+ * [R][K], x bf16 [T][K], fp32 accumulation and output. The dense shared expert's products. */
+int k3k_gemm_bf16_nt(float *y, int ldy, const uint16_t *W, const uint16_t *x, int R, int T,
+                     int K, float beta, void *stream);
 int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int rows, float eps,
                 void *stream);
 int k3k_axpy_rows(float *out, const float *add, size_t n, void *stream); /* out += add */
