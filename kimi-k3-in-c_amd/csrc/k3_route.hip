@@ -668,35 +668,48 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
 constexpr int G_MAXE = 4096, G_WCNT_E = 1024;
 
 /* inclusive scan over a wave, then over the workgroup's 16 wave totals */
-__device__ __forceinline__ int block_scan_excl(int v, int *wtot, int lane, int wv, int &total)
+/* Exclusive scans of NV values at once over a 1024-thread workgroup (one pair of barriers
+ * for all of them): x[i] becomes the sum of v[i] over the lower threads, tot[i] the total. */
+template <int NV>
+__device__ __forceinline__ void block_scan_excl_n(int (&x)[NV], int (*wtotn)[NV], int lane, int wv,
+                                                  int (&tot)[NV])
 {
-    int x = v;
+    int v[NV];
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    if (lane == 63) wtot[wv] = x;
+    for (int i = 0; i < NV; i++) v[i] = x[i];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1)
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int y = __shfl_up(x[i], o, 64);
+            if (lane >= o) x[i] += y;
+        }
+    if (lane == 63)
+#pragma unroll
+        for (int i = 0; i < NV; i++) wtotn[wv][i] = x[i];
     __syncthreads();
-    int base = 0;
-    total = 0;
-    for (int w = 0; w < 16; w++) {
-        const int tw = wtot[w];
-        if (w < wv) base += tw;
-        total += tw;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        int base = 0;
+        tot[i] = 0;
+        for (int w = 0; w < 16; w++) {
+            const int tw = wtotn[w][i];
+            if (w < wv) base += tw;
+            tot[i] += tw;
+        }
+        x[i] = base + x[i] - v[i];
     }
     __syncthreads();
-    return base + x - v;
 }
 
 /* From per-expert counts cnt[] (LDS): offsets[], fill[] (= offsets, in LDS), the jobs,
  * the passes and counts[0..3], as the gather's header describes. With pass_tok2 > 0 the
  * experts holding more than pass_tok assignments get passes of pass_tok2 in the second
  * list instead. Called by all 1024 threads; ends with a barrier. */
-__device__ void gather_plan(const int *cnt, int *fill, int *wtot, int *offsets, int *job_expert,
+__device__ void gather_plan(const int *cnt, int *fill, int (*wtot5)[5], int *offsets, int *job_expert,
                             int *job_off, int *job_cnt, int *pass_job, int *pass_tp,
                             int *pass_job2, int *pass_tp2, int *counts, int n_experts,
-                            const void *bank, int pass_tok, int pass_tok2)
+                            const unsigned char *pres, int pass_tok, int pass_tok2)
 {
     auto big = [&](int c) { return pass_tok2 > 0 && c > pass_tok; };
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -707,7 +720,7 @@ __device__ void gather_plan(const int *cnt, int *fill, int *wtot, int *offsets, 
     for (int e = ea; e < eb; e++) {
         local += cnt[e];
         if (cnt[e] > 0) {
-            if (expert_present(bank, e)) {
+            if (pres[e]) {
                 ljobs++;
                 if (big(cnt[e])) lpass2 += (cnt[e] + pass_tok2 - 1) / pass_tok2;
                 else lpass += (cnt[e] + pass_tok - 1) / pass_tok;
@@ -716,16 +729,14 @@ __device__ void gather_plan(const int *cnt, int *fill, int *wtot, int *offsets, 
             }
         }
     }
-    int tot_a, tot_b, tot_c, tot_d, tot_e;
-    int run = block_scan_excl(local, wtot, lane, wv, tot_a);
-    int jrun = block_scan_excl(ljobs, wtot, lane, wv, tot_b);
-    int prun = block_scan_excl(lpass, wtot, lane, wv, tot_c);
-    int prun2 = block_scan_excl(lpass2, wtot, lane, wv, tot_e);
-    (void)block_scan_excl(ldrop, wtot, lane, wv, tot_d);
+    int sv[5] = {local, ljobs, lpass, lpass2, ldrop}, tot[5];
+    block_scan_excl_n<5>(sv, wtot5, lane, wv, tot);
+    int run = sv[0], jrun = sv[1], prun = sv[2], prun2 = sv[3];
+    const int tot_a = tot[0], tot_b = tot[1], tot_c = tot[2], tot_e = tot[3], tot_d = tot[4];
     for (int e = ea; e < eb; e++) {
         offsets[e] = run;
         fill[e] = run;
-        if (cnt[e] > 0 && expert_present(bank, e)) {
+        if (cnt[e] > 0 && pres[e]) {
             job_expert[jrun] = e;
             job_off[jrun] = run;
             job_cnt[jrun] = cnt[e];
@@ -767,18 +778,23 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
 {
     __shared__ int cnt[G_MAXE];
     __shared__ int fill[G_MAXE];
-    __shared__ int wtot[16];
+    __shared__ int wtot5[16][5];
+    __shared__ unsigned char pres[G_MAXE];
     __shared__ unsigned short wcnt[16][G_WCNT_E];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    for (int e = tid; e < n_experts; e += 1024) cnt[e] = 0;
+    /* the bank entries' presence, loaded beside the counting */
+    for (int e = tid; e < n_experts; e += 1024) {
+        cnt[e] = 0;
+        pres[e] = expert_present(bank, e) ? 1 : 0;
+    }
     __syncthreads();
     for (int a = tid; a < N; a += 1024) {
         const int e = idx[a];
         if (e >= 0 && e < n_experts) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    gather_plan(cnt, fill, wtot, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp,
-                pass_job2, pass_tp2, counts, n_experts, bank, pass_tok, pass_tok2);
+    gather_plan(cnt, fill, wtot5, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp,
+                pass_job2, pass_tp2, counts, n_experts, pres, pass_tok, pass_tok2);
 
     /* stable placement */
     const bool wide = n_experts > G_WCNT_E;
@@ -864,19 +880,22 @@ __global__ __launch_bounds__(1024) void gather_scan_kernel(int *hist, int *offse
 {
     __shared__ int cnt[G_WCNT_E];
     __shared__ int fill[G_WCNT_E];
-    __shared__ int wtot[16];
+    __shared__ int wtot5[16][5];
+    __shared__ unsigned char pres[G_WCNT_E];
     const int tid = threadIdx.x;
     /* a thread per expert; its chunk counts are a strided column (coalesced across the
      * threads), read 16 at a time so that the loads overlap */
     for (int e = tid; e < n_experts; e += 1024) {
+        const bool pr = expert_present(bank, e);
         int t = 0;
 #pragma unroll 16
         for (int c = 0; c < nchunk; c++) t += hist[(size_t)c * n_experts + e];
         cnt[e] = t;
+        pres[e] = pr ? 1 : 0;
     }
     __syncthreads();
-    gather_plan(cnt, fill, wtot, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp,
-                pass_job2, pass_tp2, counts, n_experts, bank, pass_tok, pass_tok2);
+    gather_plan(cnt, fill, wtot5, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp,
+                pass_job2, pass_tp2, counts, n_experts, pres, pass_tok, pass_tok2);
     for (int e = tid; e < n_experts; e += 1024) {
         int run = fill[e];
 #pragma unroll 16
