@@ -1209,16 +1209,18 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
     hipStream_t st = (hipStream_t)stream;
     const bool pre = router_small_mode(T, hidden);
     /* scored records (a few tokens): one wave loads them all; else the chunk partials, a lane
-     * per expert, up to 64 of a lane's partials per load batch for up to 64 tokens and 512
-     * experts (more registers, fewer waves per CU: only while the tokens do not fill the
-     * chip). Wave 0 selects over SW keys per lane: 8 up to 512 experts, else 32. */
+     * per expert, all of a lane's partials in one load batch when they are at most 16 or 32,
+     * or 64 for up to 64 tokens and 512 experts (more registers, fewer waves per CU: only
+     * while the tokens do not fill the chip). Wave 0 selects over SW keys per lane: 8 up to
+     * 512 experts, else 32. */
 #define K3_RF(SL, SW, KB, PRE, NT)                                                                  \
     hipLaunchKernelGGL((router_final_kernel<SL, SW, KB, PRE>), dim3(T), dim3(NT), 0, st, idx, wt, nrecomp, \
                        part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm,        \
                        routed_scale, e)
     if (pre && n_experts <= 512) K3_RF(8, 8, RF_KB, true, 64);
     else if (pre) K3_RF(32, 32, RF_KB, true, 64);
-    else if (n_experts <= 512 && ks <= 64 && T <= 64) K3_RF(1, 8, 64, false, 64 * nw);
+    else if (n_experts <= 512 && ks <= 16) K3_RF(1, 8, 16, false, 64 * nw);
+    else if (n_experts <= 512 && ks > 32 && ks <= 64 && T <= 64) K3_RF(1, 8, 64, false, 64 * nw);
     else if (n_experts <= 512) K3_RF(1, 8, RF_KB, false, 64 * nw);
     else if (n_experts <= 64 * RF_MAXW) K3_RF(1, 32, RF_KB, false, 64 * nw);
     else K3_RF(2, 32, RF_KB, false, 64 * nw);
