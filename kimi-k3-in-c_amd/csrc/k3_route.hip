@@ -984,9 +984,10 @@ __global__ __launch_bounds__(256) void combine_kernel(float *out, const float *c
             const int j = min(j0 + jj, topk - 1);
             const float *c = c0 + (size_t)j * E;
             if (VEC) {
-                /* unconditional: c0 points at column 0 for threads past the row */
-                const float4 v = *reinterpret_cast<const float4 *>(c);
-                cv[jj][0] = v.x; cv[jj][1] = v.y; cv[jj][2] = v.z; cv[jj][3] = v.w;
+                /* unconditional: c0 points at column 0 for threads past the row; the rows are
+                 * read once (non-temporal) */
+                const k3_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const k3_f32x4 *>(c));
+                cv[jj][0] = v[0]; cv[jj][1] = v[1]; cv[jj][2] = v[2]; cv[jj][3] = v[3];
             } else {
 #pragma unroll
                 for (int q = 0; q < 4; q++) cv[jj][q] = i + q < E ? c[q] : 0.0f;
