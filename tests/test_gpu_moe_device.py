@@ -408,6 +408,21 @@ def test_moe_graph_replay_matches_eager(gpu, small_layer):
     _graph_replay(gpu, s["bank"], s["W"], s["bias"], s["E"], s["I"], s["N"], s["K"], s["T"], 0, xs)
 
 
+@pytest.mark.parametrize("T,K", [(1, 8), (2, 8)])
+def test_moe_graph_replay_decode_path(gpu, k3, T, K):
+    """A few tokens captured in a HIP graph: the router's scored logits, the decode gate/up
+    kernel that selects the experts itself, down and the combine. Every replay equals the
+    eager call bit for bit."""
+    E, I, N = 1024, 512, 16
+    say(f"case: graph replay, decode path T={T} K={K}")
+    rng = np.random.default_rng(90 + T)
+    bank = [k3.gen_expert(E, I, 43, e) for e in range(N)]
+    W = (rng.standard_normal((N, E)) * 0.05).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.02).astype(np.float32)
+    xs = [rng.standard_normal((T, E)).astype(np.float32) for _ in range(3)]
+    _graph_replay(gpu, bank, W, bias, E, I, N, K, T, 0, xs)
+
+
 def test_moe_graph_replay_mixed_passes(gpu, k3):
     """The mixed pass lists (hot experts' 96-token passes on a side stream forked from the
     caller's and joined back) captured in a HIP graph: every replay equals the eager call
