@@ -407,7 +407,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
                           const void *bank, int layout, int hidden, int inter, int n_experts,
                           int topk, int act, float b1, float b2, int prec, const MoeWs *w,
                           int *perm_out, int *offsets_out, int *drops_out, const RouterSel *sel,
-                          void *stream)
+                          int x_split, void *stream)
 {
     int *perm = perm_out ? perm_out : w->perm;
     int *offsets = offsets_out ? offsets_out : w->offsets;
@@ -475,7 +475,8 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
         if (drops_out && k3k_d2d(drops_out, w->counts + 2, 4, stream)) return fail("drops");
         return 0;
     }
-    if (k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
+    /* (the routed layer runs the split beside its router, on the side stream) */
+    if (!x_split && k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
     const int pass_tok2 = moe_pass_tok2(pass_tok, layout, prec);
     if (k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
                    w->pass_job2, w->pass_tp2, w->counts, w->ghist, idx, T, topk, n_experts, bank,
@@ -561,7 +562,7 @@ int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x,
     moe_layout(&c, &w, T, hidden, inter, n_experts, topk, prec);
     k3k_prof_mark(stream, K3D_STAGE_BEGIN);
     return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
-                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, stream);
+                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, 0, stream);
 }
 
 int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const float *router_w,
@@ -593,14 +594,24 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
         k3k_prof_mark(stream, K3D_STAGE_ROUTER);
         const RouterSel sel = {r.part, router_w, bias, renorm, routed_scale, exc, r.nrecomp, idx, wt};
         return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
-                              b1, b2, prec, &w, NULL, NULL, drops_out, &sel, stream);
+                              b1, b2, prec, &w, NULL, NULL, drops_out, &sel, 0, stream);
+    }
+    /* past the decode path the expert kernels take the tokens' bf16 split: it depends on x
+     * alone, so it runs on the side stream beside the router (event fork / join, captured by
+     * a graph like the rest) */
+    const int split = !moe_decode_ok(T, hidden, inter, topk, x);
+    if (split) {
+        void *side;
+        if (k3k_fork(stream, &side)) return fail("fork");
+        if (k3k_split_bf16(w.xhi, w.xlo, x, (size_t)T * hidden, side)) return fail("split");
     }
     rc = router_run(idx, wt, x, T, router_w, bias, hidden, n_experts, topk, renorm, routed_scale,
                     &r, stream);
     if (rc) return rc;
+    if (split && k3k_join(stream)) return fail("join");
     k3k_prof_mark(stream, K3D_STAGE_ROUTER);
     return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
-                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, stream);
+                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, split, stream);
 }
 
 /* ---- tiled expert layout ---------------------------------------------------------------- */
