@@ -296,7 +296,8 @@ def time_gemv(steps=200, copies=128):
 def cpu_baseline(T_sample=8, budget_s=10.0):
     """The reference's own kernels (oracle/_ref, compiled from its src/core/k3_ops.c) in
     the reference composition, on the host cores, over a bounded sample of the batch-64
-    workload: the first T_sample tokens of batch 0."""
+    workload: the first T_sample tokens of batch 0. Runs in the process it is called in,
+    with the OpenMP threads that process's environment sets."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, Ref
     kind = "reference" if Ref.available() else "port"
@@ -309,48 +310,74 @@ def cpu_baseline(T_sample=8, budget_s=10.0):
     impl.moe_routed(X[:1], W, None, bank, E, I, K)          # warm-up
     times = []
     t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
         t0 = time.perf_counter()
         impl.moe_routed(X, W, None, bank, E, I, K)
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
-    one = single_thread_rate(impl, X[:1], W, bank)
     return {"value": round(T_sample / med, 3), "unit": "tokens/s", "cores": threads,
             "kind": kind,
             "sample": f"{T_sample} tokens of the batch-64 decode layer (router + 8 experts each, "
-                      f"SiLU), {len(times)} reps, median; spread {min(times):.3f}-{max(times):.3f} s",
-            "ms_per_token": round(med / T_sample * 1e3, 2),
-            "one_thread": one, "host": host_description()}
+                      f"SiLU), {len(times)} reps after one warm-up, median; spread "
+                      f"{min(times):.3f}-{max(times):.3f} s",
+            "ms_per_token": round(med / T_sample * 1e3, 2)}
 
 
-def single_thread_rate(impl, X1, W, bank, reps=3):
-    """The same composition on one OpenMP thread (one token, median of reps), through the
-    process's libgomp; the thread count is restored afterwards. None if libgomp cannot be
-    reached."""
-    import ctypes
+def host_cores():
+    """(physical cores, logical CPUs) this process may run on: the CPUs of its affinity
+    mask, grouped by (socket, core) from /proc/cpuinfo."""
+    cpus = sorted(os.sched_getaffinity(0))
+    core_of, cur = {}, {}
     try:
-        gomp = ctypes.CDLL("libgomp.so.1")
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if ":" not in line:
+                    if "processor" in cur:
+                        core_of[cur["processor"]] = (cur.get("physical id", "0"),
+                                                     cur.get("core id", cur["processor"]))
+                    cur = {}
+                    continue
+                k, v = (t.strip() for t in line.split(":", 1))
+                if k in ("processor", "physical id", "core id"):
+                    cur[k] = v
+        if "processor" in cur:
+            core_of[cur["processor"]] = (cur.get("physical id", "0"), cur.get("core id", cur["processor"]))
     except OSError:
-        return None
-    prev = gomp.omp_get_max_threads()
-    gomp.omp_set_num_threads(1)
-    try:
-        impl.moe_routed(X1, W, None, bank, E, I, K)           # warm-up
-        ts = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            impl.moe_routed(X1, W, None, bank, E, I, K)
-            ts.append(time.perf_counter() - t0)
-    finally:
-        gomp.omp_set_num_threads(prev)
-    med = float(np.median(ts))
-    return {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": 1,
-            "sample": f"1 token, {reps} reps, median; spread {min(ts):.3f}-{max(ts):.3f} s"}
+        pass
+    phys = {core_of.get(str(c), ("?", str(c))) for c in cpus}
+    return len(phys), len(cpus)
 
 
-def host_description():
-    """CPU model, AVX-512 presence and the C library version of the host the CPU numbers
-    come from."""
+def cpu_baseline_children():
+    """The CPU baseline in child processes started before this process touches the GPU, so
+    that the OpenMP runtime of each child starts with its own thread count: all physical
+    cores of this process's CPU share (at most the OMP_NUM_THREADS the environment allows),
+    then one thread, both with OMP_PROC_BIND=close and OMP_PLACES=cores."""
+    import subprocess
+    phys, logical = host_cores()
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    all_threads = max(1, min(phys, cap) if cap > 0 else phys)
+    res = {}
+    for label, n, sample in (("all", all_threads, 8), ("one", 1, 1)):
+        env = dict(os.environ, OMP_NUM_THREADS=str(n), OMP_PROC_BIND="close", OMP_PLACES="cores")
+        log(f"bench: CPU baseline on {n} thread(s) in a child process")
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-child", str(sample)],
+                           env=env, capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            raise RuntimeError(f"CPU baseline child failed ({r.returncode}): {r.stderr[-2000:]}")
+        res[label] = json.loads(r.stdout.strip().splitlines()[-1])
+    out = res["all"]
+    one = res["one"]
+    out["one_thread"] = {"value": one["value"], "unit": one["unit"], "cores": one["cores"],
+                         "sample": one["sample"], "ms_per_token": one["ms_per_token"]}
+    out["host"] = host_description(phys, logical)
+    out["env"] = "OMP_PROC_BIND=close OMP_PLACES=cores, OMP_NUM_THREADS set per child"
+    return out
+
+
+def host_description(phys=None, logical=None):
+    """CPU model, core counts, AVX-512 presence and the C library version of the host the
+    CPU numbers come from."""
     import platform
     model, avx512 = None, None
     try:
@@ -364,7 +391,8 @@ def host_description():
                     break
     except OSError:
         pass
-    return {"cpu": model, "logical_cpus": os.cpu_count(), "avx512f": avx512,
+    return {"cpu": model, "physical_cores": phys, "logical_cpus": logical,
+            "avx512f": avx512, "isa_path": "the reference's AVX2+FMA intrinsic path",
             "libc": " ".join(platform.libc_ver())}
 
 
@@ -395,10 +423,14 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (calibrates the HBM "
                          "byte counters of a profiler run) and exit")
     args = ap.parse_args()
+    if args.cpu_child:
+        print(json.dumps(cpu_baseline(T_sample=args.cpu_child, budget_s=10.0 if args.cpu_child > 1 else 3.0)))
+        return
     if args.copy_probe:
         copy_probe()
         return
@@ -407,6 +439,7 @@ def main():
               "(this build does not shard the layer across GPUs)", file=sys.stderr)
         sys.exit(2)
 
+    cb = None if args.no_cpu else cpu_baseline_children()    # before any GPU call
     layer = Layer()
     T = 64
     secs, stages, u_mean, uniq = time_layer(layer, T, args.steps, args.warmup)
@@ -466,8 +499,7 @@ def main():
         "prefill_4096": prefill,
         "skewed_512_shared": skewed,
     }
-    if not args.no_cpu:
-        cb = cpu_baseline()
+    if cb is not None:
         line["cpu_baseline"] = cb
         line["gpu_over_cpu"] = round(tok_s / cb["value"], 1)
     print(json.dumps(line), flush=True)

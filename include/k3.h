@@ -19,9 +19,10 @@
  *   - preconditions the reference aborts on abort here too, with a FATAL message, and a
  *     HIP error (no device, out of memory, kernel fault) also aborts: a void kernel never
  *     returns with its output unwritten (reference src/core/k3_ops.c:37-78);
- *   - calls are serialised on one HIP stream per process; the library is not re-entrant
- *     across host threads (the reference's kernels are, so callers that overlapped them
- *     from several threads must serialise).
+ *   - every entry point may be called from several host threads at once, as the
+ *     reference's kernels may (reference docs/API.md:138-139): the library takes one
+ *     process-wide lock per call and runs the calls one after another on its HIP stream,
+ *     so concurrent callers are safe and see the same results as sequential ones.
  */
 #ifndef K3_AMD_H
 #define K3_AMD_H
@@ -209,6 +210,41 @@ void k3_moe_routed(float *out, int *idx, float *wt, const float *x, int T,
                    const float *router_w, const float *bias, const K3ExpertQ *bank,
                    int hidden, int inter, int n_experts, int topk, int renorm,
                    float routed_scale, int act, float b1, float b2, int prec);
+
+/* An expert bank resident in HBM behind the reference's K3ExpertSrc: the device-side
+ * counterpart of the reference's host-RAM expert cache (src/cache/k3_cache.h, whose slots
+ * become K3ExpertQ pointers at src/cache/k3_cache.c:24-33). k3_devbank_source() returns a
+ * K3ExpertSrc to put in K3MoeW.src: its get() means "ensure resident in HBM" and returns
+ * DEVICE pointers (a miss fetches the expert's host bytes from `upstream`, any host-pointer
+ * K3ExpertSrc, or fails when upstream is NULL), getmany() is the batch form and resident()
+ * answers without a transfer. k3_moe / k3_moe_prefill given this source run the experts
+ * straight from the slots, with no weight transfer once the experts are resident. Experts
+ * are width x inter MXFP4 (gate/up [inter][width], down [width][inter], group 32); `slots`
+ * experts fit, least recently used evicted first, never one that the running MoE call has
+ * fetched. layout K3_BANK_TILED regroups each matrix once at admission for the expert
+ * kernels (widths multiples of 512), K3_BANK_ROWS keeps the reference's byte order.
+ * Device pointers from get() stay valid until that slot is evicted. No reference
+ * counterpart as a function; the run layout is the reference's (src/io/k3_load.h:3-18). */
+enum { K3_BANK_ROWS = 0, K3_BANK_TILED = 1 };
+typedef struct K3DevBank K3DevBank;
+typedef struct {
+    long hits, misses, evictions, failures;
+    unsigned long long bytes_uploaded;   /* host-to-device weight bytes so far */
+    int resident, slots;
+    size_t slot_bytes;
+} K3DevBankStats;
+K3DevBank *k3_devbank_create(int n_layers, int n_experts, int width, int inter, int slots,
+                             int layout, K3ExpertSrc *upstream);
+K3ExpertSrc *k3_devbank_source(K3DevBank *bank);
+/* Bytes of one expert's on-disk run: 3 * (width*inter/2 + width*inter/32), 17,547,264 for
+ * Kimi K3's 3584 x 3072 experts. */
+size_t k3_devbank_run_bytes(int width, int inter);
+/* Admits (or replaces) expert (layer, expert) from its contiguous run, in the reference's
+ * order w1.packed w1.scale w2.packed w2.scale w3.packed w3.scale (gate = w1, down = w2,
+ * up = w3). Returns 0, or -1 with k3_dev_last_error(). */
+int k3_devbank_put_run(K3DevBank *bank, int layer, int expert, const void *run, size_t bytes);
+int k3_devbank_stats(const K3DevBank *bank, K3DevBankStats *st);
+void k3_devbank_destroy(K3DevBank *bank);
 
 /* Device residency. Registers [host, host+bytes) as immutable weights: a device copy is
  * made now and every later call that receives a pointer inside the range reads the copy.

@@ -8,11 +8,20 @@
  * library's stream, and copies the outputs back before returning. A HIP failure aborts
  * with a FATAL message: these functions return void, and returning with the output
  * unwritten is the failure the reference refuses to allow (src/core/k3_ops.c:37-78).
+ *
+ * The reference's kernels may be called from several threads at once (its docs/API.md:
+ * 138-139). Here every entry point holds one process-wide recursive lock for its whole
+ * duration, so concurrent calls run one after another on the library's stream and share
+ * its device buffers safely; recursive, because a K3ExpertSrc callback that k3_moe calls
+ * may itself be this library's HBM bank.
  */
+#define _XOPEN_SOURCE 700
 #include "k3.h"
+#include "k3_bank.h"
 #include "k3_dev.h"
 #include "k3k.h"
 
+#include <pthread.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -21,8 +30,33 @@
 long k3_expert_drops = 0;
 
 /* ---------------------------------------------------------------- plumbing ---- */
+static pthread_mutex_t g_mu;
+static pthread_once_t g_mu_once = PTHREAD_ONCE_INIT;
+
+static void mu_init(void)
+{
+    pthread_mutexattr_t a;
+    pthread_mutexattr_init(&a);
+    pthread_mutexattr_settype(&a, PTHREAD_MUTEX_RECURSIVE);
+    pthread_mutex_init(&g_mu, &a);
+    pthread_mutexattr_destroy(&a);
+}
+
+void k3h_lock(void)
+{
+    pthread_once(&g_mu_once, mu_init);
+    pthread_mutex_lock(&g_mu);
+}
+
+void k3h_unlock(void) { pthread_mutex_unlock(&g_mu); }
+
 static void *g_stream = NULL;
 static char g_regerr[256];
+
+void k3h_set_error(const char *fmt, const char *what)
+{
+    snprintf(g_regerr, sizeof g_regerr, fmt, what);
+}
 
 static void fatal(const char *what)
 {
@@ -33,12 +67,21 @@ static void fatal(const char *what)
     abort();
 }
 
+int k3h_init(void)
+{
+    if (g_stream) return 0;
+    if (k3k_init() || !(g_stream = k3k_stream_create())) {
+        k3h_set_error("no usable HIP device: %s", k3k_error());
+        return -1;
+    }
+    return 0;
+}
+
+void *k3h_stream(void) { return g_stream; }
+
 static void lib_init(void)
 {
-    if (g_stream) return;
-    if (k3k_init()) fatal("no usable HIP device");
-    g_stream = k3k_stream_create();
-    if (!g_stream) fatal("stream creation");
+    if (k3h_init()) fatal("no usable HIP device");
 }
 
 static void check(int rc, const char *what)
@@ -101,7 +144,7 @@ static const Reg *reg_find(const void *host)
     return NULL;
 }
 
-void *k3_dev_lookup(const void *host)
+static void *k3_dev_lookup_impl(const void *host)
 {
     const Reg *r = host ? reg_find(host) : NULL;
     if (!r) return NULL;
@@ -110,13 +153,13 @@ void *k3_dev_lookup(const void *host)
 
 const char *k3_dev_last_error(void) { return g_regerr; }
 
-int k3_dev_register(const void *host, size_t bytes)
+static int k3_dev_register_impl(const void *host, size_t bytes)
 {
     if (!host || !bytes) {
         snprintf(g_regerr, sizeof g_regerr, "k3_dev_register: empty range");
         return -1;
     }
-    if (g_stream == NULL && (k3k_init() || !(g_stream = k3k_stream_create()))) {
+    if (k3h_init()) {
         snprintf(g_regerr, sizeof g_regerr, "k3_dev_register: %s", k3k_error());
         return -1;
     }
@@ -150,7 +193,7 @@ int k3_dev_register(const void *host, size_t bytes)
     return 0;
 }
 
-int k3_dev_unregister(const void *host)
+static int k3_dev_unregister_impl(const void *host)
 {
     for (int i = 0; i < g_nreg; i++)
         if (g_reg[i].host == (const unsigned char *)host) {
@@ -175,7 +218,7 @@ static const void *weights(int slot, const void *host, size_t bytes)
 static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 /* ------------------------------------------------------------------- GEMVs ---- */
-void k3_matmul(float *y, const float *x, const float *W, int in, int out)
+static void k3_matmul_impl(float *y, const float *x, const float *W, int in, int out)
 {
     if (out <= 0) return;
     lib_init();
@@ -186,7 +229,7 @@ void k3_matmul(float *y, const float *x, const float *W, int in, int out)
     download(y, dy, (size_t)out * 4);
 }
 
-void k3_matmul_bf16(float *y, const float *x, const uint16_t *W, int in, int out)
+static void k3_matmul_bf16_impl(float *y, const float *x, const uint16_t *W, int in, int out)
 {
     if (out <= 0) return;
     lib_init();
@@ -197,7 +240,7 @@ void k3_matmul_bf16(float *y, const float *x, const uint16_t *W, int in, int out
     download(y, dy, (size_t)out * 4);
 }
 
-void k3_matmul_q8(float *y, const float *x, const void *W, int in, int out)
+static void k3_matmul_q8_impl(float *y, const float *x, const void *W, int in, int out)
 {
     if (out <= 0) return;
     lib_init();
@@ -208,35 +251,29 @@ void k3_matmul_q8(float *y, const float *x, const void *W, int in, int out)
     download(y, dy, (size_t)out * 4);
 }
 
-/* Preconditions of the reference's k3_matmul_mxfp4 (k3_ops.c:1383-1401), same messages. */
+/* The reference's k3_matmul_mxfp4 refuses an odd `in` and a group above 64 with a FATAL
+ * abort (k3_ops.c:1383-1401); callers that rely on that still get it. */
 static void mxfp4_preconditions(int in, int group)
 {
     if (in & 1) {
         fprintf(stderr,
                 "k3: FATAL, k3_matmul_mxfp4 called with in=%d, which is odd.\n"
-                "    Packed rows are in/2 bytes, two elements per byte; an odd `in`\n"
-                "    truncates that stride below what the trailing group's odd\n"
-                "    remainder reads, a heap read past the caller's buffer instead\n"
-                "    of failing loudly.\n",
+                "    Two elements share each packed byte, so a row of an odd width has no\n"
+                "    whole-byte stride; the matrix cannot be addressed as given.\n",
                 in);
         abort();
     }
-    if (group > 64) {
+    if (group > 64 || group <= 0) {
         fprintf(stderr,
-                "k3: FATAL, k3_matmul_mxfp4 called with group=%d, which exceeds 64.\n"
-                "    Each group is expanded into a fixed wf[64] stack buffer before\n"
-                "    the dot product; a larger group overflows it instead of failing\n"
-                "    loudly.\n",
+                "k3: FATAL, k3_matmul_mxfp4 called with group=%d, outside 1..64.\n"
+                "    The MXFP4 format used here scales blocks of at most 64 elements\n"
+                "    (32 in every checkpoint); a larger or empty block is rejected.\n",
                 group);
-        abort();
-    }
-    if (group <= 0) {
-        fprintf(stderr, "k3: FATAL, k3_matmul_mxfp4 called with group=%d.\n", group);
         abort();
     }
 }
 
-void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
+static void k3_matmul_mxfp4_impl(float *y, const float *x, const unsigned char *packed,
                      const unsigned char *scales, int in, int rows, int group)
 {
     mxfp4_preconditions(in, group);
@@ -261,7 +298,7 @@ void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
     download(y, dy, (size_t)rows * 4);
 }
 
-void k3_mxfp4_dequant(float *out, const unsigned char *packed, const unsigned char *scales,
+static void k3_mxfp4_dequant_impl(float *out, const unsigned char *packed, const unsigned char *scales,
                       int rows, int pcols, int group)
 {
     if (rows <= 0 || pcols <= 0) return;
@@ -279,7 +316,7 @@ void k3_mxfp4_dequant(float *out, const unsigned char *packed, const unsigned ch
 }
 
 /* ------------------------------------------------------------ router, norms ---- */
-void k3_router(int *idx, float *w, const float *x, const float *W, const float *bias,
+static void k3_router_impl(int *idx, float *w, const float *x, const float *W, const float *bias,
                int hidden, int n_experts, int topk, int renorm, float routed_scale)
 {
     if (topk <= 0) return;
@@ -302,7 +339,7 @@ void k3_router(int *idx, float *w, const float *x, const float *W, const float *
     download(w, dwt, (size_t)topk * 4);
 }
 
-void k3_situ_glu(float *y, const float *x, int n, float b1, float b2)
+static void k3_situ_glu_impl(float *y, const float *x, int n, float b1, float b2)
 {
     if (n <= 0) return;
     lib_init();
@@ -312,7 +349,7 @@ void k3_situ_glu(float *y, const float *x, int n, float b1, float b2)
     download(y, dy, (size_t)n * 4);
 }
 
-void k3_rmsnorm(float *y, const float *x, const float *w, int n, float eps)
+static void k3_rmsnorm_impl(float *y, const float *x, const float *w, int n, float eps)
 {
     if (n <= 0) return;
     lib_init();
@@ -410,12 +447,12 @@ static void experts_generic(float *out_d, const int *idx, const float *wt_d, con
  * device pointers, NULL where absent): out_d[T][hidden] = sum_j wt * expert(x). */
 static void run_bank(float *out_d, const int *idx, const int *idx_d, const float *wt_d,
                      const float *x_d, int T, const QPtr *bank, int hidden, int inter,
-                     int n_experts, int topk, int act, float b1, float b2, int prec)
+                     int n_experts, int topk, int act, float b1, float b2, int prec, int layout)
 {
     if ((hidden % 32) == 0 && (inter % 32) == 0) {
         void *bank_d = upload(B_BANK, bank, (size_t)n_experts * sizeof(QPtr));
         const size_t wsb = k3d_moe_ws(T, hidden, inter, n_experts, topk, prec);
-        check(k3d_moe_experts(out_d, idx_d, wt_d, x_d, T, bank_d, K3D_LAYOUT_ROWS, hidden, inter,
+        check(k3d_moe_experts(out_d, idx_d, wt_d, x_d, T, bank_d, layout, hidden, inter,
                               n_experts, topk, act, b1, b2, prec, buf(B_WS, wsb), wsb, NULL, NULL,
                               NULL, g_stream),
               "moe experts");
@@ -449,7 +486,8 @@ static void run_experts_mxfp4(float *out_d, const int *idx, const int *idx_d, co
     size_t off = 0;
     for (int e = 0; e < n_experts; e++)
         if (sel[e] && expert_ok(&hbank[e])) resolve_expert(&bank[e], &hbank[e], hidden, inter, arena, &off);
-    run_bank(out_d, idx, idx_d, wt_d, x_d, T, bank, hidden, inter, n_experts, topk, act, b1, b2, prec);
+    run_bank(out_d, idx, idx_d, wt_d, x_d, T, bank, hidden, inter, n_experts, topk, act, b1, b2, prec,
+             K3D_LAYOUT_ROWS);
     free(bank);
     free(sel);
 }
@@ -461,7 +499,7 @@ static void report_drop(int layer, int expert, const char *what)
             expert, what);
 }
 
-void k3_expert_ffn(float *out, const float *x, const K3ExpertQ *q, int hidden, int inter, int act,
+static void k3_expert_ffn_impl(float *out, const float *x, const K3ExpertQ *q, int hidden, int inter, int act,
                    float b1, float b2, float wt)
 {
     if (hidden <= 0) return;
@@ -482,7 +520,7 @@ void k3_expert_ffn(float *out, const float *x, const K3ExpertQ *q, int hidden, i
     download(out, dy, (size_t)hidden * 4);
 }
 
-void k3_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const float *router_w,
+static void k3_moe_routed_impl(float *out, int *idx, float *wt, const float *x, int T, const float *router_w,
                    const float *bias, const K3ExpertQ *bank, int hidden, int inter, int n_experts,
                    int topk, int renorm, float routed_scale, int act, float b1, float b2, int prec)
 {
@@ -541,13 +579,125 @@ static void mmw_dev(float *y_d, const float *x_d, int ntok, const void *W, int w
     check(rc, "k3_mmw");
 }
 
+/* ---------------------------------------------------- streamed-expert fetching ---- */
+/* The experts of one MoE call, fetched through K3ExpertSrc in exactly the order the
+ * reference calls it, so a source sees the same get / getmany / resident sequence and the
+ * same drops are counted:
+ *   k3_moe (k3_ops.c:576-626), per token: the cache-only compaction through resident(),
+ *     getmany(idx, nk) unless cache-only, then get() (resident() when cache-only) for
+ *     every slot j < nk; a failed get() is one drop for that (token, slot);
+ *   moe_prefill_chunk (k3_ops.c:728-781), per 64-token chunk: getmany over the chunk's
+ *     unique experts in first-seen (t, j) order, then one get() per unique expert; a
+ *     failed get() is one drop for the chunk and empties every slot of the chunk that
+ *     selected it (a chunk of one token goes through the per-token form, :710-713).
+ * Each expert's bytes go to the device on its first successful fetch of the call (or, from
+ * this library's HBM bank, are used where they lie), before the next callback can recycle
+ * them. didx is the device copy of the routing: -1 marks a slot that contributes nothing
+ * (dropped, filtered by the cache-only routing, or past the kept slots). */
+typedef struct {
+    const K3MoeW *w;
+    int L, I, N, K, T;
+    int bank_layout;          /* -1: the source hands out host pointers; else K3_BANK_* */
+    QPtr *bank;               /* [N] device pointers of the fetched experts */
+    char *arena;
+    size_t off;
+    int *hidx, *didx;
+    float *hwt;
+} Fetch;
+
+static int fetch(Fetch *f, int e, int via_resident)
+{
+    K3ExpertSrc *s = f->w->src;
+    K3ExpertQ q;
+    memset(&q, 0, sizeof q);
+    int miss;
+    if (via_resident) miss = !s->resident || !s->resident(s, f->w->layer, e, &q);
+    else miss = s->get(s, f->w->layer, e, &q) != 0;
+    /* a source that reports success with a missing tensor is treated as a failed fetch
+     * (the reference would dereference the NULL pointer) */
+    if (miss || !expert_ok(&q) || e < 0 || e >= f->N) return 0;
+    if (!f->bank[e].p1) {
+        if (f->bank_layout >= 0) {
+            f->bank[e].p1 = q.p1; f->bank[e].s1 = q.s1; f->bank[e].p3 = q.p3;
+            f->bank[e].s3 = q.s3; f->bank[e].p2 = q.p2; f->bank[e].s2 = q.s2;
+        } else {
+            resolve_expert(&f->bank[e], &q, f->L, f->I, f->arena, &f->off);
+            check(k3k_sync(g_stream), "synchronize");   /* bytes taken before the next get() */
+        }
+    }
+    return 1;
+}
+
+/* k3_moe's per-token form for token t. */
+static void fetch_token(Fetch *f, int t)
+{
+    const K3MoeW *w = f->w;
+    const int K = f->K;
+    int *it = f->hidx + (size_t)t * K, *dt = f->didx + (size_t)t * K;
+    float *wtt = f->hwt + (size_t)t * K;
+    int nk = K;
+    if (w->cache_only && w->src->resident) {
+        int m = 0;
+        float wsum = 0.0f;
+        for (int j = 0; j < K; j++)
+            if (w->src->resident(w->src, w->layer, it[j], NULL)) {
+                it[m] = it[j];
+                wtt[m] = wtt[j];
+                wsum += wtt[j];
+                m++;
+            }
+        nk = m;
+        if (wsum > 0.0f)
+            for (int j = 0; j < nk; j++) wtt[j] /= wsum;
+    }
+    if (!w->cache_only && w->src->getmany) w->src->getmany(w->src, w->layer, it, nk);
+    for (int j = 0; j < K; j++) dt[j] = -1;
+    for (int j = 0; j < nk; j++) {
+        if (fetch(f, it[j], w->cache_only)) {
+            dt[j] = it[j];
+        } else if (!w->cache_only) {
+            report_drop(w->layer, it[j], "token");
+        }
+    }
+}
+
+/* moe_prefill_chunk's fetch for the n-token chunk starting at t0. */
+static void fetch_chunk(Fetch *f, int t0, int n, int *uniq, unsigned char *seen)
+{
+    const K3MoeW *w = f->w;
+    const int K = f->K;
+    const size_t a0 = (size_t)t0 * K, a1 = (size_t)(t0 + n) * K;
+    int nu = 0;
+    memset(seen, 0, (size_t)f->N);
+    for (size_t a = a0; a < a1; a++) {
+        const int e = f->hidx[a];
+        f->didx[a] = e;
+        if (e >= 0 && e < f->N && !seen[e]) {
+            seen[e] = 1;
+            uniq[nu++] = e;
+        }
+    }
+    if (w->src->getmany) w->src->getmany(w->src, w->layer, uniq, nu);
+    for (int u = 0; u < nu; u++) {
+        const int e = uniq[u];
+        if (fetch(f, e, 0)) continue;
+        report_drop(w->layer, e, "chunk");
+        for (size_t a = a0; a < a1; a++)
+            if (f->hidx[a] == e) f->didx[a] = -1;
+    }
+}
+
 /* Stable LatentMoE over T tokens (reference k3_ops.c:556-656), batched on the device:
  * route all tokens, down-project, run the selected experts expert-major, sum in slot
- * order, RMSNorm the aggregate, up-project, add the unweighted shared expert. prefill
- * selects the reference's expert-major drop accounting (k3_ops.c:760-781) over its
- * per-token one (:616-626); the arithmetic is the same either way, as in the reference. */
+ * order, RMSNorm the aggregate, up-project, add the unweighted shared expert. The
+ * arithmetic per token is the same in both forms, as in the reference; `batched` selects
+ * the fetch order and drop accounting of k3_moe_prefill's expert-major chunks over
+ * k3_moe's per-token one. idx/wt receive what the reference leaves there: the last
+ * token's routing after a per-token pass, nothing after a batched chunk. */
+#define MOE_DEV_BLOCK 1024    /* tokens per device pass of the experts (bounds contrib) */
+
 static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T,
-                       int *idx_last, float *wt_last, int prefill)
+                       int *idx_last, float *wt_last, int batched)
 {
     const int E = c->hidden, L = c->latent, I = c->moe_inter, K = c->topk, N = c->n_experts;
     const int SI = I * c->n_shared;
@@ -559,8 +709,9 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
     lib_init();
     const size_t TK = (size_t)T * K;
     int *hidx = (int *)malloc(TK * sizeof(int));
+    int *didx = (int *)malloc(TK * sizeof(int));
     float *hwt = (float *)malloc(TK * sizeof(float));
-    if (!hidx || !hwt) {
+    if (!hidx || !didx || !hwt) {
         fprintf(stderr, "k3: FATAL, host allocation in k3_moe failed.\n");
         abort();
     }
@@ -579,80 +730,76 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
     check(k3k_d2h(hidx, di, TK * 4, g_stream), "device to host copy");
     download(hwt, dwt, TK * 4);
 
-    /* Draft cache-only routing (k3_ops.c:584-593): keep resident experts, renormalise. */
-    if (w->cache_only && w->src && w->src->resident) {
-        for (int t = 0; t < T; t++) {
-            int *it = hidx + (size_t)t * K;
-            float *wtt = hwt + (size_t)t * K;
-            int m = 0;
-            float wsum = 0.0f;
-            for (int j = 0; j < K; j++)
-                if (w->src->resident(w->src, w->layer, it[j], NULL)) {
-                    it[m] = it[j];
-                    wtt[m] = wtt[j];
-                    wsum += wtt[j];
-                    m++;
-                }
-            if (wsum > 0.0f)
-                for (int j = 0; j < m; j++) wtt[j] /= wsum;
-            for (int j = m; j < K; j++) {
-                it[j] = -1;        /* filtered slot: contributes nothing */
-                wtt[j] = 0.0f;
-            }
-        }
-        check(k3k_h2d(di, hidx, TK * 4, g_stream), "host to device copy");
-        check(k3k_h2d(dwt, hwt, TK * 4, g_stream), "host to device copy");
-    }
-
     /* 2. down-project into the latent space */
     float *dz = (float *)buf(B_Z, (size_t)T * L * 4);
     mmw_dev(dz, dx, T, w->down, w->wdt, E, L, L, B_P);
 
     /* 3. routed experts, weighted sum in slot order */
     float *dacc = (float *)buf(B_ACC, (size_t)T * L * 4);
+    int wrote_last = 0;
     if (w->src) {
-        /* Expert-major: fetch each unique expert once and take its bytes to the device
-         * before the next get(), which may recycle the source's memory (the reference's
-         * prefill loop also consumes each expert before fetching the next, k3_ops.c:757-795). */
-        QPtr *bank = (QPtr *)calloc((size_t)N, sizeof(QPtr));
+        Fetch f;
+        memset(&f, 0, sizeof f);
+        f.w = w;
+        f.L = L;
+        f.I = I;
+        f.N = N;
+        f.K = K;
+        f.T = T;
+        f.hidx = hidx;
+        f.didx = didx;
+        f.hwt = hwt;
+        f.bank_layout = k3_bank_layout(w->src, L, I);
+        if (f.bank_layout == -2) {
+            fprintf(stderr, "k3: FATAL, k3_moe: the HBM expert bank holds experts of another "
+                            "shape than latent=%d x moe_inter=%d.\n", L, I);
+            abort();
+        }
+        f.bank = (QPtr *)calloc((size_t)N, sizeof(QPtr));
         int *uniq = (int *)malloc(TK * sizeof(int));
         unsigned char *seen = (unsigned char *)calloc((size_t)N, 1);
-        if (!bank || !uniq || !seen) {
+        if (!f.bank || !uniq || !seen) {
             fprintf(stderr, "k3: FATAL, host allocation in k3_moe failed.\n");
             abort();
         }
-        int nu = 0;
-        for (size_t a = 0; a < TK; a++) {
-            const int e = hidx[a];
-            if (e >= 0 && e < N && !seen[e]) { seen[e] = 1; uniq[nu++] = e; }
-        }
-        const size_t per_expert = 2 * (pk_bytes(I, L) + sc_bytes(I, L)) + pk_bytes(L, I) +
-                                  sc_bytes(L, I) + 6 * 512;
-        char *arena = nu ? (char *)buf(B_ARENA, (size_t)nu * per_expert) : NULL;
-        size_t off = 0;
-        if (!w->cache_only && w->src->getmany) w->src->getmany(w->src, w->layer, uniq, nu);
-        for (int u = 0; u < nu; u++) {
-            const int e = uniq[u];
-            K3ExpertQ q;
-            memset(&q, 0, sizeof q);
-            const int miss = w->cache_only ? !w->src->resident(w->src, w->layer, e, &q)
-                                           : (w->src->get(w->src, w->layer, e, &q) != 0);
-            if (miss || !expert_ok(&q)) {
-                if (w->cache_only) continue;
-                if (prefill) {
-                    report_drop(w->layer, e, "chunk");
-                } else {
-                    for (size_t a = 0; a < TK; a++)
-                        if (hidx[a] == e) report_drop(w->layer, e, "token");
-                }
-                continue;
+        if (f.bank_layout < 0) {
+            /* upper bound of the upload arena: every expert the routing names, once */
+            int nu = 0;
+            for (size_t a = 0; a < TK; a++) {
+                const int e = hidx[a];
+                if (e >= 0 && e < N && !seen[e]) { seen[e] = 1; nu++; }
             }
-            resolve_expert(&bank[e], &q, L, I, arena, &off);
-            check(k3k_sync(g_stream), "synchronize");      /* bytes taken before next get() */
+            const size_t per_expert = 2 * (pk_bytes(I, L) + sc_bytes(I, L)) + pk_bytes(L, I) +
+                                      sc_bytes(L, I) + 6 * 512;
+            f.arena = nu ? (char *)buf(B_ARENA, (size_t)nu * per_expert) : NULL;
         }
-        run_bank(dacc, hidx, di, dwt, dz, T, bank, L, I, N, K, K3_ACT_SITU, c->situ_b1,
-                 c->situ_b2, 0);
-        free(bank);
+        k3_bank_call(w->src, 1);
+        if (batched) {
+            for (int t0 = 0; t0 < T; t0 += 64) {
+                const int n = T - t0 < 64 ? T - t0 : 64;
+                if (n == 1) {
+                    fetch_token(&f, t0);
+                    wrote_last = 1;
+                } else {
+                    fetch_chunk(&f, t0, n, uniq, seen);
+                }
+            }
+        } else {
+            for (int t = 0; t < T; t++) fetch_token(&f, t);
+            wrote_last = 1;
+        }
+        /* the routing the device uses: kept slots, renormalised weights */
+        check(k3k_h2d(di, didx, TK * 4, g_stream), "host to device copy");
+        check(k3k_h2d(dwt, hwt, TK * 4, g_stream), "host to device copy");
+        const int layout = f.bank_layout >= 0 ? f.bank_layout : K3D_LAYOUT_ROWS;
+        for (int b0 = 0; b0 < T; b0 += MOE_DEV_BLOCK) {
+            const int nb = T - b0 < MOE_DEV_BLOCK ? T - b0 : MOE_DEV_BLOCK;
+            const size_t o = (size_t)b0 * K;
+            run_bank(dacc + (size_t)b0 * L, didx + o, di + o, dwt + o, dz + (size_t)b0 * L, nb,
+                     f.bank, L, I, N, K, K3_ACT_SITU, c->situ_b1, c->situ_b2, 0, layout);
+        }
+        k3_bank_call(w->src, 0);
+        free(f.bank);
         free(uniq);
         free(seen);
     } else {
@@ -677,6 +824,7 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
                       "expert w2");
             }
         check(k3k_combine(dacc, contrib, dwt, di, NULL, N, T, K, L, g_stream), "combine");
+        wrote_last = 1;
     }
 
     /* 4. RMSNorm of the aggregate, 5. up-project */
@@ -699,9 +847,12 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
         check(k3k_axpy_rows(dout, sdn, (size_t)T * E, g_stream), "shared add");
     }
     download(out, dout, (size_t)T * E * 4);
-    if (idx_last) memcpy(idx_last, hidx + (size_t)(T - 1) * K, (size_t)K * sizeof(int));
-    if (wt_last) memcpy(wt_last, hwt + (size_t)(T - 1) * K, (size_t)K * sizeof(float));
+    if (wrote_last) {
+        if (idx_last) memcpy(idx_last, hidx + (size_t)(T - 1) * K, (size_t)K * sizeof(int));
+        if (wt_last) memcpy(wt_last, hwt + (size_t)(T - 1) * K, (size_t)K * sizeof(float));
+    }
     free(hidx);
+    free(didx);
     free(hwt);
 }
 
@@ -709,13 +860,120 @@ void k3_moe(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T, 
             float *wt, float *scratch)
 {
     (void)scratch;
+    k3h_lock();
     moe_latent(out, x, w, c, T, idx, wt, 0);
+    k3h_unlock();
 }
 
 void k3_moe_prefill(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T, int *idx,
                     float *wt, float *scratch)
 {
     (void)scratch;
+    /* the reference's conditions for its batched form (k3_ops.c:693-702) */
     const int batched = w->src && T > 1 && !w->cache_only && !getenv("K3_NO_BATCH_PREFILL");
+    k3h_lock();
     moe_latent(out, x, w, c, T, idx, wt, batched);
+    k3h_unlock();
+}
+
+/* ------------------------------------------ locked entry points (see the top) ---- */
+void k3_matmul(float *y, const float *x, const float *W, int in, int out)
+{
+    k3h_lock();
+    k3_matmul_impl(y, x, W, in, out);
+    k3h_unlock();
+}
+
+void k3_matmul_bf16(float *y, const float *x, const uint16_t *W, int in, int out)
+{
+    k3h_lock();
+    k3_matmul_bf16_impl(y, x, W, in, out);
+    k3h_unlock();
+}
+
+void k3_matmul_q8(float *y, const float *x, const void *W, int in, int out)
+{
+    k3h_lock();
+    k3_matmul_q8_impl(y, x, W, in, out);
+    k3h_unlock();
+}
+
+void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
+                     const unsigned char *scales, int in, int rows, int group)
+{
+    k3h_lock();
+    k3_matmul_mxfp4_impl(y, x, packed, scales, in, rows, group);
+    k3h_unlock();
+}
+
+void k3_mxfp4_dequant(float *out, const unsigned char *packed, const unsigned char *scales,
+                      int rows, int pcols, int group)
+{
+    k3h_lock();
+    k3_mxfp4_dequant_impl(out, packed, scales, rows, pcols, group);
+    k3h_unlock();
+}
+
+void k3_router(int *idx, float *w, const float *x, const float *W, const float *bias,
+               int hidden, int n_experts, int topk, int renorm, float routed_scale)
+{
+    k3h_lock();
+    k3_router_impl(idx, w, x, W, bias, hidden, n_experts, topk, renorm, routed_scale);
+    k3h_unlock();
+}
+
+void k3_situ_glu(float *y, const float *x, int n, float b1, float b2)
+{
+    k3h_lock();
+    k3_situ_glu_impl(y, x, n, b1, b2);
+    k3h_unlock();
+}
+
+void k3_rmsnorm(float *y, const float *x, const float *w, int n, float eps)
+{
+    k3h_lock();
+    k3_rmsnorm_impl(y, x, w, n, eps);
+    k3h_unlock();
+}
+
+void k3_expert_ffn(float *out, const float *x, const K3ExpertQ *q, int hidden, int inter, int act,
+                   float b1, float b2, float wt)
+{
+    k3h_lock();
+    k3_expert_ffn_impl(out, x, q, hidden, inter, act, b1, b2, wt);
+    k3h_unlock();
+}
+
+void k3_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const float *router_w,
+                   const float *bias, const K3ExpertQ *bank, int hidden, int inter, int n_experts,
+                   int topk, int renorm, float routed_scale, int act, float b1, float b2, int prec)
+{
+    k3h_lock();
+    k3_moe_routed_impl(out, idx, wt, x, T, router_w, bias, bank, hidden, inter, n_experts, topk,
+                       renorm, routed_scale, act, b1, b2, prec);
+    k3h_unlock();
+}
+
+int k3_dev_register(const void *host, size_t bytes)
+{
+    k3h_lock();
+    int r = k3_dev_register_impl(host, bytes);
+    k3h_unlock();
+    return r;
+}
+
+int k3_dev_unregister(const void *host)
+{
+    k3h_lock();
+    int r = k3_dev_unregister_impl(host);
+    k3h_unlock();
+    return r;
+}
+
+void *k3_dev_lookup(const void *host)
+{
+    k3h_lock();
+    void *r = k3_dev_lookup_impl(host);
+    k3h_unlock();
+    return r;
 }

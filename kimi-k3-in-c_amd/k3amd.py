@@ -71,7 +71,13 @@ class K3Cfg(C.Structure):
 class K3MoeW(C.Structure):
     _fields_ = [("gate", P), ("bias", P), ("w1", P), ("w3", P), ("w2", P), ("latent_norm", P),
                 ("down", P), ("up", P), ("sh1", P), ("sh3", P), ("sh2", P), ("wdt", I),
-                ("src", C.POINTER(K3ExpertSrc)), ("layer", I), ("cache_only", I)]
+                ("src", P), ("layer", I), ("cache_only", I)]
+
+
+class K3DevBankStats(C.Structure):
+    _fields_ = [("hits", C.c_long), ("misses", C.c_long), ("evictions", C.c_long),
+                ("failures", C.c_long), ("bytes_uploaded", C.c_ulonglong), ("resident", I),
+                ("slots", I), ("slot_bytes", SZ)]
 
 
 def _declare(L):
@@ -97,6 +103,12 @@ def _declare(L):
     d("k3_dev_unregister", I, P)
     d("k3_dev_lookup", P, P)
     d("k3_dev_last_error", C.c_char_p)
+    d("k3_devbank_create", P, I, I, I, I, I, I, P)
+    d("k3_devbank_source", P, P)
+    d("k3_devbank_run_bytes", SZ, I, I)
+    d("k3_devbank_put_run", I, P, I, I, P, SZ)
+    d("k3_devbank_stats", I, P, C.POINTER(K3DevBankStats))
+    d("k3_devbank_destroy", None, P)
     # device API
     d("k3d_init", I)
     d("k3d_error", C.c_char_p)
@@ -144,7 +156,9 @@ def exported_symbols():
     return ["k3_matmul", "k3_matmul_bf16", "k3_matmul_q8", "k3_mxfp4_dequant",
             "k3_matmul_mxfp4", "k3_router", "k3_situ_glu", "k3_rmsnorm", "k3_moe_scratch",
             "k3_moe", "k3_moe_prefill", "k3_expert_ffn", "k3_moe_routed", "k3_dev_register",
-            "k3_dev_unregister", "k3_dev_lookup", "k3_dev_last_error", "k3_expert_drops"]
+            "k3_dev_unregister", "k3_dev_lookup", "k3_dev_last_error", "k3_expert_drops",
+            "k3_devbank_create", "k3_devbank_source", "k3_devbank_run_bytes",
+            "k3_devbank_put_run", "k3_devbank_stats", "k3_devbank_destroy"]
 
 
 def _p(a):
@@ -265,6 +279,74 @@ def moe_routed(x, router_w, bias, bank, hidden, inter, topk, renorm=1, routed_sc
 
 def expert_drops():
     return C.c_long.in_dll(lib(), "k3_expert_drops").value
+
+
+def cfg_struct(cfg):
+    """K3Cfg from a dict with hidden, latent, inter, n_experts, topk, n_shared, renorm,
+    latent_norm, routed_scale, rms_eps, b1, b2 (the MoE fields; the rest stay zero)."""
+    c = K3Cfg()
+    c.hidden, c.latent, c.moe_inter = cfg["hidden"], cfg["latent"], cfg["inter"]
+    c.n_experts, c.topk, c.n_shared = cfg["n_experts"], cfg["topk"], cfg["n_shared"]
+    c.moe_renorm, c.latent_norm = cfg["renorm"], cfg["latent_norm"]
+    c.routed_scale, c.rms_eps = cfg["routed_scale"], cfg["rms_eps"]
+    c.situ_b1, c.situ_b2 = cfg["b1"], cfg["b2"]
+    return c
+
+
+def moe(x, cfg, W, wdt, src_ptr, prefill, layer=0, cache_only=0, idx=None, wt=None):
+    """k3_moe (prefill 0) or k3_moe_prefill (prefill 1) through the library. W: dict of
+    host arrays gate, bias, latent_norm, down, up, sh1, sh3, sh2 (w1/w3/w2 for the
+    resident fp32 bank); src_ptr: address of a K3ExpertSrc or None. Returns out, idx, wt
+    (the topk-wide buffers after the call, initialised to -7 / nan unless given) and the
+    increase of k3_expert_drops."""
+    c = cfg_struct(cfg)
+    g = lambda k: W[k].ctypes.data if W.get(k) is not None else None  # noqa: E731
+    w = K3MoeW(g("gate"), g("bias"), g("w1"), g("w3"), g("w2"), g("latent_norm"), g("down"),
+               g("up"), g("sh1"), g("sh3"), g("sh2"), wdt, src_ptr, layer, cache_only)
+    x = _f32(x).reshape(-1, cfg["hidden"])
+    out = np.empty_like(x)
+    K = cfg["topk"]
+    idx = np.full(K, -7, np.int32) if idx is None else np.array(idx, np.int32)
+    wt = np.full(K, np.nan, np.float32) if wt is None else np.array(wt, np.float32)
+    scratch = np.empty(lib().k3_moe_scratch(C.byref(c)), np.float32)
+    d0 = expert_drops()
+    fn = lib().k3_moe_prefill if prefill else lib().k3_moe
+    fn(_p(out), _p(x), C.byref(w), C.byref(c), x.shape[0], _p(idx), _p(wt), _p(scratch))
+    return out, idx, wt, expert_drops() - d0
+
+
+class HbmBank:
+    """k3_devbank_*: an expert bank in HBM behind a K3ExpertSrc."""
+
+    def __init__(self, n_layers, n_experts, width, inter, slots, layout=K3D_LAYOUT_TILED,
+                 upstream_ptr=None):
+        self.h = lib().k3_devbank_create(n_layers, n_experts, width, inter, slots, layout,
+                                         upstream_ptr)
+        if not self.h:
+            raise RuntimeError("k3_devbank_create: " + lib().k3_dev_last_error().decode())
+        self.src = lib().k3_devbank_source(self.h)
+        self.width, self.inter = width, inter
+
+    def put_run(self, layer, expert, run):
+        run = _u8(run)
+        rc = lib().k3_devbank_put_run(self.h, layer, expert, run.ctypes.data, run.nbytes)
+        if rc != 0:
+            raise RuntimeError("k3_devbank_put_run: " + lib().k3_dev_last_error().decode())
+
+    def stats(self):
+        st = K3DevBankStats()
+        check_dev(lib().k3_devbank_stats(self.h, C.byref(st)), "k3_devbank_stats")
+        return {k: getattr(st, k) for k, _ in K3DevBankStats._fields_}
+
+    def destroy(self):
+        if self.h:
+            lib().k3_devbank_destroy(self.h)
+            self.h = None
+
+
+def check_dev(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what}: {lib().k3_dev_last_error().decode()}")
 
 
 def dev_register(arr):

@@ -430,6 +430,199 @@ void orc_moe_latent(float *out, const float *x, const OrcMoeW *w, const OrcMoeCf
     free(wt);
 }
 
+/* ------------------------------------------------- streamed MXFP4 LatentMoE ---- */
+/* k3_mmw (include/k3/k3.h:289-295) for the two weight types the MoE tail uses here. */
+static void mmw(float *y, const float *x, const void *W, int wdt, int in, int out)
+{
+    if (wdt == 1) orc_matmul_bf16(y, x, (const uint16_t *)W, in, out);
+    else if (wdt == 0) orc_matmul(y, x, (const float *)W, in, out);
+    else fatal("orc_moe_q: weight type not restated", wdt);
+}
+
+/* One (token, slot) of a streamed expert: gate/up out of MXFP4, SiTU, down
+ * (k3_ops.c:628-631 and :788-791, identical arithmetic). */
+static void expert_q(float *edn, const float *z, const OrcExpertQ *q, int L, int I,
+                     float b1, float b2, float *gu, float *act)
+{
+    orc_matmul_mxfp4(gu, z, q->p1, q->s1, L, I, 32);
+    orc_matmul_mxfp4(gu + I, z, q->p3, q->s3, L, I, 32);
+    orc_situ_glu(act, gu, I, b1, b2);
+    orc_matmul_mxfp4(edn, act, q->p2, q->s2, I, L, 32);
+}
+
+/* The tail shared by both forms (k3_ops.c:646-654 and :813-820): RMSNorm of the
+ * aggregate, up-projection, then the shared expert on the original input added
+ * unweighted. acc is modified in place. */
+static void moe_tail(float *ot, float *acc, const float *xt, const OrcMoeQW *w,
+                     const OrcMoeCfg *c, float *sgu, float *sact, float *sdn)
+{
+    const int E = c->hidden, L = c->latent, SI = c->inter * c->n_shared;
+    if (c->latent_norm) orc_rmsnorm(acc, acc, w->latent_norm, L, c->rms_eps);
+    mmw(ot, acc, w->up, w->wdt, L, E);
+    mmw(sgu, xt, w->sh1, w->wdt, E, SI);
+    mmw(sgu + SI, xt, w->sh3, w->wdt, E, SI);
+    orc_situ_glu(sact, sgu, SI, c->b1, c->b2);
+    mmw(sdn, sact, w->sh2, w->wdt, SI, E);
+    for (int i = 0; i < E; i++) ot[i] += sdn[i];
+}
+
+typedef struct {
+    float *z, *acc, *gu, *act, *edn, *sgu, *sact, *sdn;
+} QScr;
+
+static void qscr_alloc(QScr *s, const OrcMoeCfg *c)
+{
+    const int E = c->hidden, L = c->latent, I = c->inter, SI = c->inter * c->n_shared;
+    float *p = (float *)malloc((size_t)(2 * L + 3 * I + L + 3 * SI + E) * sizeof(float));
+    if (!p) fatal("oracle allocation", E);
+    s->z = p;
+    s->acc = s->z + L;
+    s->gu = s->acc + L;
+    s->act = s->gu + 2 * I;
+    s->edn = s->act + I;
+    s->sgu = s->edn + L;
+    s->sact = s->sgu + 2 * SI;
+    s->sdn = s->sact + SI;
+}
+
+/* k3_moe (k3_ops.c:556-656) with a streamed source, tokens one after another. idx/wt
+ * are topk-wide and reused per token, so they end holding the last token's routing
+ * (after the cache-only compaction, whose tail keeps the router's values). */
+static void moe_q_tokens(float *out, const float *x, const OrcMoeQW *w, const OrcMoeCfg *c,
+                         int T, int *idx, float *wt, long *drops)
+{
+    const int E = c->hidden, L = c->latent, I = c->inter, K = c->topk;
+    OrcExpertSrc *src = w->src;
+    QScr s;
+    qscr_alloc(&s, c);
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * E;
+        float *ot = out + (size_t)t * E;
+        orc_router(idx, wt, xt, w->gate, w->bias, E, c->n_experts, K, c->renorm,
+                   c->routed_scale);
+        int nk = K;
+        if (w->cache_only && src->resident) {
+            int m = 0;
+            float wsum = 0.0f;
+            for (int j = 0; j < K; j++)
+                if (src->resident(src, w->layer, idx[j], NULL)) {
+                    idx[m] = idx[j];
+                    wt[m] = wt[j];
+                    wsum += wt[j];
+                    m++;
+                }
+            nk = m;
+            if (wsum > 0.0f)
+                for (int j = 0; j < nk; j++) wt[j] /= wsum;
+        }
+        mmw(s.z, xt, w->down, w->wdt, E, L);
+        for (int i = 0; i < L; i++) s.acc[i] = 0.0f;
+        if (!w->cache_only && src->getmany) src->getmany(src, w->layer, idx, nk);
+        for (int j = 0; j < nk; j++) {
+            OrcExpertQ q;
+            const int miss = w->cache_only ? !src->resident(src, w->layer, idx[j], &q)
+                                           : (src->get(src, w->layer, idx[j], &q) != 0);
+            if (miss) {
+                if (!w->cache_only) (*drops)++;
+                continue;
+            }
+            expert_q(s.edn, s.z, &q, L, I, c->b1, c->b2, s.gu, s.act);
+            const float wj = wt[j];
+            for (int i = 0; i < L; i++) s.acc[i] += wj * s.edn[i];
+        }
+        moe_tail(ot, s.acc, xt, w, c, s.sgu, s.sact, s.sdn);
+    }
+    free(s.z);
+}
+
+/* moe_prefill_chunk (k3_ops.c:717-825): route and down-project every token of the chunk,
+ * list its unique experts in first-seen (t, j) order, fetch each once (a failed fetch is
+ * one drop for the chunk and zeroes every slot it would have filled), compute every
+ * (token, slot) of that expert into contrib, then per token sum contrib in slot order and
+ * finish with the same tail as k3_moe. idx/wt are not written. */
+static void moe_q_chunk(float *out, const float *x, const OrcMoeQW *w, const OrcMoeCfg *c,
+                        int T, long *drops)
+{
+    const int E = c->hidden, L = c->latent, I = c->inter, K = c->topk, N = c->n_experts;
+    OrcExpertSrc *src = w->src;
+    int *ridx = (int *)malloc((size_t)T * K * sizeof(int));
+    float *rwt = (float *)malloc((size_t)T * K * sizeof(float));
+    float *zz = (float *)malloc((size_t)T * L * sizeof(float));
+    float *contrib = (float *)malloc((size_t)T * K * L * sizeof(float));
+    int *uniq = (int *)malloc((size_t)T * K * sizeof(int));
+    char *seen = (char *)calloc((size_t)N, 1);
+    if (!ridx || !rwt || !zz || !contrib || !uniq || !seen) fatal("oracle allocation", T);
+    QScr s;
+    qscr_alloc(&s, c);
+    int nu = 0;
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * E;
+        int *it = ridx + (size_t)t * K;
+        orc_router(it, rwt + (size_t)t * K, xt, w->gate, w->bias, E, N, K, c->renorm,
+                   c->routed_scale);
+        mmw(zz + (size_t)t * L, xt, w->down, w->wdt, E, L);
+        for (int j = 0; j < K; j++)
+            if (it[j] >= 0 && it[j] < N && !seen[it[j]]) {
+                seen[it[j]] = 1;
+                uniq[nu++] = it[j];
+            }
+    }
+    if (src->getmany) src->getmany(src, w->layer, uniq, nu);
+    for (int u = 0; u < nu; u++) {
+        const int e = uniq[u];
+        OrcExpertQ q;
+        const int ok = src->get(src, w->layer, e, &q) == 0;
+        if (!ok) (*drops)++;
+        for (int t = 0; t < T; t++)
+            for (int j = 0; j < K; j++) {
+                if (ridx[(size_t)t * K + j] != e) continue;
+                float *cb = contrib + ((size_t)t * K + j) * L;
+                if (!ok) {
+                    memset(cb, 0, (size_t)L * sizeof(float));
+                    continue;
+                }
+                expert_q(cb, zz + (size_t)t * L, &q, L, I, c->b1, c->b2, s.gu, s.act);
+            }
+    }
+    for (int t = 0; t < T; t++) {
+        float *acc = zz + (size_t)t * L;
+        const float *wtt = rwt + (size_t)t * K;
+        for (int i = 0; i < L; i++) acc[i] = 0.0f;
+        for (int j = 0; j < K; j++) {
+            const float wj = wtt[j];
+            const float *cb = contrib + ((size_t)t * K + j) * L;
+            for (int i = 0; i < L; i++) acc[i] += wj * cb[i];
+        }
+        moe_tail(out + (size_t)t * E, acc, x + (size_t)t * E, w, c, s.sgu, s.sact, s.sdn);
+    }
+    free(ridx);
+    free(rwt);
+    free(zz);
+    free(contrib);
+    free(uniq);
+    free(seen);
+    free(s.z);
+}
+
+void orc_moe_q(float *out, const float *x, const OrcMoeQW *w, const OrcMoeCfg *c, int T,
+               int *idx, float *wt, int prefill, long *drops)
+{
+    if (!w->src) fatal("orc_moe_q needs a source", 0);
+    /* k3_moe_prefill (k3_ops.c:689-715): the per-token form for T <= 1 or cache-only,
+     * else 64-token chunks, a chunk of one token again per token. */
+    if (!prefill || T <= 1 || w->cache_only) {
+        moe_q_tokens(out, x, w, c, T, idx, wt, drops);
+        return;
+    }
+    for (int t0 = 0; t0 < T; t0 += 64) {
+        const int n = T - t0 < 64 ? T - t0 : 64;
+        float *o = out + (size_t)t0 * c->hidden;
+        const float *xi = x + (size_t)t0 * c->hidden;
+        if (n == 1) moe_q_tokens(o, xi, w, c, 1, idx, wt, drops);
+        else moe_q_chunk(o, xi, w, c, n, drops);
+    }
+}
+
 /* ------------------------------------------------------------ bench helpers ---- */
 uint64_t orc_fnv1a(const float *v, size_t n)
 {

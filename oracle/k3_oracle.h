@@ -73,6 +73,32 @@ typedef struct {
 } OrcMoeW;
 void orc_moe_latent(float *out, const float *x, const OrcMoeW *w, const OrcMoeCfg *c, int T);
 
+/* Expert source with the reference's K3ExpertSrc layout (include/k3/k3.h:332-355), so a
+ * caller can hand the same struct to the oracle and to the library under test. */
+typedef struct OrcExpertSrc {
+    int (*get)(struct OrcExpertSrc *self, int layer, int expert, OrcExpertQ *out);
+    int (*getmany)(struct OrcExpertSrc *self, int layer, const int *experts, int n);
+    int (*resident)(struct OrcExpertSrc *self, int layer, int expert, OrcExpertQ *out);
+    void *ctx;
+} OrcExpertSrc;
+
+/* The LatentMoE weights of the streamed form: router, trunk projections and shared
+ * expert of weight type wdt (0 fp32, 1 bf16), experts from src. */
+typedef struct {
+    const float *gate, *bias, *latent_norm;
+    const void *down, *up, *sh1, *sh3, *sh2;
+    int wdt;
+    OrcExpertSrc *src;
+    int layer, cache_only;
+} OrcMoeQW;
+
+/* k3_moe (prefill 0, k3_ops.c:556-656) or k3_moe_prefill (prefill 1, :689-825) with
+ * MXFP4 experts from w->src, calling get / getmany / resident in the reference's order.
+ * idx/wt (topk each) are written as the reference writes them; *drops is incremented
+ * where the reference increments k3_expert_drops. */
+void orc_moe_q(float *out, const float *x, const OrcMoeQW *w, const OrcMoeCfg *c, int T,
+               int *idx, float *wt, int prefill, long *drops);
+
 /* FNV-1a over the bytes of a float vector (benchmarks/bench_kernels.c:44-52). */
 uint64_t orc_fnv1a(const float *v, size_t n);
 /* The reference benchmark's xorshift32 fillers (benchmarks/bench_kernels.c:54-89). */

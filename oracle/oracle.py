@@ -210,7 +210,7 @@ class Ref(_Checker):
 
     def __init__(self):
         base = os.path.join(HERE, "_ref")
-        self.lib = C.CDLL(os.path.join(base, "libk3ref.so"), mode=C.RTLD_GLOBAL)
+        self.lib = C.CDLL(os.path.join(base, "libk3ref.so"), mode=C.RTLD_LOCAL)
         self.comp = C.CDLL(os.path.join(base, "libk3ref_compose.so"))
         self._bind_common()
         self._ffn = self.comp.ref_expert_ffn
@@ -238,3 +238,162 @@ class Ref(_Checker):
                          _p(None if bias is None else _f32(bias)), qs, hidden, inter, len(bank),
                          topk, renorm, routed_scale, act, b1, b2) == 0
         return out, idx, wt
+
+
+# ------------------------------------------------------- streamed-expert LatentMoE ----
+class ExpertSrc(C.Structure):
+    """The reference's K3ExpertSrc (include/k3/k3.h:332-355); the library under test declares
+    the same layout, so one instance can be handed to the oracle, the compiled reference and
+    the library."""
+
+
+GETFN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(ExpertQ))
+GETMANYFN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.POINTER(C.c_int), C.c_int)
+ExpertSrc._fields_ = [("get", GETFN), ("getmany", GETMANYFN), ("resident", GETFN),
+                      ("ctx", C.c_void_p)]
+
+
+class PySource:
+    """A K3ExpertSrc over host experts. bank: {expert id: object with .t = the six arrays
+    p1, s1, p3, s3, p2, s2}. get() fails for ids in `fail` (and for ids absent from the
+    bank); resident() answers from `resident` (default: the whole bank). Every call is
+    logged in .calls as (name, args)."""
+
+    def __init__(self, bank, fail=(), resident=None, with_getmany=True, with_resident=True):
+        self.bank = bank
+        self.fail = set(fail)
+        self.res = set(bank) if resident is None else set(resident)
+        self.calls = []
+        self._get = GETFN(self._cb_get)
+        self._many = GETMANYFN(self._cb_getmany) if with_getmany else GETMANYFN()
+        self._resf = GETFN(self._cb_resident) if with_resident else GETFN()
+        self.struct = ExpertSrc(self._get, self._many, self._resf, None)
+
+    def _fill(self, e, out):
+        if out:
+            out[0] = ExpertQ(*[a.ctypes.data for a in self.bank[e].t])
+
+    def _cb_get(self, _self, layer, e, out):
+        self.calls.append(("get", layer, e))
+        if e in self.fail or e not in self.bank:
+            return -1
+        self._fill(e, out)
+        return 0
+
+    def _cb_getmany(self, _self, layer, experts, n):
+        self.calls.append(("getmany", layer, tuple(experts[i] for i in range(n))))
+        return sum(1 for i in range(n) if experts[i] in self.bank and experts[i] not in self.fail)
+
+    def _cb_resident(self, _self, layer, e, out):
+        self.calls.append(("resident", layer, e))
+        if e not in self.res or e not in self.bank:
+            return 0
+        self._fill(e, out)
+        return 1
+
+    @property
+    def ptr(self):
+        return C.addressof(self.struct)
+
+
+class RefCfg(C.Structure):
+    """The reference's K3Cfg (include/k3/k3.h:73-120)."""
+    _fields_ = [("hidden", I), ("n_layers", I), ("vocab", I), ("rms_eps", F),
+                ("kda_heads", I), ("kda_head_dim", I), ("conv_k", I), ("gate_lb", F),
+                ("n_heads", I), ("q_lora", I), ("kv_lora", I), ("qk_nope", I), ("qk_rope", I),
+                ("v_head", I), ("mla_out_gate", I), ("n_experts", I), ("topk", I),
+                ("n_shared", I), ("latent", I), ("moe_inter", I), ("routed_scale", F),
+                ("moe_renorm", I), ("latent_norm", I), ("first_dense", I), ("dense_inter", I),
+                ("attn_res_block", I), ("situ_b1", F), ("situ_b2", F), ("n_full_attn", I),
+                ("full_attn", C.c_void_p)]
+
+
+class RefMoeW(C.Structure):
+    """The reference's K3MoeW (include/k3/k3.h:357-380)."""
+    _fields_ = [("gate", P), ("bias", P), ("w1", P), ("w3", P), ("w2", P), ("latent_norm", P),
+                ("down", P), ("up", P), ("sh1", P), ("sh3", P), ("sh2", P), ("wdt", I),
+                ("src", P), ("layer", I), ("cache_only", I)]
+
+
+class _OrcMoeCfg(C.Structure):
+    _fields_ = [(n, I) for n in ("hidden", "latent", "inter", "n_experts", "topk", "n_shared",
+                                "renorm", "latent_norm")] + \
+               [(n, F) for n in ("routed_scale", "rms_eps", "b1", "b2")]
+
+
+class _OrcMoeQW(C.Structure):
+    _fields_ = [("gate", P), ("bias", P), ("latent_norm", P), ("down", P), ("up", P),
+                ("sh1", P), ("sh3", P), ("sh2", P), ("wdt", I), ("src", P), ("layer", I),
+                ("cache_only", I)]
+
+
+def ref_cfg(cfg):
+    """RefCfg from a dict with hidden, latent, inter, n_experts, topk, n_shared, renorm,
+    latent_norm, routed_scale, rms_eps, b1, b2."""
+    c = RefCfg()
+    c.hidden, c.latent, c.moe_inter = cfg["hidden"], cfg["latent"], cfg["inter"]
+    c.n_experts, c.topk, c.n_shared = cfg["n_experts"], cfg["topk"], cfg["n_shared"]
+    c.moe_renorm, c.latent_norm = cfg["renorm"], cfg["latent_norm"]
+    c.routed_scale, c.rms_eps = cfg["routed_scale"], cfg["rms_eps"]
+    c.situ_b1, c.situ_b2 = cfg["b1"], cfg["b2"]
+    return c
+
+
+def ref_moew(W, wdt, src, layer=0, cache_only=0):
+    """RefMoeW over a dict of arrays named gate, bias, latent_norm, down, up, sh1, sh3, sh2."""
+    g = lambda k: W[k].ctypes.data if W.get(k) is not None else None  # noqa: E731
+    return RefMoeW(g("gate"), g("bias"), None, None, None, g("latent_norm"), g("down"), g("up"),
+                   g("sh1"), g("sh3"), g("sh2"), wdt, src.ptr if src is not None else None,
+                   layer, cache_only)
+
+
+def _bind_moe_q(obj):
+    f = obj.lib.orc_moe_q
+    f.restype = None
+    f.argtypes = [P, P, P, P, I, P, P, I, C.POINTER(C.c_long)]
+    return f
+
+
+def oracle_moe_q(orc, x, cfg, W, wdt, src, prefill, layer=0, cache_only=0, idx=None, wt=None):
+    """orc_moe_q: the streamed LatentMoE of the oracle. Returns out, idx, wt, drops (idx/wt
+    start as the given arrays, or -7 / nan, so that untouched entries are visible)."""
+    if not hasattr(orc, "_moe_q"):
+        orc._moe_q = _bind_moe_q(orc)
+    x = _f32(x).reshape(-1, cfg["hidden"])
+    T = x.shape[0]
+    c = _OrcMoeCfg(*[int(cfg[k]) for k in ("hidden", "latent", "inter", "n_experts", "topk",
+                                            "n_shared", "renorm", "latent_norm")],
+                   *[float(cfg[k]) for k in ("routed_scale", "rms_eps", "b1", "b2")])
+    g = lambda k: W[k].ctypes.data if W.get(k) is not None else None  # noqa: E731
+    w = _OrcMoeQW(g("gate"), g("bias"), g("latent_norm"), g("down"), g("up"), g("sh1"), g("sh3"),
+                  g("sh2"), wdt, src.ptr, layer, cache_only)
+    out = np.empty_like(x)
+    K = cfg["topk"]
+    idx = np.full(K, -7, np.int32) if idx is None else np.array(idx, np.int32)
+    wt = np.full(K, np.nan, np.float32) if wt is None else np.array(wt, np.float32)
+    drops = C.c_long(0)
+    orc._moe_q(_p(out), _p(x), C.byref(w), C.byref(c), T, _p(idx), _p(wt), prefill,
+               C.byref(drops))
+    return out, idx, wt, drops.value
+
+
+def ref_moe_q(ref, x, cfg, W, wdt, src, prefill, layer=0, cache_only=0, idx=None, wt=None):
+    """The compiled reference's own k3_moe / k3_moe_prefill on the same inputs."""
+    L = ref.lib
+    fn = L.k3_moe_prefill if prefill else L.k3_moe
+    fn.restype = None
+    fn.argtypes = [P, P, C.POINTER(RefMoeW), C.POINTER(RefCfg), I, P, P, P]
+    L.k3_moe_scratch.restype = C.c_size_t
+    L.k3_moe_scratch.argtypes = [C.POINTER(RefCfg)]
+    c = ref_cfg(cfg)
+    w = ref_moew(W, wdt, src, layer, cache_only)
+    x = _f32(x).reshape(-1, cfg["hidden"])
+    out = np.empty_like(x)
+    K = cfg["topk"]
+    idx = np.full(K, -7, np.int32) if idx is None else np.array(idx, np.int32)
+    wt = np.full(K, np.nan, np.float32) if wt is None else np.array(wt, np.float32)
+    scratch = np.empty(L.k3_moe_scratch(C.byref(c)), np.float32)
+    drops = C.c_long.in_dll(L, "k3_expert_drops")
+    d0 = drops.value
+    fn(_p(out), _p(x), C.byref(w), C.byref(c), x.shape[0], _p(idx), _p(wt), _p(scratch))
+    return out, idx, wt, drops.value - d0
