@@ -105,6 +105,23 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T,
                    int act, float b1, float b2, int prec, void *ws, size_t ws_bytes,
                    int *perm_out, int *offsets_out, int *drops_out, void *stream);
 
+/* k3d_moe_routed with no workspace argument and no allocation, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The scratch lives in a static device array
+ * of K3D_STATIC_WS_BYTES (40 MiB) that each GPU holds until the process ends: enough for
+ * decode batches of up to 64 tokens at hidden 7168 / inter 2048 / 384 experts / top-8 or
+ * at 3584 / 3072 / 896 / top-16 (k3d_moe_ws of the call must not exceed it; larger calls
+ * return an error). k3d_init must have run on the device first (it looks the array up and
+ * makes the one-time uploads). All calls on one GPU share the array: calls that overlap
+ * on one GPU race. Otherwise identical to k3d_moe_routed, results bit for bit. */
+#define K3D_STATIC_WS_BYTES ((size_t)40 << 20)
+size_t k3d_static_ws_bytes(void);
+int k3d_moe_routed_static(float *out, int *idx, float *wt, const float *x, int T,
+                          const float *router_w, const float *bias, const void *bank, int layout,
+                          int hidden, int inter, int n_experts, int topk, int renorm,
+                          float routed_scale, int act, float b1, float b2, int prec, int *perm_out,
+                          int *offsets_out, int *drops_out, void *stream);
+
 /* The always-on dense shared expert with bf16 weights, on the matrix cores:
  *   s[t] = W2 . act(W1 x[t], W3 x[t]),  W1, W3 [inter][hidden], W2 [hidden][inter] bf16,
  * y = s (accumulate 0) or y += s (accumulate 1, after the routed sum: the order of the

@@ -31,6 +31,8 @@ static int bad(const char *what)
 
 const char *k3d_error(void) { return g_msg; }
 
+int k3dx_bad(const char *msg) { return bad(msg); }
+
 static int exc_table(const K3kExc **out);
 
 /* Device selection and the one-time uploads (router tables), so that no later entry point
@@ -38,6 +40,8 @@ static int exc_table(const K3kExc **out);
 int k3d_init(void)
 {
     if (k3k_init()) return fail("init");
+    if (k3k_side_init()) return fail("init: side stream");
+    if (k3s_static_setup()) return fail("init: static workspace");
     const K3kExc *e;
     return exc_table(&e);
 }

@@ -152,7 +152,9 @@ extern "C" int k3k_stream_destroy(void *stream)
 static hipStream_t g_side = nullptr;
 static hipEvent_t g_fork = nullptr, g_join = nullptr;
 
-extern "C" int k3k_fork(void *stream, void **side)
+/* Creates the side stream and its events (once); k3d_init calls it so that no later entry
+ * point creates anything. */
+extern "C" int k3k_side_init(void)
 {
     if (k3k_init()) return -1;
     if (!g_side) {
@@ -162,6 +164,12 @@ extern "C" int k3k_fork(void *stream, void **side)
         if (e == hipSuccess) e = hipEventCreateWithFlags(&g_join, hipEventDisableTiming);
         if (e != hipSuccess) return k3k_fail("fork: hipEventCreate", e);
     }
+    return 0;
+}
+
+extern "C" int k3k_fork(void *stream, void **side)
+{
+    if (k3k_side_init()) return -1;
     hipError_t e = hipEventRecord(g_fork, (hipStream_t)stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(g_side, g_fork, 0);
     if (e != hipSuccess) return k3k_fail("fork", e);

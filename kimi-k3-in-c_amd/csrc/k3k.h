@@ -34,6 +34,7 @@ int k3k_cu_count(void);
 /* Graph capture of the work enqueued on `stream` (a created stream, not NULL). */
 /* k3k_fork: *side = a second stream that first waits for the work queued on stream;
  * k3k_join: stream waits for the work queued on the side stream since. */
+int k3k_side_init(void);
 int k3k_fork(void *stream, void **side);
 int k3k_join(void *stream);
 int k3k_graph_begin(void *stream);
@@ -219,6 +220,13 @@ int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int rows, float
                 void *stream);
 int k3k_axpy_rows(float *out, const float *add, size_t n, void *stream); /* out += add */
 int k3k_scale(float *out, const float *in, float s, size_t n, void *stream);
+
+/* ---- the allocation-free workspace (k3_static.hip) --------------------------------- */
+/* Looks up, once per device, the device address of the library's static workspace for the
+ * current device (called by k3d_init). */
+int k3s_static_setup(void);
+/* Error text for a k3d_* entry point implemented outside k3_devapi.c; returns -2. */
+int k3dx_bad(const char *msg);
 
 #ifdef __cplusplus
 }

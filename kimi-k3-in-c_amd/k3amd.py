@@ -136,6 +136,9 @@ def _declare(L):
     d("k3d_moe_ws", SZ, I, I, I, I, I, I)
     d("k3d_moe_routed", I, P, P, P, P, I, P, P, P, I, I, I, I, I, I, F, I, F, F, I, P, SZ, P, P,
       P, P)
+    d("k3d_static_ws_bytes", SZ)
+    d("k3d_moe_routed_static", I, P, P, P, P, I, P, P, P, I, I, I, I, I, I, F, I, F, F, I, P, P, P,
+      P)
     d("k3d_moe_experts", I, P, P, P, P, I, P, I, I, I, I, I, I, F, F, I, P, SZ, P, P, P, P)
     d("k3d_shared_ws", SZ, I, I, I, I)
     d("k3d_shared_expert", I, P, I, P, I, P, P, P, I, I, I, F, F, I, P, SZ, P)
