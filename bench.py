@@ -249,9 +249,39 @@ def time_skewed(layer, T=512, steps=5, warmup=1):
             "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st.items()}}
 
 
+def time_back_to_back(launch, ncalls, per_graph=64, reps=8):
+    """Wall-clock microseconds per call of `launch(i, stream)` run back to back: per_graph
+    consecutive calls captured in one HIP graph, the graph replayed reps times (calls
+    i = 0, 1, ... across the whole run, ncalls distinct), no events between launches."""
+    L = k3amd.lib()
+    stream = L.k3d_stream_create()
+    ngraph = max(1, ncalls // per_graph)
+    graphs = []
+    for g in range(ngraph):
+        k3amd.check(L.k3d_graph_begin(stream), "k3d_graph_begin")
+        for c in range(per_graph):
+            launch(g * per_graph + c, stream)
+        ex = C.c_void_p()
+        k3amd.check(L.k3d_graph_end(stream, C.byref(ex)), "k3d_graph_end")
+        graphs.append(ex)
+    for g in graphs:
+        k3amd.check(L.k3d_graph_launch(g, stream), "k3d_graph_launch")
+    k3amd.check(L.k3d_sync(stream))
+    t0 = time.perf_counter()
+    for r in range(reps):
+        k3amd.check(L.k3d_graph_launch(graphs[r % ngraph], stream), "k3d_graph_launch")
+    k3amd.check(L.k3d_sync(stream))
+    t1 = time.perf_counter()
+    for g in graphs:
+        L.k3d_graph_destroy(g)
+    L.k3d_stream_destroy(stream)
+    return (t1 - t0) / (reps * per_graph) * 1e6
+
+
 def time_gemv(steps=200, copies=128):
     """2048x7168 MXFP4 GEMV, one token, rotating over `copies` distinct weight copies
-    (>= 1 GB, well past the last-level cache) so every launch streams from HBM."""
+    (>= 1 GB, well past the last-level cache) so every launch streams from HBM. Kernel time
+    from HIP events around each launch; throughput from back-to-back launches in a graph."""
     L = k3amd.lib()
     packed, scales, x = wl.gemv_inputs()
     rows, inn = packed.shape[0], packed.shape[1] * 2
@@ -267,20 +297,19 @@ def time_gemv(steps=200, copies=128):
     dy = k3amd.DevBuf(rows * 4)
     ws = k3amd.DevBuf(L.k3d_matmul_mxfp4_ws(1, inn))
 
-    def launch(c):
+    def launch(c, stream=None):
         base = w.ptr + (c % copies) * stride
         k3amd.check(L.k3d_matmul_mxfp4(dy.ptr, dx.ptr, 1, base, base + pk_b, inn, rows, 0, ws.ptr,
-                                       ws.nbytes, None), "k3d_matmul_mxfp4")
+                                       ws.nbytes, stream), "k3d_matmul_mxfp4")
     for c in range(20):
         launch(c)
     k3amd.check(L.k3d_sync(None))
     prof = k3amd.Profile(max_marks=4 * steps + 16)
-    t0 = time.perf_counter()
     for c in range(steps):
         launch(c)
     k3amd.check(L.k3d_sync(None))
-    t1 = time.perf_counter()
     st = prof.end()
+    b2b = time_back_to_back(launch, copies)
     for b in (w, dx, dy, ws):
         b.free()
     algo = pk_b + sc_b + inn * 4 + rows * 4        # weights + x + y: 7,835,648 B
@@ -289,8 +318,47 @@ def time_gemv(steps=200, copies=128):
     return {"shape": [rows, inn], "copies_rotated": copies, "algorithmic_bytes": algo,
             "kernel_us": round(kern_ms * 1e3, 3),
             "kernel_GBps": round(algo / (kern_ms * 1e-3) / 1e9, 1),
-            "launch_rate_us": round((t1 - t0) / steps * 1e6, 3),
-            "frac_of_peak": round(algo / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            "frac_of_peak": round(algo / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "back_to_back_us": round(b2b, 3),
+            "back_to_back_frac_of_peak": round(algo / (b2b * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+
+
+def time_trunk_gemv(rows=12288, inn=7168, copies=4, steps=40):
+    """The bf16 trunk GEMV of the reference's kernel benchmark (KDA q-projection, 7168 ->
+    12288, benchmarks/bench_kernels.c:102-127) through k3d_matmul_bf16, one token, over
+    `copies` weight copies (704 MB, past the 256 MB last-level cache)."""
+    L = k3amd.lib()
+    Wb = k3amd.gen_bf16_normal(rows * inn, wl.stream("trunk.w"), 0.0, 0.02)
+    x = k3amd.gen_normal(inn, wl.stream("trunk.x"))
+    stride = (Wb.nbytes + 4095) // 4096 * 4096
+    w = k3amd.DevBuf(copies * stride)
+    for c in range(copies):
+        w.upload(Wb, c * stride)
+    dx = k3amd.DevBuf(inn * 4).upload(x)
+    dy = k3amd.DevBuf(rows * 4)
+
+    def launch(c, stream=None):
+        k3amd.check(L.k3d_matmul_bf16(dy.ptr, dx.ptr, 1, w.ptr + (c % copies) * stride, inn, rows,
+                                      stream), "k3d_matmul_bf16")
+    for c in range(8):
+        launch(c)
+    k3amd.check(L.k3d_sync(None))
+    prof = k3amd.Profile(max_marks=4 * steps + 16)
+    for c in range(steps):
+        launch(c)
+    k3amd.check(L.k3d_sync(None))
+    st = prof.end()
+    b2b = time_back_to_back(launch, 4 * copies, per_graph=16)
+    for b in (w, dx, dy):
+        b.free()
+    algo = rows * inn * 2 + inn * 4 + rows * 4
+    ms, n = st.get("gemv", (0.0, 0))
+    kern_ms = ms / max(n, 1)
+    return {"shape": [rows, inn], "copies_rotated": copies, "algorithmic_bytes": algo,
+            "kernel_us": round(kern_ms * 1e3, 3),
+            "kernel_GBps": round(algo / (kern_ms * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(algo / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "back_to_back_us": round(b2b, 3)}
 
 
 def cpu_baseline(T_sample=8, budget_s=10.0):
@@ -424,6 +492,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--only", nargs="+", default=None,
+                    help="time only these workloads (decode64 batch1 gemv trunk ffn prefill "
+                         "skewed) and print their figures instead of the benchmark line")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (calibrates the HBM "
                          "byte counters of a profiler run) and exit")
@@ -438,6 +509,37 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build does not shard the layer across GPUs)", file=sys.stderr)
         sys.exit(2)
+
+    if args.only:
+        # a subset of the extra workloads, for kernel work: one JSON object, not the line
+        res = {}
+        need_layer = {"decode64", "batch1", "ffn", "prefill", "skewed"} & set(args.only)
+        layer = Layer() if need_layer else None
+        for name in args.only:
+            if name == "decode64":
+                secs, st, u, _ = time_layer(layer, 64, args.steps, args.warmup)
+                res[name] = {"ms_per_step": round(secs / args.steps * 1e3, 4), "unique": u,
+                             "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st.items()}}
+            elif name == "batch1":
+                n = max(args.steps * 5, 50)
+                secs, st, u, _ = time_layer(layer, 1, n, args.warmup)
+                res[name] = {"ms_per_step": round(secs / n * 1e3, 4),
+                             "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st.items()}}
+            elif name == "gemv":
+                res[name] = time_gemv()
+            elif name == "trunk":
+                res[name] = time_trunk_gemv()
+            elif name == "ffn":
+                res[name] = time_expert_ffn(layer)
+            elif name == "prefill":
+                res[name] = time_prefill(layer)
+            elif name == "skewed":
+                res[name] = time_skewed(layer)
+            else:
+                raise SystemExit(f"unknown section {name}")
+            log(f"bench: {name} {res[name]}")
+        print(json.dumps(res), flush=True)
+        return
 
     cb = None if args.no_cpu else cpu_baseline_children()    # before any GPU call
     layer = Layer()
@@ -459,13 +561,14 @@ def main():
     log(f"bench: batch-1 layer {b1_ms:.3f} ms/step")
     gemv = time_gemv()
     log(f"bench: gemv {gemv}")
+    trunk = time_trunk_gemv()
+    log(f"bench: trunk gemv {trunk}")
     ffn = time_expert_ffn(layer)
     log(f"bench: expert ffn {ffn}")
     prefill = time_prefill(layer)
     log(f"bench: prefill {prefill}")
     skewed = time_skewed(layer)
     log(f"bench: skewed {skewed}")
-
     line = {
         "metric": "MoE-layer tokens/s + achieved HBM GB/s (MXFP4 expert GEMV), batch 1 & 64",
         "value": round(tok_s, 1),
@@ -495,6 +598,7 @@ def main():
                    "layer_GBps": round(b1_bytes / (b1_ms * 1e-3) / 1e9, 1),
                    "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st1.items()}},
         "gemv_2048x7168": gemv,
+        "trunk_gemv_bf16_12288x7168": trunk,
         "expert_ffn_decode": ffn,
         "prefill_4096": prefill,
         "skewed_512_shared": skewed,

@@ -206,13 +206,19 @@ int k3d_matmul_mxfp4(float *y, const float *x, int ntok, const uint8_t *packed,
 
 int k3d_matmul_f32(float *y, const float *x, int ntok, const float *W, int in, int out, void *stream)
 {
-    return k3k_gemv_f32(y, x, W, in, out, ntok, out, stream) ? fail("gemv_f32") : 0;
+    k3k_prof_mark(stream, K3D_STAGE_BEGIN);
+    if (k3k_gemv_f32(y, x, W, in, out, ntok, out, stream)) return fail("gemv_f32");
+    k3k_prof_mark(stream, K3D_STAGE_GEMV);
+    return 0;
 }
 
 int k3d_matmul_bf16(float *y, const float *x, int ntok, const uint16_t *W, int in, int out,
                     void *stream)
 {
-    return k3k_gemv_bf16(y, x, W, in, out, ntok, out, stream) ? fail("gemv_bf16") : 0;
+    k3k_prof_mark(stream, K3D_STAGE_BEGIN);
+    if (k3k_gemv_bf16(y, x, W, in, out, ntok, out, stream)) return fail("gemv_bf16");
+    k3k_prof_mark(stream, K3D_STAGE_GEMV);
+    return 0;
 }
 
 /* ---- router -------------------------------------------------------------------------- */

@@ -1,0 +1,72 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Dense bf16 / fp32 GEMV and GEMM (the trunk projections and the dense shared expert)
+through the C ABI against the oracle's k3_matmul_bf16 / k3_matmul restatement (fp64
+accumulation, src/core/k3_ops.c:265-291, 1108-1213 of the reference):
+max|err| <= 1e-4 ||ref||inf for fp32 activations; k3_matmul_bf16 bit-identical to
+k3_matmul on the widened weights for one token (the reference's own invariant,
+tests/unit/test_ops.c:811-848)."""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import max_err_rel_inf
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def dev_matmul(gpu, X, W, bf16=True):
+    L = gpu.lib()
+    X = np.ascontiguousarray(X, np.float32)
+    T, inn = X.shape
+    out = W.shape[0]
+    bufs = [gpu.DevBuf(X.nbytes).upload(X), gpu.DevBuf(W.nbytes).upload(W), gpu.DevBuf(T * out * 4)]
+    try:
+        dx, dw, dy = bufs
+        fn = L.k3d_matmul_bf16 if bf16 else L.k3d_matmul_f32
+        gpu.check(fn(dy.ptr, dx.ptr, T, dw.ptr, inn, out, None), "k3d_matmul")
+        gpu.check(L.k3d_sync(None))
+        return dy.download(np.empty((T, out), np.float32))
+    finally:
+        for b in bufs:
+            b.free()
+
+
+def test_trunk_gemv_bench_shape(gpu, orc, k3):
+    """The reference benchmark's bf16 GEMV (KDA q-projection 7168 -> 12288) with its own
+    inputs: within tolerance of the oracle, whose output hashes to the reference's."""
+    say("case: bf16 gemv 12288x7168, bench inputs")
+    W = orc.fill_bf16(7168 * 12288, 12345).reshape(12288, 7168)
+    x = orc.fill_f(7168, 999)
+    want = orc.matmul_bf16(x, W)
+    assert orc.fnv1a(want) == 0x83C8504A4CB3FAC6
+    assert max_err_rel_inf(gpu.matmul_bf16(x, W), want) <= TOL
+    assert max_err_rel_inf(dev_matmul(gpu, x[None], W)[0], want) <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8, 17])
+@pytest.mark.parametrize("shape", [(3584, 7168), (7168, 6144), (100, 264), (257, 72)])
+def test_dense_matmul_tokens(gpu, orc, k3, T, shape):
+    out, inn = shape
+    say(f"case: bf16/f32 matmul {out}x{inn} T={T}")
+    Wb = k3.gen_bf16_normal(inn * out, 71 + T, 0.0, 0.02).reshape(out, inn)
+    X = k3.gen_normal(T * inn, 72 + T).reshape(T, inn)
+    Y = dev_matmul(gpu, X, Wb)
+    Wf = (Wb.astype(np.uint32) << 16).view(np.float32)
+    Yf = dev_matmul(gpu, X, Wf, bf16=False)
+    for t in range(T):
+        want = orc.matmul_bf16(X[t], Wb)
+        assert max_err_rel_inf(Y[t], want) <= TOL, t
+        assert max_err_rel_inf(Yf[t], want) <= TOL, t
+    if T == 1:
+        assert np.array_equal(bits(Y), bits(Yf))
