@@ -126,11 +126,11 @@ int k3d_moe_routed_static(float *out, int *idx, float *wt, const float *x, int T
  *   s[t] = W2 . act(W1 x[t], W3 x[t]),  W1, W3 [inter][hidden], W2 [hidden][inter] bf16,
  * y = s (accumulate 0) or y += s (accumulate 1, after the routed sum: the order of the
  * reference's shared tail, k3_ops.c:650-654). The reference computes each product with
- * k3_matmul_bf16 (fp64 accumulation); here fp32 MFMA accumulation (rocBLAS bf16 GEMMs)
- * with the activations as two bf16 terms (prec 0, max|err| <= 1e-4 ||ref||inf) or one
- * (prec 1, 2e-2 relative). hidden and inter must be multiples of 512. The BLAS library
- * initialises on its first call, so make one eager call before capturing this in a HIP
- * graph; calls from several threads serialise on the library's one BLAS handle. */
+ * k3_matmul_bf16 (fp64 accumulation); here fp32 MFMA accumulation in the library's own
+ * bf16 GEMM kernels (gate and up in one pass with the activation in the epilogue, then
+ * down) with the activations as two bf16 terms (prec 0, max|err| <= 1e-4 ||ref||inf) or
+ * one (prec 1, 2e-2 relative). hidden and inter must be multiples of 64. Nothing is
+ * allocated and no library is initialised, so the call can be captured in a HIP graph. */
 size_t k3d_shared_ws(int T, int hidden, int inter, int prec);
 int k3d_shared_expert(float *y, int accumulate, const float *x, int T, const uint16_t *w1,
                       const uint16_t *w3, const uint16_t *w2, int hidden, int inter, int act,

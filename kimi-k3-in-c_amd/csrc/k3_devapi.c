@@ -642,13 +642,12 @@ int k3d_mxfp4_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
 }
 
 /* ---- dense (bf16) shared expert ------------------------------------------------------------
- * Plain dense GEMMs (rocBLAS, bf16 in, fp32 accumulation): gate and up into the halves of one
- * [T][2 inter] fp32 buffer, act + bf16 split in one elementwise kernel, then down. Two-term
- * activations (prec 0) add the lo term's product as a second GEMM with beta 1. The
- * accumulating form adds the finished output onto y with one fp32 add per element. */
+ * Two launches of the dense GEMM kernel (k3_gemm.hip) after the activation split: gate and up
+ * in one pass over x with the activation and its bf16 split in the epilogue, then down,
+ * written or added onto y (one fp32 add of the finished sum, the reference's
+ * `ot[i] += sdn[i]`, k3_ops.c:654). */
 typedef struct {
     uint16_t *xhi, *xlo, *ahi, *alo;
-    float *gu, *tmp;
 } ShWs;
 
 static size_t shared_layout(Carve *c, ShWs *w, int T, int hidden, int inter, int prec)
@@ -657,8 +656,6 @@ static size_t shared_layout(Carve *c, ShWs *w, int T, int hidden, int inter, int
     w->xlo = prec == 0 ? (uint16_t *)take(c, (size_t)T * hidden * 2) : NULL;
     w->ahi = (uint16_t *)take(c, (size_t)T * inter * 2);
     w->alo = prec == 0 ? (uint16_t *)take(c, (size_t)T * inter * 2) : NULL;
-    w->gu = (float *)take(c, (size_t)T * 2 * inter * 4);
-    w->tmp = (float *)take(c, (size_t)T * hidden * 4);
     return c->off;
 }
 
@@ -674,27 +671,17 @@ int k3d_shared_expert(float *y, int accumulate, const float *x, int T, const uin
                       float b1, float b2, int prec, void *ws, size_t ws_bytes, void *stream)
 {
     if (T <= 0) return 0;
-    if (hidden % 512 || inter % 512) return bad("k3d_shared_expert: hidden and inter must be multiples of 512");
+    if (hidden % 64 || inter % 64) return bad("k3d_shared_expert: hidden and inter must be multiples of 64");
     if (!w1 || !w3 || !w2) return bad("k3d_shared_expert: missing weights");
     if (ws_bytes < k3d_shared_ws(T, hidden, inter, prec)) return bad("k3d_shared_expert: workspace too small");
     Carve c = {(char *)ws, 0};
     ShWs w;
     shared_layout(&c, &w, T, hidden, inter, prec);
-    const int ld = 2 * inter;
     if (k3k_split_bf16(w.xhi, w.xlo, x, (size_t)T * hidden, stream)) return fail("split");
-    if (k3k_gemm_bf16_nt(w.gu, ld, w1, w.xhi, inter, T, hidden, 0.0f, stream) ||
-        k3k_gemm_bf16_nt(w.gu + inter, ld, w3, w.xhi, inter, T, hidden, 0.0f, stream))
+    if (k3k_dense_gateup(w.ahi, w.alo, w1, w3, w.xhi, w.xlo, inter, T, hidden, act, b1, b2, stream))
         return fail("shared gate/up");
-    if (prec == 0 && (k3k_gemm_bf16_nt(w.gu, ld, w1, w.xlo, inter, T, hidden, 1.0f, stream) ||
-                      k3k_gemm_bf16_nt(w.gu + inter, ld, w3, w.xlo, inter, T, hidden, 1.0f, stream)))
-        return fail("shared gate/up (lo)");
-    if (k3k_act_split(w.ahi, w.alo, w.gu, inter, T, act, b1, b2, stream)) return fail("shared act");
-    float *dst = accumulate ? w.tmp : y;
-    if (k3k_gemm_bf16_nt(dst, hidden, w2, w.ahi, hidden, T, inter, 0.0f, stream))
+    if (k3k_dense_gemm(y, hidden, accumulate, w2, w.ahi, w.alo, hidden, T, inter, stream))
         return fail("shared down");
-    if (prec == 0 && k3k_gemm_bf16_nt(dst, hidden, w2, w.alo, hidden, T, inter, 1.0f, stream))
-        return fail("shared down (lo)");
-    if (accumulate && k3k_axpy_rows(y, w.tmp, (size_t)T * hidden, stream)) return fail("shared add");
     k3k_prof_mark(stream, K3D_STAGE_SHARED);
     return 0;
 }

@@ -94,7 +94,7 @@ static void check(int rc, const char *what)
 
 /* Reusable device buffers, one per role, grown on demand. */
 enum { B_X, B_Y, B_P, B_S, B_WS, B_BIAS, B_RW, B_IDX, B_WT, B_ARENA, B_BANK, B_Z, B_ACC,
-       B_SGU, B_SDN, B_OUT, B_W2, B_W3, B_T0, B_T1, B_T2, B_COUNT };
+       B_SGU, B_SDN, B_OUT, B_W2, B_W3, B_T0, B_T1, B_T2, B_XS, B_COUNT };
 static void *g_buf[B_COUNT];
 static size_t g_cap[B_COUNT];
 
@@ -567,13 +567,21 @@ static size_t wbytes(int wdt, int in, int out)
     return (size_t)in * out * 4;
 }
 
-/* y[t*ldy + o] = W x[t] for a tagged weight matrix (k3_mmw, reference k3.h:289-295). */
+/* y[t*ldy + o] = W x[t] for a tagged weight matrix (k3_mmw, reference k3.h:289-295). Up to
+ * four tokens stream the weights through the vector-unit GEMV; more bf16 tokens go to the
+ * matrix-core GEMM with the activations split into two bf16 terms (fp32-accurate). */
 static void mmw_dev(float *y_d, const float *x_d, int ntok, const void *W, int wdt, int in, int out,
                     int ldy, int slot)
 {
     const void *dw = weights(slot, W, wbytes(wdt, in, out));
     int rc;
-    if (wdt == K3_WBF16) rc = k3k_gemv_bf16(y_d, x_d, (const uint16_t *)dw, in, out, ntok, ldy, g_stream);
+    if (wdt == K3_WBF16 && ntok > 4 && in % 64 == 0 &&
+        (unsigned long long)out * in * 2 < 0x80000000ull && (unsigned long long)ntok * in * 2 < 0x80000000ull) {
+        uint16_t *xs = (uint16_t *)buf(B_XS, (size_t)ntok * in * 4);
+        uint16_t *xl = xs + (size_t)ntok * in;
+        check(k3k_split_bf16(xs, xl, x_d, (size_t)ntok * in, g_stream), "activation split");
+        rc = k3k_dense_gemm(y_d, ldy, 0, (const uint16_t *)dw, xs, xl, out, ntok, in, g_stream);
+    } else if (wdt == K3_WBF16) rc = k3k_gemv_bf16(y_d, x_d, (const uint16_t *)dw, in, out, ntok, ldy, g_stream);
     else if (wdt == K3_WI8) rc = k3k_gemv_q8(y_d, x_d, dw, in, out, ntok, ldy, g_stream);
     else rc = k3k_gemv_f32(y_d, x_d, (const float *)dw, in, out, ntok, ldy, g_stream);
     check(rc, "k3_mmw");

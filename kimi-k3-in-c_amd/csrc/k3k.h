@@ -211,11 +211,17 @@ int k3k_act(float *y, const float *gu, int n, int rows, int act, float b1, float
 int k3k_act_split(uint16_t *hi, uint16_t *lo, const float *gu, int n, int rows, int act,
                   float b1, float b2, void *stream);
 
-/* ---- plain dense GEMM (rocBLAS) ---------------------------------------------------- */
-/* y[t][r] = beta * y[t][r] + sum_k W[r][k] * x[t][k], t < T, r < R (row stride ldy): W bf16
- * [R][K], x bf16 [T][K], fp32 accumulation and output. The dense shared expert's products. */
-int k3k_gemm_bf16_nt(float *y, int ldy, const uint16_t *W, const uint16_t *x, int R, int T,
-                     int K, float beta, void *stream);
+/* ---- dense bf16 GEMM on the matrix cores (k3_gemm.hip) ------------------------------ */
+/* y[t][r] (= or, accumulate, +=) sum_k W[r][k] * (xhi + xlo)[t][k], t < T, r < R, row stride
+ * ldy: W bf16 [R][K], activations as bf16 terms [T][K] (xlo NULL: one term), K % 64 == 0,
+ * operands under 2 GiB. fp32 accumulation and output. */
+int k3k_dense_gemm(float *y, int ldy, int accumulate, const uint16_t *W, const uint16_t *xhi,
+                   const uint16_t *xlo, int R, int T, int K, void *stream);
+/* The dense SwiGLU's first half: act(W_gate x, W_up x) for rows r < R of both [R][K]
+ * matrices, written as bf16 terms ahi (and alo when not NULL) [T][R]. */
+int k3k_dense_gateup(uint16_t *ahi, uint16_t *alo, const uint16_t *wg, const uint16_t *wu,
+                     const uint16_t *xhi, const uint16_t *xlo, int R, int T, int K, int act,
+                     float b1, float b2, void *stream);
 int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int rows, float eps,
                 void *stream);
 int k3k_axpy_rows(float *out, const float *add, size_t n, void *stream); /* out += add */

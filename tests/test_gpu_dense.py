@@ -70,3 +70,24 @@ def test_dense_matmul_tokens(gpu, orc, k3, T, shape):
         assert max_err_rel_inf(Yf[t], want) <= TOL, t
     if T == 1:
         assert np.array_equal(bits(Y), bits(Yf))
+
+
+@pytest.mark.parametrize("T,prec", [(512, 1), (512, 0), (77, 0), (130, 1)])
+def test_shared_expert_config4_shape(gpu, orc, wl, T, prec):
+    """The dense SwiGLU shared expert at 7168 -> 2048 -> 7168 on the matrix cores, added
+    onto an existing output (the reference's ot[i] += sdn[i]): sampled tokens against the
+    oracle's bf16 composition (k3_matmul_bf16, SiLU-GLU, k3_matmul_bf16)."""
+    say(f"case: shared expert 7168/2048 T={T} prec={prec}")
+    E, I = 7168, 2048
+    w1, w3, w2 = wl.shared_expert_weights()
+    X = wl.tokens(T, tag=f"dense.shared.{T}")
+    y0 = wl.tokens(T, tag=f"dense.shared.y0.{T}") * 0.5
+    got = gpu.shared_expert_device(X, w1, w3, w2, E, I, prec=prec, y0=y0)
+    tol = TOL if prec == 0 else 2e-2
+    for t in np.random.default_rng(T).choice(T, min(T, 12), replace=False):
+        g = orc.matmul_bf16(X[t], w1.reshape(I, E))
+        u = orc.matmul_bf16(X[t], w3.reshape(I, E))
+        s = orc.matmul_bf16(orc.silu_glu(np.concatenate([g, u]), I), w2.reshape(E, I))
+        want = y0[t] + s
+        assert max_err_rel_inf(got[t], want) <= tol, t
+        assert max_err_rel_inf(got[t] - y0[t], s) <= (tol if prec == 0 else 2e-2), t
