@@ -143,6 +143,18 @@ __device__ __forceinline__ uint32_t k3_bload4(k3_rsrc r, uint32_t off)
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL);
 }
 
+/* 16 bytes per lane from a buffer straight into LDS (buffer_load_dwordx4 ... lds): lane L
+ * writes lds_row + 16 L, where lds_row is wave-uniform; counts against vmcnt. The builtin
+ * exists only for the device pass (in the host pass it would drop the kernel's stub). */
+__device__ __forceinline__ void k3_dma16(k3_rsrc r, void *lds_row, uint32_t voff, uint32_t soff)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_row, 16, voff, soff, 0, 0);
+#else
+    (void)r; (void)lds_row; (void)voff; (void)soff;
+#endif
+}
+
 __device__ __forceinline__ k3_bf16x8 k3_as_bf16x8(uint4 v)
 {
     return __builtin_bit_cast(k3_bf16x8, v);
@@ -166,6 +178,18 @@ __device__ __forceinline__ float k3_act_pair(float g, float u, int act, float b1
     const float a = b1 * tanhf(g / b1) * k3_sigmoid_dev(g);
     const float v = b2 * tanhf(u / b2);
     return a * v;
+}
+
+/* The same activations for the bf16 prefill path, whose result is rounded to bf16: exp
+ * through the hardware exp2 (__expf) and tanh(y) = 1 - 2 / (e^(2y) + 1), a relative error
+ * near 1e-6 (far below bf16's 2^-8) and few registers. */
+__device__ __forceinline__ float k3_act_pair_fast(float g, float u, int act, float b1, float b2)
+{
+    const float sg = __fdividef(1.0f, 1.0f + __expf(-g));
+    if (act == 1) return g * sg * u;
+    const float tg = 1.0f - __fdividef(2.0f, __expf(2.0f * (g / b1)) + 1.0f);
+    const float tu = 1.0f - __fdividef(2.0f, __expf(2.0f * (u / b2)) + 1.0f);
+    return (b1 * tg * sg) * (b2 * tu);
 }
 
 #endif

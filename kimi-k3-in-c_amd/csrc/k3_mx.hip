@@ -1151,23 +1151,62 @@ int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
 
 /* ---- prefill: large token passes, one-term activations --------------------------------
  * mx_prefill_kernel: GATEUP / DOWN for passes of up to 16*NB tokens with the activations
- * as single bf16 terms (the prefill precision), weights tiled MXFP4. Same item = (pass, row block) and K order as mx_moe_kernel, but K is staged
- * 128 * SPC columns at a time so that the pass's tokens fit in LDS: each expert's weights
- * are streamed once per pass of up to 16*NB tokens, and every dequantized weight fragment
- * feeds MT x NB MFMAs. Stage c covers steps c SPC .. c SPC + SPC - 1 (128 columns each).
- * Activation loads are unconditional (rows clamped to a valid token); only the LDS stores
- * are masked. Weight loads keep the default cache policy: an expert with several passes
- * re-reads its weights, and the caches then serve part of them. NW waves share one staged
- * copy of the pass's activations. */
-template <int MODE, int MT, int NB, int LAYOUT, int SPC = 2, int NW = 4>
+ * as single bf16 terms (the prefill precision), weights in the tiled MXFP4 layout. An item
+ * is (pass, row block); a wave owns MT tiles of 16 weight rows and all the pass's tokens,
+ * so every dequantized weight fragment feeds NB MFMAs and each weight byte is read once per
+ * pass. K is staged 128 * SPC columns at a time: the pass's activations for a stage are
+ * copied into LDS by the buffer unit (buffer_load ... lds: no registers, no LDS store
+ * instructions), double-buffered with one barrier per stage, and shared by the NW waves.
+ *
+ * LDS layout of a stage buffer: 16-byte slots, token p's column piece o (8 bf16) at slot
+ * p * (PR + 1) + o: rows padded by one slot, so the 16 tokens of a fragment read start 4
+ * banks apart and cover all 64 banks. A DMA instruction fills 64 consecutive slots (lane L
+ * the L-th), so each lane loads the piece that its slot holds (a padding slot loads its
+ * row's first piece again).
+ *
+ * The inner loop is software-pipelined over sub-steps u of 32 columns with no branches:
+ * while the MT x NB MFMAs of sub-step u issue, the wave dequantizes sub-step u+1's weights
+ * (v_cvt_scalef32_pk_bf16_fp4, exact) into a second set of A fragments and reads u+1's B
+ * fragments from LDS into the registers that u's MFMAs of the same token block have just
+ * consumed; the issue order is pinned with scheduling-group barriers. Weights are loaded
+ * two stages ahead into alternating register slots, each step's registers reloaded as soon
+ * as its last sub-step is dequantized.
+ *
+ * All addresses are in bounds by construction: a wave's weight tiles are clamped to the
+ * last tile of the matrix and prefetches past the last stage re-read the last stage.
+ * Token blocks of a pass past its last token are computed on whatever their LDS rows hold
+ * (those rows load a valid token's activations): an output column of an MFMA depends only
+ * on its own B row, and those columns are never stored. Weight loads keep the default
+ * cache policy: an expert with several passes re-reads its weights, and the caches then
+ * serve part of them. */
+__device__ __forceinline__ uint4 k3_bload16s(k3_rsrc r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t k3_bload4s(k3_rsrc r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
+template <int MODE, int MT, int NB, int SPC, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void mx_prefill_kernel(K3kMxArgs a)
 {
-    constexpr int NTH = 64 * NW, KC = 128 * SPC, LDT = KC + 8, PT = 16 * NB, PR = KC / 8;
+    constexpr int KC = 128 * SPC, PT = 16 * NB, PR = KC / 8;
     constexpr int RT = (MODE == K3K_MX_GATEUP) ? MT / 2 : MT;
-    constexpr int NPC = PT * PR;                              /* 16-byte pieces per stage */
-    constexpr int PPT = (NPC + NTH - 1) / NTH;
-    __shared__ __attribute__((aligned(16))) uint16_t bsh[2][PT + 1][LDT];
+    constexpr int PRP = PR + 1;                               /* slots per token row */
+    constexpr int DPW = (PT * PRP + 64 * NW - 1) / (64 * NW); /* DMA instructions per wave */
+    constexpr int NSL = DPW * 64 * NW;                        /* 16-byte slots per stage */
+    constexpr int NU = 4 * SPC;                               /* 32-column sub-steps per stage */
+    /* s_waitcnt operand: vmcnt <= one stage's weight and scale loads (MT (SPC + 1)), the
+     * other counters unconstrained (gfx9 encoding: vmcnt 3:0 and 15:14, expcnt 6:4,
+     * lgkmcnt 11:8) */
+    constexpr int NLD = MT * (SPC + 1);
+    static_assert(NLD < 64, "vmcnt field");
+    constexpr int WAIT_STAGE = (NLD & 15) | (7 << 4) | (15 << 8) | ((NLD >> 4) << 14);
+    constexpr int WAIT_STAGE_LDS = (NLD & 15) | (7 << 4) | ((NLD >> 4) << 14);   /* and lgkmcnt 0 */
+    __shared__ __attribute__((aligned(1024))) uint4 bs0[NSL];
+    __shared__ __attribute__((aligned(1024))) uint4 bs1[NSL];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1188,9 +1227,10 @@ void mx_prefill_kernel(K3kMxArgs a)
     const int nlw = ((int)gridDim.x - 1 - xg) / nx + 1;
     const int pbeg = (int)((long)npass * xg / nx), pend = (int)((long)npass * (xg + 1) / nx);
     const int n_items = (pend - pbeg) * n_rb;
-
-    for (int i = tid; i < 2 * LDT / 8; i += NTH)
-        *reinterpret_cast<uint4 *>(&bsh[i / (LDT / 8)][PT][(i % (LDT / 8)) * 8]) = make_uint4(0, 0, 0, 0);
+    /* lane's B fragment slot: token r16 (+16 per block), piece 16 (u / 4) + 4 g + u % 4 of
+     * the stage (the 8 columns matching the weight codes it holds) */
+    const int lrd = r16 * PRP + 4 * g;
+    const uint32_t lvoff = (uint32_t)lane * 16u, lsoff = (uint32_t)lane * 4u;
 
     for (int item = li; item < n_items; item += nlw) {
         const int rb = item % n_rb, pass = pbeg + item / n_rb;
@@ -1199,9 +1239,8 @@ void mx_prefill_kernel(K3kMxArgs a)
         const int off = a.job_off[j];
         const int tok0 = a.pass_tp[pass] * PT;
         const int ntok = __builtin_amdgcn_readfirstlane(min(PT, a.job_cnt[j] - tok0));
-        const int nbu = (ntok + 15) >> 4;             /* token blocks holding tokens */
         const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[e];
-        const uint32_t prow = LAYOUT == 1 ? (uint32_t)((rows + 15) & ~15) : (uint32_t)rows;
+        const uint32_t prow = (uint32_t)((rows + 15) & ~15);
         const uint32_t pbytes = prow * rstride;
         const uint32_t sbytes = prow * nblk;
         k3_rsrc rp0, rp1, rs0, rs1;
@@ -1212,32 +1251,27 @@ void mx_prefill_kernel(K3kMxArgs a)
             rp0 = rp1 = k3_make_rsrc(q.p2, pbytes);
             rs0 = rs1 = k3_make_rsrc(q.s2, sbytes);
         }
-        uint32_t poff[MT], soff[MT];
+        /* the wave's tiles (wave-uniform byte offsets), clamped to the last tile */
+        uint32_t ptile[MT], stile[MT];
         const int ntile = (rows + 15) >> 4;
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             const int mt = (MODE == K3K_MX_GATEUP) ? (m % RT) : m;
             const int t = min((rb * rpg + wv * rpw) / 16 + mt, ntile - 1);
-            poff[m] = (uint32_t)t * (uint32_t)nchunk * 4096u + (uint32_t)lane * 16u;
-            soff[m] = (uint32_t)t * (uint32_t)nchunk * 256u + (uint32_t)lane * 4u;
+            ptile[m] = (uint32_t)t * (uint32_t)nchunk * 4096u;
+            stile[m] = (uint32_t)t * (uint32_t)nchunk * 256u;
         }
-        /* staging pieces: token row p = pc / PR, 16-byte column piece o = pc % PR */
+        /* DMA sources: instruction i of this wave fills slots 64 (wv + NW i) + lane */
         const uint32_t xbytes = (uint32_t)a.n_xrows * (uint32_t)K * 2u;
         const k3_rsrc rx = k3_make_rsrc(a.xhi, xbytes);
-        uint32_t gsrc[PPT];
-        int ldst[PPT];
+        uint32_t gsrc[DPW];
 #pragma unroll
-        for (int i = 0; i < PPT; i++) {
-            const int pc = tid + NTH * i, p = pc / PR, o = pc % PR;
-            const bool ok = pc < NPC && p < ntok;
-            const int ar = a.perm[off + tok0 + (ok ? p : 0)];
+        for (int i = 0; i < DPW; i++) {
+            const int s = 64 * (wv + NW * i) + lane, p = s / PRP, o = (s % PRP) % PR;
+            const int ar = a.perm[off + tok0 + (p < ntok ? p : 0)];
             const int xr = (MODE == K3K_MX_GATEUP) ? ar / a.topk : ar;
             gsrc[i] = ((uint32_t)xr * (uint32_t)K + (uint32_t)o * 8u) * 2u;
-            ldst[i] = ok ? p * LDT + o * 8 : -1;
         }
-        int brow[NB];
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) brow[nb] = nb * 16 + r16 < ntok ? nb * 16 + r16 : PT;
 
         k3_f32x4 acc[MT][NB];
 #pragma unroll
@@ -1245,94 +1279,136 @@ void mx_prefill_kernel(K3kMxArgs a)
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) acc[m][nb] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
 
-        /* weights two stages ahead: stages alternate between the two register slots */
-        uint4 qa[2][SPC][MT];
-        uint32_t sq[MT], sqn[MT], sqnn[MT];
-        uint4 bst[PPT];
-        auto load_b = [&](int c) {
-#pragma unroll
-            for (int i = 0; i < PPT; i++) bst[i] = k3_bload16(rx, gsrc[i] + (uint32_t)c * KC * 2u);
-        };
-        auto store_b = [&](int buf) {
-#pragma unroll
-            for (int i = 0; i < PPT; i++)
-                if (ldst[i] >= 0) *reinterpret_cast<uint4 *>(&bsh[buf][0][0] + ldst[i]) = bst[i];
-        };
+        uint4 qa[2][SPC][MT];                 /* weights of two stages (register slots) */
+        uint32_t ss[2][MT];                   /* scale dwords of the two stages, by slot */
+        k3_bf16x8 avc[MT], avn[MT];           /* A fragments: sub-step u and u + 1 */
+        uint4 bv[NB];                         /* B fragments of the current sub-step */
         auto load_step = [&](int c, int d, auto slot) {
             constexpr int S = decltype(slot)::value;
-            /* step s = c SPC + d: 128 columns, 1 KB per tile */
-            const uint32_t bo = (uint32_t)(c * SPC + d) * 1024u;
+            const uint32_t bo = (uint32_t)min(c * SPC + d, nstage * SPC - 1) * 1024u;   /* 1 KB per tile */
 #pragma unroll
             for (int m = 0; m < MT; m++)
-                qa[S][d][m] = k3_bload16(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo);
+                qa[S][d][m] = k3_bload16s(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, lvoff, ptile[m] + bo);
         };
-        auto load_scales = [&](int c, uint32_t *ss) {
+        /* the scale dword (4 steps' bytes) of stage c's 512-column chunk into a register slot
+         * (c clamped: past the end re-reads the last stage) */
+        auto load_scales = [&](int c, auto slot) {
+            constexpr int S = decltype(slot)::value;
+            const uint32_t so = (uint32_t)(min(c, nstage - 1) * SPC >> 2) * 256u;
 #pragma unroll
             for (int m = 0; m < MT; m++)
-                ss[m] = k3_bload4(m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1, soff[m] + (uint32_t)((c * SPC) >> 2) * 256u);
+                ss[S][m] = k3_bload4s(m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1, lsoff, stile[m] + so);
+        };
+        auto lds_b = [&](auto bufsel, int nb, int u) -> uint4 {
+            constexpr int B = decltype(bufsel)::value;
+            return (B ? bs1 : bs0)[lrd + nb * 16 * PRP + 16 * (u >> 2) + (u & 3)];
+        };
+        /* dequantize sub-step u of a register slot; the scale of step c SPC + u / 4 */
+        auto deq = [&](const uint4 (&qs)[SPC][MT], const uint32_t *sw, int c, int u, k3_bf16x8 *dst) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const uint32_t sraw = (sw[m] >> (8 * ((c * SPC + (u >> 2)) & 3))) & 0xFFu;
+                const bool nanb = sraw == 255u;               /* NaN byte: the block is 0 */
+                const uint4 qv = qs[u >> 2][m];
+                const uint32_t codes = (u & 3) == 0 ? qv.x : (u & 3) == 1 ? qv.y : (u & 3) == 2 ? qv.z : qv.w;
+                dst[m] = k3_dequant8_bf16(nanb ? 0u : codes, k3_e8m0_operand(nanb ? 127u : sraw));
+            }
         };
 
         using P0 = std::integral_constant<int, 0>;
         using P1 = std::integral_constant<int, 1>;
-        /* Every prefetch is issued unconditionally (past the last stage the loads read
-         * data that is never used, or zeros past the end of a buffer), so that the wait for
-         * a stage's weights counts exactly the loads issued after them instead of draining
-         * the queue; the stage count is even (K % 512 == 0). */
-        load_b(0);
-        load_scales(0, sq);
+        /* The K loop for passes of NBU token blocks (the blocks past the pass's last token
+         * are not computed). */
+        auto run = [&](auto nbu_c) {
+            constexpr int NBU = decltype(nbu_c)::value;
+            constexpr int DPU = (NBU * 16 * PRP + 64 * NW - 1) / (64 * NW);   /* DMA per wave */
+            /* stage c's activations (the NBU blocks) into stage buffer B; c clamped: past
+             * the end re-reads the last stage */
+            auto dma_b = [&](int c, auto bufsel) {
+                constexpr int B = decltype(bufsel)::value;
+                const uint32_t so = (uint32_t)min(c, nstage - 1) * KC * 2u;
 #pragma unroll
-        for (int d = 0; d < SPC; d++) load_step(0, d, P0{});
-        load_scales(1, sqn);
+                for (int i = 0; i < DPU; i++) k3_dma16(rx, (B ? bs1 : bs0) + 64 * (wv + NW * i), gsrc[i], so);
+            };
+            /* Every prefetch is issued unconditionally, so that the wait for a stage's
+             * weights counts exactly the loads issued after them instead of draining the
+             * queue; the stage count is even. The previous item's last (unused) DMA has
+             * landed and every wave is past its reads before stages 0 and 1 are fetched. */
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            dma_b(0, P0{});
+            dma_b(1, P1{});
+            load_scales(0, P0{});
 #pragma unroll
-        for (int d = 0; d < SPC; d++) load_step(1, d, P1{});
-        store_b(0);
-        __syncthreads();
-        auto stage = [&](int c, auto slot) {
-            constexpr int S = decltype(slot)::value;
-            const int buf = c & 1;
-            load_b(c + 1);
-            load_scales(c + 2, sqnn);
+            for (int d = 0; d < SPC; d++) load_step(0, d, P0{});
+            load_scales(1, P1{});
 #pragma unroll
-            for (int d = 0; d < SPC; d++) {
-                float so[MT];
-                bool nanb[MT];
-                if (LAYOUT != 2) {
+            for (int d = 0; d < SPC; d++) load_step(1, d, P1{});
+            deq(qa[0], ss[0], 0, 0, avc);
+            __builtin_amdgcn_s_waitcnt(WAIT_STAGE);       /* everything but stage 1's loads */
+            __syncthreads();
 #pragma unroll
-                    for (int m = 0; m < MT; m++) {
-                        const uint32_t sraw = (sq[m] >> (8 * ((c * SPC + d) & 3))) & 0xFFu;
-                        nanb[m] = sraw == 255u;              /* NaN byte: the block is 0 */
-                        so[m] = k3_e8m0_operand(nanb[m] ? 127u : sraw);
+            for (int nb = 0; nb < NBU; nb++) bv[nb] = lds_b(P0{}, nb, 0);
+
+            auto stage = [&](int c, auto slot) {
+                constexpr int S = decltype(slot)::value;
+                using SN = std::integral_constant<int, S ^ 1>;
+#pragma unroll
+                for (int u = 0; u < NU; u++) {
+                    if (u == NU - 1) {
+                        /* This wave's reads of buffer S are in registers and stage c + 1's
+                         * activations (DMA issued a stage ago, before this stage's weight
+                         * and scale loads) have landed; after the barrier both hold for
+                         * every wave: buffer S takes stage c + 2, and the last sub-step's
+                         * MFMAs overlap the first reads of stage c + 1. */
+                        __builtin_amdgcn_s_waitcnt(WAIT_STAGE_LDS);
+                        __syncthreads();
+                        dma_b(c + 2, slot);
                     }
-                }
+                    if (u + 1 < NU) deq(qa[S], ss[S], c, u + 1, avn);
+                    else deq(qa[S ^ 1], ss[S ^ 1], c + 1, 0, avn);
 #pragma unroll
-                for (int pp = 0; pp < 4; pp++) {
-                    /* this piece's weights, dequantized once and used by NB MFMAs */
-                    k3_bf16x8 av[MT];
-#pragma unroll
-                    for (int m = 0; m < MT; m++) {
-                        const uint4 qv = qa[S][d][m];
-                        const uint32_t codes = pp == 0 ? qv.x : pp == 1 ? qv.y : pp == 2 ? qv.z : qv.w;
-                        av[m] = k3_dequant8_bf16(nanb[m] ? 0u : codes, so[m]);
-                    }
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++) {
-                        if (nb >= nbu) break;             /* a pass's last blocks may be empty */
-                        const uint4 bv = *reinterpret_cast<const uint4 *>(&bsh[buf][brow[nb]][(4 * d + g) * 32 + pp * 8]);
+                    for (int nb = 0; nb < NBU; nb++) {
 #pragma unroll
                         for (int m = 0; m < MT; m++)
-                            acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[m], k3_as_bf16x8(bv), acc[m][nb], 0, 0, 0);
+                            acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(avc[m], k3_as_bf16x8(bv[nb]), acc[m][nb], 0, 0, 0);
+                        if (u + 1 < NU) bv[nb] = lds_b(slot, nb, u + 1);
+                        else bv[nb] = lds_b(SN{}, nb, 0);
                     }
-                }
-                load_step(c + 2, d, slot);
-            }
-            store_b(buf ^ 1);
+                    /* step u / 4's last sub-step is dequantized: its registers take stage
+                     * c + 2, and after the stage's last step its scale dwords too */
+                    if ((u & 3) == 2) load_step(c + 2, u >> 2, slot);
+                    if (u == NU - 2) load_scales(c + 2, slot);
 #pragma unroll
-            for (int m = 0; m < MT; m++) { sq[m] = sqn[m]; sqn[m] = sqnn[m]; }
-            __syncthreads();
+                    for (int m = 0; m < MT; m++) avc[m] = avn[m];
+                    /* issue order of the sub-step: each token block's MT MFMAs interleaved
+                     * with the next sub-step's dequantization, then that block's next B read */
+#pragma unroll
+                    for (int nb = 0; nb < NBU; nb++) {
+#pragma unroll
+                        for (int m = 0; m < MT; m++) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      /* MFMA */
+                            __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);      /* VALU */
+                        }
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          /* DS read */
+                        if ((u & 3) == 2 && nb < MT) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); /* VMEM */
+                        if (u == NU - 2 && nb + MT >= NBU) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            };
+            for (int c = 0; c < nstage; c += 2) {
+                stage(c, P0{});
+                stage(c + 1, P1{});
+            }
         };
-        for (int c = 0; c < nstage; c += 2) {
-            stage(c, P0{});
-            stage(c + 1, P1{});
+        switch ((ntok + 15) >> 4) {
+            case 1: if (NB >= 1) run(std::integral_constant<int, (NB >= 1 ? 1 : NB)>{}); break;
+            case 2: if (NB >= 2) run(std::integral_constant<int, (NB >= 2 ? 2 : NB)>{}); break;
+            case 3: if (NB >= 3) run(std::integral_constant<int, (NB >= 3 ? 3 : NB)>{}); break;
+            case 4: if (NB >= 4) run(std::integral_constant<int, (NB >= 4 ? 4 : NB)>{}); break;
+            case 5: if (NB >= 5) run(std::integral_constant<int, (NB >= 5 ? 5 : NB)>{}); break;
+            default: run(std::integral_constant<int, NB>{}); break;
         }
 
 #pragma unroll
@@ -1343,12 +1419,19 @@ void mx_prefill_kernel(K3kMxArgs a)
             for (int m = 0; m < RT; m++) {
                 const int base = rb * rpg + wv * rpw + 16 * m + 4 * g;
                 if (MODE == K3K_MX_GATEUP) {
-                    uint16_t *oh = a.ahi + (size_t)orow * rows;
+                    /* the activation is rounded to bf16: its fast form suffices */
+                    uint16_t h[4];
+#pragma unroll
                     for (int jj = 0; jj < 4; jj++)
-                        if (base + jj < rows) {
-                            const float v = k3_act_pair(acc[m][nb][jj], acc[m + RT][nb][jj], a.act, a.b1, a.b2);
-                            oh[base + jj] = k3_bf16_rne(v);
-                        }
+                        h[jj] = k3_bf16_rne(k3_act_pair_fast(acc[m][nb][jj], acc[m + RT][nb][jj], a.act, a.b1, a.b2));
+                    uint16_t *oh = a.ahi + (size_t)orow * rows + base;
+                    if (base + 3 < rows && (rows & 3) == 0) {
+                        *reinterpret_cast<uint2 *>(oh) = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+                    } else {
+                        for (int jj = 0; jj < 4; jj++)
+                            if (base + jj < rows) oh[jj] = h[jj];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 } else {
                     float *o = a.out + (size_t)orow * rows;
                     if (base + 3 < rows && (rows & 3) == 0) {
@@ -1364,10 +1447,10 @@ void mx_prefill_kernel(K3kMxArgs a)
     }
 }
 
-template <int MODE, int MT, int NB, int LAYOUT, int SPC = 2, int NW = 4>
+template <int MODE, int MT, int NB, int SPC, int NW>
 int launch_prefill(const K3kMxArgs *a, int grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((mx_prefill_kernel<MODE, MT, NB, LAYOUT, SPC, NW>), dim3(grid), dim3(64 * NW), 0, st, *a);
+    hipLaunchKernelGGL((mx_prefill_kernel<MODE, MT, NB, SPC, NW>), dim3(grid), dim3(64 * NW), 0, st, *a);
     K3K_LAUNCH_CHECK("mx_prefill launch");
     return 0;
 }
@@ -1498,10 +1581,10 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
         const long items = (long)a->max_passes * ((a->rows + rpg - 1) / rpg);
         const int grid = (int)(items < (long)cus ? (items > 0 ? items : 1) : (long)cus);
         if (a->pass_tok == 96)
-            return gu ? launch_prefill<K3K_MX_GATEUP, 4, 6, 1, 1, 8>(a, grid, st)
-                      : launch_prefill<K3K_MX_DOWN, 4, 6, 1, 1, 8>(a, grid, st);
-        return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 1, 2, 8>(a, grid, st)
-                  : launch_prefill<K3K_MX_DOWN, 4, 3, 1, 2, 8>(a, grid, st);
+            return gu ? launch_prefill<K3K_MX_GATEUP, 4, 6, 1, 8>(a, grid, st)
+                      : launch_prefill<K3K_MX_DOWN, 4, 6, 1, 8>(a, grid, st);
+        return gu ? launch_prefill<K3K_MX_GATEUP, 4, 3, 2, 8>(a, grid, st)
+                  : launch_prefill<K3K_MX_DOWN, 4, 3, 2, 8>(a, grid, st);
     }
     if (a->pass_tok == 32) {
         /* prefill: 32-token passes, two MFMA column blocks per weight fragment, activations

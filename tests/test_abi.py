@@ -37,6 +37,17 @@ def test_library_exports_every_declared_symbol(k3):
     assert "k3_expert_drops" in have
 
 
+def test_library_has_no_unresolved_symbols(k3):
+    """Every symbol the library imports comes from a versioned system library (HIP runtime,
+    libc, libgomp): a kernel whose host stub the compiler dropped would otherwise show up
+    only as a load failure on a GPU machine."""
+    out = subprocess.run(["nm", "-D", "--undefined-only", k3.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    loose = [ln.split()[-1] for ln in out.splitlines()
+             if ln.split() and ln.split()[0] == "U" and "@" not in ln.split()[-1]]
+    assert not loose, f"unresolved symbols: {loose}"
+
+
 def test_python_mirror_binds_all(k3):
     for name in k3.exported_symbols():
         assert hasattr(k3.lib(), name)
