@@ -335,29 +335,38 @@ __device__ __forceinline__ void gemv_finish(uint16_t *xs, k3_f32x4 acc, int wv, 
     }
 }
 
-/* mx_gemv_chunk_kernel: K % 512 == 0, one 512-column chunk per wave (kw = K / 512 <= 16).
- * A lane loads blocks 4i+g (i = 0..3) of its row and the row's 16 scale bytes of the chunk
- * in one 16-byte load, with the default cache policy: the two halves of each 128-byte
- * line come from two load instructions. */
+/* mx_gemv_chunk_kernel: K % 512 == 0, one 512-column chunk per wave (kw = K / 512 <= 16),
+ * one or two tokens; a workgroup per 16-row tile. The latency of the few loads a lane makes
+ * is the whole cost, so nothing else may wait behind them:
+ *  - each wave loads only its own chunk of the activations (lane L: columns 8L .. 8L+7 of
+ *    each token) first, then its weights (blocks 4i+g, i = 0..3, of its row, and the row's
+ *    16 scale bytes of the chunk in one 16-byte load), splits the activations into bf16
+ *    terms in a wave-private LDS region and reads its B operands back from there: LDS
+ *    operations of one wave complete in order, so no workgroup barrier precedes the
+ *    products;
+ *  - the activation terms of all tokens share each MFMA (B column j = token j / NS, term
+ *    j % NS; the other columns read a zero block), and the four k-slices of a block
+ *    accumulate into four independent sums;
+ *  - the waves' sums meet through LDS behind one barrier, and 16 ntok threads add them in
+ *    wave order. */
 template <int NS>
 __global__ __launch_bounds__(1024) void mx_gemv_chunk_kernel(K3kMxArgs a, int kw)
 {
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
-    constexpr int XPT = 4;                                  /* 2 ntok float4 per thread */
-    const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* wave w: [ntok NS + 1][512] */
+    const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     const int K = a.K, nblk = K >> 5, rows = a.rows, ntok = a.ntok;
+    const int ncol = ntok * NS;                              /* B columns holding terms */
     const int tile = blockIdx.x;
-    const int nq = ntok * (K >> 2);
-    float4 xv[XPT];
+    float4 xv[2][2];
 #pragma unroll
-    for (int j = 0; j < XPT; j++) {
-        const int i = tid + j * nthr;
-        xv[j] = i < nq ? *reinterpret_cast<const float4 *>(a.xf32 + 4 * (size_t)i) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            xv[t][h] = t < ntok ? *reinterpret_cast<const float4 *>(a.xf32 + (size_t)t * K + wv * 512 + 8 * lane + 4 * h)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
     uint4 q[4];
-    uint32_t sc[4];
     const int row = min(tile * 16 + r16, rows - 1);         /* rows past the end: discarded */
     const k3_rsrc rp = k3_make_rsrc(a.packed, (uint32_t)rows * (uint32_t)(K >> 1));
     const k3_rsrc rs = k3_make_rsrc(a.scales, (uint32_t)rows * (uint32_t)nblk);
@@ -365,22 +374,63 @@ __global__ __launch_bounds__(1024) void mx_gemv_chunk_kernel(K3kMxArgs a, int kw
 #pragma unroll
     for (int i = 0; i < 4; i++) q[i] = k3_bload16(rp, pb + (uint32_t)(4 * i + g) * 16u);
     const uint4 sv = k3_bload16(rs, (uint32_t)row * (uint32_t)nblk + (uint32_t)wv * 16u);
-    sc[0] = (sv.x >> (8 * g)) & 0xffu;
-    sc[1] = (sv.y >> (8 * g)) & 0xffu;
-    sc[2] = (sv.z >> (8 * g)) & 0xffu;
-    sc[3] = (sv.w >> (8 * g)) & 0xffu;
-    gemv_stage_x<NS>(xs, xv, tid, nthr, nq, ntok, K);
-    __syncthreads();
-    const int xr = r16 < ntok ? r16 : 0;
-    const uint32_t bm = r16 < ntok ? ~0u : 0u;
-    k3_f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    uint16_t *wx = xs + (size_t)wv * (ncol + 1) * 512;       /* column j: wx + 512 j; zeros: wx + 512 ncol */
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        if (t >= ntok) break;
+        uint16_t h[8], l[8];
+        const float f[8] = {xv[t][0].x, xv[t][0].y, xv[t][0].z, xv[t][0].w,
+                            xv[t][1].x, xv[t][1].y, xv[t][1].z, xv[t][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) k3_split2(f[e], h[e], l[e]);
+        *reinterpret_cast<uint4 *>(wx + (t * NS) * 512 + 8 * lane) =
+            make_uint4(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                       h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16));
+        if (NS == 2)
+            *reinterpret_cast<uint4 *>(wx + (t * NS + 1) * 512 + 8 * lane) =
+                make_uint4(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16),
+                           l[4] | ((uint32_t)l[5] << 16), l[6] | ((uint32_t)l[7] << 16));
+    }
+    *reinterpret_cast<uint4 *>(wx + ncol * 512 + 8 * lane) = make_uint4(0, 0, 0, 0);
+    __builtin_amdgcn_wave_barrier();
+    const uint16_t *bcol = wx + min(r16, ncol) * 512;
+    const uint32_t scw[4] = {sv.x, sv.y, sv.z, sv.w};
+    k3_f32x4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int blk = wv * 16 + 4 * i + g;
-        gemv_step<NS>(acc, q[i], sc[i], &xs[(size_t)xr * K + blk * 32],
-                      &xs[(size_t)(ntok + xr) * K + blk * 32], bm);
+        const int blk = 4 * i + g;                          /* MX block of the chunk */
+        uint32_t ss = (scw[i] >> (8 * g)) & 0xffu;
+        uint4 qq = q[i];
+        if (ss == 255u) {                                   /* NaN byte: the block is 0 */
+            qq = make_uint4(0, 0, 0, 0);
+            ss = 127u;
+        }
+        const float so = k3_e8m0_operand(ss);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t codes = p == 0 ? qq.x : p == 1 ? qq.y : p == 2 ? qq.z : qq.w;
+            const uint4 bv = *reinterpret_cast<const uint4 *>(bcol + blk * 32 + 8 * p);
+            acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3_dequant8_bf16(codes, so), k3_as_bf16x8(bv), acc[p], 0, 0, 0);
+        }
     }
-    gemv_finish(xs, acc[0] + acc[1], wv, kw, lane, r16, g, ntok, tile, a.rows, a.y, a.ldy);
+    /* lane (g, r16): rows 4g..4g+3 of column r16; a token's value is its columns' sum */
+    k3_f32x4 v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    if (NS == 2) {
+        k3_f32x4 nx;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) nx[jj] = __shfl_down(v[jj], 1, 16);
+        v += nx;
+    }
+    float *red = reinterpret_cast<float *>(xs + (size_t)kw * (ncol + 1) * 512);   /* [kw][ntok][16] */
+    if (r16 < ncol && r16 % NS == 0)
+        *reinterpret_cast<float4 *>(&red[(wv * ntok + r16 / NS) * 16 + 4 * g]) = make_float4(v[0], v[1], v[2], v[3]);
+    __syncthreads();
+    if (tid < ntok * 16) {
+        const int t = tid >> 4, rr = tid & 15;
+        float sum = red[t * 16 + rr];
+        for (int w = 1; w < kw; w++) sum += red[(w * ntok + t) * 16 + rr];
+        if (tile * 16 + rr < rows) a.y[(size_t)t * a.ldy + tile * 16 + rr] = sum;
+    }
 }
 
 /* mx_gemv_small_kernel: any K % 32 == 0 (row-major), runs of at most SMAX steps per wave
@@ -1547,6 +1597,8 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
             const int kw = chunked ? a->K / 512 : (nsteps + 7) / 8;
             size_t lds = (size_t)a->nsplit * a->ntok * a->K * 2;
             if (lds < (size_t)kw * 1024) lds = (size_t)kw * 1024;
+            /* chunked: per wave ntok nsplit + 1 columns of 512 bf16, then the sums */
+            if (chunked) lds = (size_t)kw * (a->ntok * a->nsplit + 1) * 1024 + (size_t)kw * a->ntok * 64;
             const int grid = (a->rows + 15) / 16;
             void (*kern)(K3kMxArgs, int);
             if (chunked)
