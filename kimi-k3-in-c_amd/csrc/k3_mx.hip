@@ -997,16 +997,16 @@ void mx_moe_kernel(K3kMxArgs a)
         const uint32_t xbytes = (uint32_t)a.n_xrows * (uint32_t)K * 2u;
         const k3_rsrc rxh = k3_make_rsrc(a.xhi, xbytes);
         const k3_rsrc rxl = k3_make_rsrc(NS == 2 ? a.xlo : a.xhi, xbytes);
+        /* every staging load is issued (rows past the pass read the pass's first token; only
+         * their LDS stores are skipped), so that the waits count exactly the loads issued
+         * after the one they wait for */
         uint32_t gsrc[PPW];
 #pragma unroll
         for (int i = 0; i < PPW; i++) {
             const int rh = wv + NW * i, p = rh / NS;
-            gsrc[i] = 0;
-            if (rh < NRH && p < ntok) {
-                const int ar = a.perm[off + tok0 + p];
-                const int xr = (MODE == K3K_MX_GATEUP) ? ar / a.topk : ar;
-                gsrc[i] = ((uint32_t)xr * (uint32_t)K + (uint32_t)lane * 8u) * 2u;
-            }
+            const int ar = a.perm[off + tok0 + (rh < NRH && p < ntok ? p : 0)];
+            const int xr = (MODE == K3K_MX_GATEUP) ? ar / a.topk : ar;
+            gsrc[i] = ((uint32_t)xr * (uint32_t)K + (uint32_t)lane * 8u) * 2u;
         }
         /* B operand rows: token column nb*16 + r16 of the pass, or the zero row; PACK: token
          * r16 % 8 of term r16 / 8 */
@@ -1034,12 +1034,15 @@ void mx_moe_kernel(K3kMxArgs a)
         uint32_t sq[SQN], sqn[SQN], sqnn[SQN];
         uint4 bst[PPW];
 
+        /* Loads past the last chunk are issued too, at an offset beyond the buffer (2^31:
+         * every operand is smaller): they return zeros and move no data. */
+        constexpr uint32_t OOB = 0x80000000u;
         auto load_b = [&](int c) {
+            const uint32_t co = (uint32_t)c * KC * 2u;
 #pragma unroll
             for (int i = 0; i < PPW; i++) {
                 const int rh = wv + NW * i;
-                if (rh < NRH && rh / NS < ntok)
-                    bst[i] = k3_bload16(rh % NS ? rxl : rxh, gsrc[i] + (uint32_t)c * KC * 2u);
+                bst[i] = k3_bload16(rh % NS ? rxl : rxh, c < nchunk ? gsrc[i] + co : OOB);
             }
         };
         auto store_b = [&](int buf) {
@@ -1056,17 +1059,18 @@ void mx_moe_kernel(K3kMxArgs a)
                                             : ((uint32_t)c * 4u + (uint32_t)d) * 1024u;
 #pragma unroll
             for (int m = 0; m < MT; m++)
-                qa[S][d][m] = k3_bload16<WPOL>(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, poff[m] + bo);
+                qa[S][d][m] = k3_bload16<WPOL>(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1,
+                                               c < nchunk ? poff[m] + bo : OOB);
         };
         auto load_scales = [&](int c, uint32_t *ss) {
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 const k3_rsrc rs = m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1;
                 if (LAYOUT == 0) {
-                    const uint4 v = k3_bload16<WPOL>(rs, soff[m] + (uint32_t)c * 16u);
+                    const uint4 v = k3_bload16<WPOL>(rs, c < nchunk ? soff[m] + (uint32_t)c * 16u : OOB);
                     ss[4 * m] = v.x; ss[4 * m + 1] = v.y; ss[4 * m + 2] = v.z; ss[4 * m + 3] = v.w;
                 } else {
-                    ss[m] = k3_bload4<WPOL>(rs, soff[m] + (uint32_t)c * 256u);
+                    ss[m] = k3_bload4<WPOL>(rs, c < nchunk ? soff[m] + (uint32_t)c * 256u : OOB);
                 }
             }
         };
@@ -1077,7 +1081,7 @@ void mx_moe_kernel(K3kMxArgs a)
         load_scales(0, sq);
 #pragma unroll
         for (int d = 0; d < SPC; d++) load_step(0, d, I0{});
-        if (DEPTH == 2 && nchunk > 1) {
+        if (DEPTH == 2) {
             load_scales(1, sqn);
 #pragma unroll
             for (int d = 0; d < SPC; d++) load_step(1, d, I1{});
@@ -1088,9 +1092,14 @@ void mx_moe_kernel(K3kMxArgs a)
             constexpr int S = decltype(slot)::value;
             const int buf = c & 1;
             const bool more = c + 1 < nchunk;
-            const bool more2 = c + DEPTH < nchunk;
-            if (more) load_b(c + 1);
-            if (more2) load_scales(c + DEPTH, DEPTH == 2 ? sqnn : sqn);
+            /* Every prefetch is issued (past the end: zeros, no data moved), so that the waits
+             * count exactly the loads issued after the one they wait for. For decode passes
+             * the barrier keeps the compiler from sinking the staging loads down to their LDS
+             * stores, which would wait for them (and every older load) on the spot; larger
+             * passes would hold too many registers for the staging across the chunk. */
+            load_b(c + 1);
+            load_scales(c + DEPTH, DEPTH == 2 ? sqnn : sqn);
+            if constexpr (PT <= 8) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int d = 0; d < SPC; d++) {
                 /* B operand: token columns (or the zero row), block 4d+g of the chunk */
@@ -1112,11 +1121,12 @@ void mx_moe_kernel(K3kMxArgs a)
                     const uint32_t sraw = LAYOUT == 0 ? (sq[4 * m + d] >> (8 * g)) & 0xFFu
                                                       : (sq[m] >> (8 * d)) & 0xFFu;
                     const bool nanb = sraw == 255u;              /* NaN byte: the block is 0 */
+                    const uint32_t keep = nanb ? 0u : ~0u;       /* a mask, not a branch */
                     qq[m] = qa[S][d][m];
-                    qq[m].x = nanb ? 0u : qq[m].x;
-                    qq[m].y = nanb ? 0u : qq[m].y;
-                    qq[m].z = nanb ? 0u : qq[m].z;
-                    qq[m].w = nanb ? 0u : qq[m].w;
+                    qq[m].x &= keep;
+                    qq[m].y &= keep;
+                    qq[m].z &= keep;
+                    qq[m].w &= keep;
                     so[m] = k3_e8m0_operand(nanb ? 127u : sraw);
                 }
 #pragma unroll
@@ -1132,7 +1142,7 @@ void mx_moe_kernel(K3kMxArgs a)
                                 acc[m][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, k3_as_bf16x8(bl[nb][pp]), acc[m][nb], 0, 0, 0);
                         }
                     }
-                if (more2) load_step(c + DEPTH, d, slot);
+                load_step(c + DEPTH, d, slot);
             }
             if (more) store_b(buf ^ 1);
 #pragma unroll
@@ -1223,7 +1233,8 @@ int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
  * as its last sub-step is dequantized.
  *
  * All addresses are in bounds by construction: a wave's weight tiles are clamped to the
- * last tile of the matrix and prefetches past the last stage re-read the last stage.
+ * last tile of the matrix, and prefetches past the last stage re-read it (GATEUP) or read
+ * at an offset past the end of their buffer (DOWN: zeros, no data moved).
  * Token blocks of a pass past its last token are computed on whatever their LDS rows hold
  * (those rows load a valid token's activations): an output column of an MFMA depends only
  * on its own B row, and those columns are never stored. Weight loads keep the default
@@ -1281,6 +1292,12 @@ void mx_prefill_kernel(K3kMxArgs a)
      * the stage (the 8 columns matching the weight codes it holds) */
     const int lrd = r16 * PRP + 4 * g;
     const uint32_t lvoff = (uint32_t)lane * 16u, lsoff = (uint32_t)lane * 4u;
+    /* Prefetches past the last stage are issued too, so that every wait counts exactly the
+     * loads issued after the one it waits for: DOWN's at a per-lane offset of 2^31, beyond
+     * every buffer (zeros, no data moved); GATEUP's re-read the last stage, because the
+     * offset select would cost it registers it does not have. The wave-uniform part of
+     * each address stays clamped inside the buffer. */
+    constexpr uint32_t OOB = 0x80000000u;
 
     for (int item = li; item < n_items; item += nlw) {
         const int rb = item % n_rb, pass = pbeg + item / n_rb;
@@ -1336,18 +1353,20 @@ void mx_prefill_kernel(K3kMxArgs a)
         auto load_step = [&](int c, int d, auto slot) {
             constexpr int S = decltype(slot)::value;
             const uint32_t bo = (uint32_t)min(c * SPC + d, nstage * SPC - 1) * 1024u;   /* 1 KB per tile */
+            const uint32_t vo = (MODE == K3K_MX_GATEUP || c < nstage) ? lvoff : OOB;
 #pragma unroll
             for (int m = 0; m < MT; m++)
-                qa[S][d][m] = k3_bload16s(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, lvoff, ptile[m] + bo);
+                qa[S][d][m] = k3_bload16s(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1, vo, ptile[m] + bo);
         };
         /* the scale dword (4 steps' bytes) of stage c's 512-column chunk into a register slot
          * (c clamped: past the end re-reads the last stage) */
         auto load_scales = [&](int c, auto slot) {
             constexpr int S = decltype(slot)::value;
             const uint32_t so = (uint32_t)(min(c, nstage - 1) * SPC >> 2) * 256u;
+            const uint32_t vo = (MODE == K3K_MX_GATEUP || c < nstage) ? lsoff : OOB;
 #pragma unroll
             for (int m = 0; m < MT; m++)
-                ss[S][m] = k3_bload4s(m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1, lsoff, stile[m] + so);
+                ss[S][m] = k3_bload4s(m < RT || MODE != K3K_MX_GATEUP ? rs0 : rs1, vo, stile[m] + so);
         };
         auto lds_b = [&](auto bufsel, int nb, int u) -> uint4 {
             constexpr int B = decltype(bufsel)::value;
@@ -1378,11 +1397,12 @@ void mx_prefill_kernel(K3kMxArgs a)
                 constexpr int B = decltype(bufsel)::value;
                 const uint32_t so = (uint32_t)min(c, nstage - 1) * KC * 2u;
 #pragma unroll
-                for (int i = 0; i < DPU; i++) k3_dma16(rx, (B ? bs1 : bs0) + 64 * (wv + NW * i), gsrc[i], so);
+                for (int i = 0; i < DPU; i++)
+                    k3_dma16(rx, (B ? bs1 : bs0) + 64 * (wv + NW * i), (MODE == K3K_MX_GATEUP || c < nstage) ? gsrc[i] : OOB, so);
             };
             /* Every prefetch is issued unconditionally, so that the wait for a stage's
              * weights counts exactly the loads issued after them instead of draining the
-             * queue; the stage count is even. The previous item's last (unused) DMA has
+             * queue; the stage count is even. The previous item's last DMA (zeros) has
              * landed and every wave is past its reads before stages 0 and 1 are fetched. */
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
