@@ -616,28 +616,38 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
      * scale bytes (dword i, byte g = step i) */
     uint4 qa[2][NM][4];
     uint4 sq[2][NM];
+    /* Chunks past the wave's last are loaded too, at an offset beyond every buffer (2^31):
+     * they return zeros and move no data. With no load under a branch, every wait counts
+     * exactly the loads issued after the one it waits for, so chunk c + 1 stays in flight
+     * while chunk c is multiplied. */
+    constexpr uint32_t OOB = 0x80000000u;
     auto load = [&](int c, auto slot) {
         constexpr int S = decltype(slot)::value;
+        const bool in = c < c1;
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             if (LAYOUT == 1) {
                 const uint32_t tc = (uint32_t)tile * (uint32_t)nchunk + (uint32_t)c;
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    qa[S][m][i] = k3_bload16<WPOL>(rp[m], tc * 4096u + (uint32_t)i * 1024u + (uint32_t)lane * 16u);
-                sq[S][m].x = k3_bload4<WPOL>(rs[m], tc * 256u + (uint32_t)lane * 4u);
+                    qa[S][m][i] = k3_bload16<WPOL>(rp[m], in ? tc * 4096u + (uint32_t)i * 1024u + (uint32_t)lane * 16u : OOB);
+                sq[S][m].x = k3_bload4<WPOL>(rs[m], in ? tc * 256u + (uint32_t)lane * 4u : OOB);
             } else {
                 const uint32_t pb = (uint32_t)row * (uint32_t)(K >> 1) + (uint32_t)c * 256u;
 #pragma unroll
-                for (int i = 0; i < 4; i++) qa[S][m][i] = k3_bload16<WPOL>(rp[m], pb + (uint32_t)(4 * i + g) * 16u);
-                sq[S][m] = k3_bload16<WPOL>(rs[m], (uint32_t)row * (uint32_t)nblk + (uint32_t)c * 16u);
+                for (int i = 0; i < 4; i++) qa[S][m][i] = k3_bload16<WPOL>(rp[m], in ? pb + (uint32_t)(4 * i + g) * 16u : OOB);
+                sq[S][m] = k3_bload16<WPOL>(rs[m], in ? (uint32_t)row * (uint32_t)nblk + (uint32_t)c * 16u : OOB);
             }
         }
     };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
-    if (c0 < c1) load(c0, P0{});
-    if (c0 + 1 < c1) load(c0 + 1, P1{});
+    /* issued in the loop's order (slot 0, then slot 1): the waits at the loop head take the
+     * worse of the two ways in, so a reordered prologue would make them wait for slot 1 too */
+    load(c0, P0{});
+    __builtin_amdgcn_sched_barrier(0);
+    load(c0 + 1, P1{});
+    __builtin_amdgcn_sched_barrier(0);
     for (int i = tid; i < 64; i += nthr)
         reinterpret_cast<uint4 *>(&xs[(size_t)NS * K])[i] = make_uint4(0, 0, 0, 0);
     if (MODE == K3K_MX_GATEUP) {
@@ -687,14 +697,14 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
             }
         }
     };
-    for (int c = c0; c < c1; c += 2) {
+    int c = c0;
+    for (; c + 1 < c1; c += 2) {
         comp(c, P0{});
-        if (c + 2 < c1) load(c + 2, P0{});
-        if (c + 1 < c1) {
-            comp(c + 1, P1{});
-            if (c + 3 < c1) load(c + 3, P1{});
-        }
+        load(c + 2, P0{});
+        comp(c + 1, P1{});
+        load(c + 3, P1{});
     }
+    if (c < c1) comp(c, P0{});
     /* K shares in order: share 0 adds those of shares 1.. (LDS reused after the products);
      * then column 0 (hi) + column 1 (lo) */
     k3_f32x4 *red = reinterpret_cast<k3_f32x4 *>(xs);
@@ -793,25 +803,31 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
     const int row = min(tile * 16 + r16, rows - 1);
     uint4 qa[2][4];
     uint4 sq[2];
+    /* chunks past the wave's last load zeros from beyond the buffer, so no load sits under
+     * a branch and the waits count exactly (as in mx_decode_kernel) */
+    constexpr uint32_t OOB = 0x80000000u;
     auto load = [&](int c, auto slot) {
         constexpr int S = decltype(slot)::value;
+        const bool in = c < c1;
         if (LAYOUT == 1) {
             const uint32_t tc = (uint32_t)tile * (uint32_t)nchunk + (uint32_t)c;
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                qa[S][i] = k3_bload16<WPOL>(rp, tc * 4096u + (uint32_t)i * 1024u + (uint32_t)lane * 16u);
-            sq[S].x = k3_bload4<WPOL>(rs, tc * 256u + (uint32_t)lane * 4u);
+                qa[S][i] = k3_bload16<WPOL>(rp, in ? tc * 4096u + (uint32_t)i * 1024u + (uint32_t)lane * 16u : OOB);
+            sq[S].x = k3_bload4<WPOL>(rs, in ? tc * 256u + (uint32_t)lane * 4u : OOB);
         } else {
             const uint32_t pb = (uint32_t)row * (uint32_t)(K >> 1) + (uint32_t)c * 256u;
 #pragma unroll
-            for (int i = 0; i < 4; i++) qa[S][i] = k3_bload16<WPOL>(rp, pb + (uint32_t)(4 * i + g) * 16u);
-            sq[S] = k3_bload16<WPOL>(rs, (uint32_t)row * (uint32_t)nblk + (uint32_t)c * 16u);
+            for (int i = 0; i < 4; i++) qa[S][i] = k3_bload16<WPOL>(rp, in ? pb + (uint32_t)(4 * i + g) * 16u : OOB);
+            sq[S] = k3_bload16<WPOL>(rs, in ? (uint32_t)row * (uint32_t)nblk + (uint32_t)c * 16u : OOB);
         }
     };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
-    if (c0 < c1) load(c0, P0{});
-    if (c0 + 1 < c1) load(c0 + 1, P1{});
+    load(c0, P0{});                                         /* in the loop's order */
+    __builtin_amdgcn_sched_barrier(0);
+    load(c0 + 1, P1{});
+    __builtin_amdgcn_sched_barrier(0);
     /* this wave's slot and columns of the activation terms into [slot][term][K] (the waves
      * of one slot stage disjoint column ranges), and the row of zeros (every wave writes the
      * same zeros): no workgroup barrier before the products */
@@ -869,14 +885,14 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
             }
         }
     };
-    for (int c = c0; c < c1; c += 2) {
+    int c = c0;
+    for (; c + 1 < c1; c += 2) {
         comp(c, P0{});
-        if (c + 2 < c1) load(c + 2, P0{});
-        if (c + 1 < c1) {
-            comp(c + 1, P1{});
-            if (c + 3 < c1) load(c + 3, P1{});
-        }
+        load(c + 2, P0{});
+        comp(c + 1, P1{});
+        load(c + 3, P1{});
     }
+    if (c < c1) comp(c, P0{});
     /* lanes of token column 0 (hi) and 1 (lo) hold the tile's 16 rows, four each */
     if (r16 < NS) {
         const k3_f32x4 sum = acc[0] + acc[1];
