@@ -648,6 +648,8 @@ int k3d_mxfp4_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
  * `ot[i] += sdn[i]`, k3_ops.c:654). */
 typedef struct {
     uint16_t *xhi, *xlo, *ahi, *alo;
+    float *part;
+    size_t part_bytes;
 } ShWs;
 
 static size_t shared_layout(Carve *c, ShWs *w, int T, int hidden, int inter, int prec)
@@ -656,6 +658,10 @@ static size_t shared_layout(Carve *c, ShWs *w, int T, int hidden, int inter, int
     w->xlo = prec == 0 ? (uint16_t *)take(c, (size_t)T * hidden * 2) : NULL;
     w->ahi = (uint16_t *)take(c, (size_t)T * inter * 2);
     w->alo = prec == 0 ? (uint16_t *)take(c, (size_t)T * inter * 2) : NULL;
+    /* the GEMMs' K-slice sums (both GEMMs reuse it, one after the other) */
+    const size_t pg = k3k_dense_part_bytes(inter, T, hidden, 1), pd = k3k_dense_part_bytes(hidden, T, inter, 0);
+    w->part_bytes = pg > pd ? pg : pd;
+    w->part = (float *)take(c, w->part_bytes);
     return c->off;
 }
 
@@ -678,9 +684,11 @@ int k3d_shared_expert(float *y, int accumulate, const float *x, int T, const uin
     ShWs w;
     shared_layout(&c, &w, T, hidden, inter, prec);
     if (k3k_split_bf16(w.xhi, w.xlo, x, (size_t)T * hidden, stream)) return fail("split");
-    if (k3k_dense_gateup(w.ahi, w.alo, w1, w3, w.xhi, w.xlo, inter, T, hidden, act, b1, b2, stream))
+    if (k3k_dense_gateup(w.ahi, w.alo, w1, w3, w.xhi, w.xlo, inter, T, hidden, act, b1, b2, w.part,
+                         w.part_bytes, stream))
         return fail("shared gate/up");
-    if (k3k_dense_gemm(y, hidden, accumulate, w2, w.ahi, w.alo, hidden, T, inter, stream))
+    if (k3k_dense_gemm(y, hidden, accumulate, w2, w.ahi, w.alo, hidden, T, inter, w.part, w.part_bytes,
+                       stream))
         return fail("shared down");
     k3k_prof_mark(stream, K3D_STAGE_SHARED);
     return 0;

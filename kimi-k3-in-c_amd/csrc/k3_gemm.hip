@@ -11,25 +11,36 @@
  * arrive as one bf16 term (2e-2 bar) or two (hi + lo, x = hi + lo within 2^-17|x|, the
  * 1e-4 ||ref||inf bar), each term one v_mfma_f32_16x16x32_bf16 into the same accumulator.
  *
- * A workgroup of 4 waves (2 x 2) owns a tile of 128 weight rows x BN tokens and walks K 64
- * columns at a time. Each step's A (128 x 64) and B (BN x 64 per term) tiles are loaded
- * from global memory with 16-byte buffer loads (8 consecutive lanes read one row's 128
- * contiguous bytes; rows past R or T read zeros), kept in registers while the MFMAs consume
- * the previous step from LDS, then stored into the other half of a double-buffered LDS
- * (rows padded to 72 elements so the fragment reads of 16 rows spread over the banks); one
- * barrier per step. A wave owns 64 rows x BN/2 tokens: 4 x BN/32 MFMA tiles.
+ * A workgroup of 4 waves (2 x 2) owns a tile of 128 weight rows x BN tokens (BN = 128 with
+ * one activation term, 64 with two) and walks its K range 64 columns at a time. A wave owns
+ * 64 rows x BN/2 tokens, 4 x BN/32 accumulator blocks: per 32 columns it reads 4 weight and
+ * BN/32 (per term) activation fragments from LDS for 16 MFMAs, so the LDS delivers what the
+ * matrix cores consume. Each 64-column step's A (128 x 64) and B (BN x 64 per term) tiles
+ * come from global memory with 16-byte buffer loads (8 consecutive lanes read one row's
+ * 128 contiguous bytes; rows past R or T read zeros from beyond the buffer), two steps ahead
+ * in a ring of two register slots, and are stored into a double-buffered LDS (rows padded
+ * to 72 elements: the 16 rows of a fragment read start 36 banks apart, so a 16-lane
+ * group's 16-byte reads cover the 64 banks once); one barrier per step.
+ *
+ * When the tiles cannot give every CU two workgroups, K is split into S slices (at least
+ * 256 columns each): slice s writes its fp32 sums to part[s][t][col], and a second kernel
+ * adds the slices in order and finishes (the activation, or the write / accumulation of
+ * y). Without a partials buffer S is 1 and the GEMM kernel finishes itself.
  *
  * GATEUP: the 128 rows are 64 gate rows (W = w_gate) and the same 64 rows of w_up, laid out
- * so that every wave holds 32 gate and the matching 32 up rows; the epilogue applies the
- * activation to each (gate, up) pair in registers and writes it as bf16 term(s) [T][R], the
- * input of the next GEMM. PLAIN writes or accumulates fp32 Y with row stride ldy.
+ * so that every wave holds 32 gate and the matching 32 up rows; the activation is applied to
+ * each (gate, up) pair and written as bf16 term(s) [T][R], the input of the next GEMM (with
+ * slices, part columns 0..R-1 hold gate sums and R..2R-1 up sums). PLAIN writes or
+ * accumulates fp32 Y with row stride ldy.
  *
  * Tiles are ordered row block major, token block minor, and dealt to the 8 XCDs in
- * contiguous ranges (workgroup b runs on XCD b % 8), so the token blocks that share a weight
- * row block run on one XCD and read it through one L2.
+ * contiguous ranges (workgroup b runs on XCD b % 8), so the token blocks and slices that
+ * share a weight row block run on one XCD and read it through one L2.
  */
 #include "k3_common.h"
 #include "k3k.h"
+
+#include <type_traits>
 
 namespace {
 
@@ -46,13 +57,16 @@ struct DgArgs {
     uint16_t *ahi, *alo;              /* GATEUP output [T][R] (alo may be null) */
     int act;
     float b1, b2;
-    int ntr, ntt, per_xcd;            /* row blocks, token blocks, tiles per XCD */
+    float *part;                      /* nsl > 1: [nsl][T][ncol] fp32 slice sums */
+    int nsl, ncol;                    /* K slices; part columns (R, or 2R for GATEUP) */
+    int ntr, ntt, per_xcd;            /* row blocks, token blocks, work items per XCD */
 };
 
 template <int MODE, int NS, int BN>
-__global__ __launch_bounds__(256) void dense_gemm_kernel(DgArgs a)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void dense_gemm_kernel(DgArgs a)
 {
     constexpr int NJ = BN / 32;                    /* token fragments per wave */
+    constexpr int NA = DG_BM * 8 / 256, NB = BN * 8 / 256;   /* 16-byte chunks per thread */
     __shared__ __attribute__((aligned(16))) uint16_t As[2][DG_BM * DG_LD];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NS][BN * DG_LD];
 
@@ -62,12 +76,15 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DgArgs a)
     const int g = lane >> 4, r16 = lane & 15;
 
     const int xcd = blockIdx.x % K3_NXCD;
-    const int tile = xcd * a.per_xcd + (int)blockIdx.x / K3_NXCD;
-    if (tile >= a.ntr * a.ntt) return;
+    const int item = xcd * a.per_xcd + (int)blockIdx.x / K3_NXCD;
+    if (item >= a.ntr * a.ntt * a.nsl) return;
+    const int sl = item % a.nsl, tile = item / a.nsl;
     const int rb = tile / a.ntt, tb = tile % a.ntt;
     const int tok0 = tb * BN;
     /* first weight row of this tile in w0 (and w1): GATEUP tiles cover 64 rows of each */
     const int row0 = MODE == K3K_MX_GATEUP ? rb * (DG_BM / 2) : rb * DG_BM;
+    const int nks_all = a.K / DG_KS;
+    const int ks0 = sl * nks_all / a.nsl, nks = (sl + 1) * nks_all / a.nsl - ks0;
 
     const uint32_t Kb = (uint32_t)a.K * 2u;        /* bytes per row */
     const k3_rsrc rw0 = k3_make_rsrc(a.w0, (uint32_t)a.R * Kb);
@@ -76,51 +93,53 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DgArgs a)
     const k3_rsrc rxl = k3_make_rsrc(NS == 2 ? a.xlo : a.xhi, (uint32_t)a.T * Kb);
 
     /* global -> register staging: thread tid loads chunk c = tid + 256 i of a tile, row
-     * c / 8, 16-byte column c % 8 */
-    constexpr int NA = DG_BM * 8 / 256, NB = BN * 8 / 256;
-    uint4 ra[NA], rbh[NB], rbl[NS == 2 ? NB : 1];
-    uint32_t aoff[NA], boff[NB];
-    /* Rows past R or T get an offset at 2^31, beyond every operand (each is < 2 GiB): the
-     * buffer loads return zeros there. Chunk i of thread tid lies in rows 32i..32i+31, so
-     * for GATEUP the first half of the chunks are gate rows and the second half up rows. */
+     * c / 8, 16-byte column c % 8. Rows past R or T, and steps past the slice, get an offset
+     * at 2^31, beyond every operand (each is < 2 GiB): the buffer loads return zeros there,
+     * and no load sits under a branch. Chunk i of thread tid lies in rows 32i..32i+31, so for
+     * GATEUP the first half of the chunks are gate rows and the second half up rows. */
     constexpr uint32_t OOB = 0x80000000u;
+    uint32_t aoff[NA], boff[NB];
 #pragma unroll
     for (int i = 0; i < NA; i++) {
         const int c = tid + 256 * i, row = c >> 3, col = c & 7;
         const int wrow = MODE == K3K_MX_GATEUP ? row0 + (row & (DG_BM / 2 - 1)) : row0 + row;
-        aoff[i] = wrow < a.R ? (uint32_t)wrow * Kb + (uint32_t)col * 16u : OOB;
+        aoff[i] = wrow < a.R ? (uint32_t)wrow * Kb + (uint32_t)(ks0 * DG_KS * 2) + (uint32_t)col * 16u : OOB;
     }
 #pragma unroll
     for (int i = 0; i < NB; i++) {
         const int c = tid + 256 * i, row = c >> 3, col = c & 7;
         const int t = tok0 + row;
-        boff[i] = t < a.T ? (uint32_t)t * Kb + (uint32_t)col * 16u : OOB;
+        boff[i] = t < a.T ? (uint32_t)t * Kb + (uint32_t)(ks0 * DG_KS * 2) + (uint32_t)col * 16u : OOB;
     }
-    auto gload = [&](int ks) {
+    uint4 ra[2][NA], rbh[2][NB], rbl[2][NS == 2 ? NB : 1];
+    auto gload = [&](int ks, auto slot) {
+        constexpr int S = decltype(slot)::value;
+        const bool in = ks < nks;
         const uint32_t kb = (uint32_t)ks * (DG_KS * 2);
 #pragma unroll
         for (int i = 0; i < NA; i++) {
-            const uint32_t o = aoff[i] == OOB ? OOB : aoff[i] + kb;
-            ra[i] = (MODE == K3K_MX_GATEUP && i >= NA / 2) ? k3_bload16(rw1, o) : k3_bload16(rw0, o);
+            const uint32_t o = (aoff[i] == OOB || !in) ? OOB : aoff[i] + kb;
+            ra[S][i] = (MODE == K3K_MX_GATEUP && i >= NA / 2) ? k3_bload16(rw1, o) : k3_bload16(rw0, o);
         }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
-            const uint32_t o = boff[i] == OOB ? OOB : boff[i] + kb;
-            rbh[i] = k3_bload16(rxh, o);
-            if (NS == 2) rbl[i] = k3_bload16(rxl, o);
+            const uint32_t o = (boff[i] == OOB || !in) ? OOB : boff[i] + kb;
+            rbh[S][i] = k3_bload16(rxh, o);
+            if (NS == 2) rbl[S][i] = k3_bload16(rxl, o);
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int buf, auto slot) {
+        constexpr int S = decltype(slot)::value;
 #pragma unroll
         for (int i = 0; i < NA; i++) {
             const int c = tid + 256 * i;
-            *reinterpret_cast<uint4 *>(&As[buf][(c >> 3) * DG_LD + (c & 7) * 8]) = ra[i];
+            *reinterpret_cast<uint4 *>(&As[buf][(c >> 3) * DG_LD + (c & 7) * 8]) = ra[S][i];
         }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
             const int c = tid + 256 * i;
-            *reinterpret_cast<uint4 *>(&Bs[buf][0][(c >> 3) * DG_LD + (c & 7) * 8]) = rbh[i];
-            if (NS == 2) *reinterpret_cast<uint4 *>(&Bs[buf][NS - 1][(c >> 3) * DG_LD + (c & 7) * 8]) = rbl[i];
+            *reinterpret_cast<uint4 *>(&Bs[buf][0][(c >> 3) * DG_LD + (c & 7) * 8]) = rbh[S][i];
+            if (NS == 2) *reinterpret_cast<uint4 *>(&Bs[buf][NS - 1][(c >> 3) * DG_LD + (c & 7) * 8]) = rbl[S][i];
         }
     };
 
@@ -138,13 +157,15 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DgArgs a)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = k3_f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nks = a.K / DG_KS;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int ks = 0; ks < nks; ks++) {
-        const int buf = ks & 1;
-        if (ks + 1 < nks) gload(ks + 1);
+    using R0 = std::integral_constant<int, 0>;
+    using R1 = std::integral_constant<int, 1>;
+    /* step ks: its ring slot (ks & 1) is free once it is in LDS, so ks + 2 loads into it;
+     * ks is multiplied out of LDS buffer ks & 1 and ks + 1 stored into the other (past the
+     * slice the slot holds zeros and that buffer is not read again) */
+    auto step = [&](int ks, auto slot) {
+        constexpr int S = decltype(slot)::value;
+        const int buf = S;
+        gload(ks + 2, slot);
 #pragma unroll
         for (int kk = 0; kk < DG_KS; kk += 32) {
             k3_bf16x8 af[4], bf[NS][NJ];
@@ -165,15 +186,45 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DgArgs a)
                     for (int s = 0; s < NS; s++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[s][j], acc[i][j], 0, 0, 0);
         }
-        if (ks + 1 < nks) lstore(buf ^ 1);
+        lstore(buf ^ 1, std::integral_constant<int, S ^ 1>{});
         __syncthreads();
+    };
+    gload(0, R0{});
+    gload(1, R1{});
+    lstore(0, R0{});
+    __syncthreads();
+    /* whole pairs in the loop, so that no load or store sits under a branch there */
+    int ks = 0;
+    for (; ks + 1 < nks; ks += 2) {
+        step(ks, R0{});
+        step(ks + 1, R1{});
     }
+    if (ks < nks) step(ks, R0{});
 
     /* epilogue: lane holds token column r16 and rows 4g..4g+3 of each 16 x 16 tile */
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int t = tok0 + bcol0 + 16 * j + r16;
         if (t >= a.T) continue;
+        if (a.nsl > 1) {
+            /* this slice's sums, in order of the part columns */
+            float *p = a.part + ((size_t)sl * a.T + t) * a.ncol;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int lr = arow[i] + 4 * g;          /* row inside the tile */
+                const int col = MODE == K3K_MX_GATEUP
+                                    ? (lr < DG_BM / 2 ? row0 + lr : a.R + row0 + lr - DG_BM / 2)
+                                    : row0 + lr;
+                const int rr = MODE == K3K_MX_GATEUP ? (lr < DG_BM / 2 ? row0 + lr : row0 + lr - DG_BM / 2) : col;
+                if (rr + 3 < a.R)
+                    *reinterpret_cast<float4 *>(p + col) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+                else
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (rr + e < a.R) p[col + e] = acc[i][j][e];
+            }
+            continue;
+        }
         if (MODE == K3K_MX_GATEUP) {
 #pragma unroll
             for (int i = 0; i < 2; i++) {
@@ -206,34 +257,101 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DgArgs a)
     }
 }
 
+/* The slices' sums added in slice order, then the GEMM's finish: GATEUP applies the
+ * activation to (gate, up) and writes its bf16 term(s); PLAIN writes or accumulates y. One
+ * thread per (token, 4 consecutive rows); R % 4 == 0. */
+template <int MODE>
+__global__ __launch_bounds__(256) void dense_finish_kernel(DgArgs a)
+{
+    const int n4 = a.R >> 2;
+    const size_t total = (size_t)a.T * n4;
+    for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < total; k += (size_t)gridDim.x * blockDim.x) {
+        const int t = (int)(k / n4), r = (int)(k % n4) * 4;
+        const size_t slice = (size_t)a.T * a.ncol;
+        const float *p = a.part + (size_t)t * a.ncol;
+        float4 s = *reinterpret_cast<const float4 *>(p + r);
+        float4 u = MODE == K3K_MX_GATEUP ? *reinterpret_cast<const float4 *>(p + a.R + r) : s;
+        for (int q = 1; q < a.nsl; q++) {
+            const float4 v = *reinterpret_cast<const float4 *>(p + q * slice + r);
+            s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+            if (MODE == K3K_MX_GATEUP) {
+                const float4 w = *reinterpret_cast<const float4 *>(p + q * slice + a.R + r);
+                u.x += w.x; u.y += w.y; u.z += w.z; u.w += w.w;
+            }
+        }
+        if (MODE == K3K_MX_GATEUP) {
+            const float gv[4] = {s.x, s.y, s.z, s.w}, uv[4] = {u.x, u.y, u.z, u.w};
+            uint16_t hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) k3_split2(k3_act_pair(gv[e], uv[e], a.act, a.b1, a.b2), hi[e], lo[e]);
+            *reinterpret_cast<uint2 *>(a.ahi + (size_t)t * a.R + r) =
+                make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+            if (a.alo)
+                *reinterpret_cast<uint2 *>(a.alo + (size_t)t * a.R + r) =
+                    make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+        } else {
+            float *o = a.y + (size_t)t * a.ldy + r;
+            const float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = a.accumulate ? o[e] + sv[e] : sv[e];
+        }
+    }
+}
+
+/* K slices: enough for two workgroups per CU, each slice at least 256 columns (4 steps);
+ * 1 without a large enough partials buffer or when the output rows are not a multiple of 4. */
+static int dense_slices(int tiles, int K, int R, int T, int ncol, size_t part_bytes)
+{
+    if (R % 4) return 1;
+    const long want = 2L * k3k_cu_count();
+    int s = 1;
+    while (s < 8 && (long)tiles * s < want && K / DG_KS / (2 * s) >= 4 &&
+           (size_t)(2 * s) * T * ncol * 4 <= part_bytes)
+        s *= 2;
+    return s;
+}
+
 template <int MODE, int NS, int BN>
-int launch_dense(DgArgs a, hipStream_t st)
+int launch_dense(DgArgs a, size_t part_bytes, hipStream_t st)
 {
     const int rows_per_tile = MODE == K3K_MX_GATEUP ? DG_BM / 2 : DG_BM;
     a.ntr = (a.R + rows_per_tile - 1) / rows_per_tile;
     a.ntt = (a.T + BN - 1) / BN;
     const int tiles = a.ntr * a.ntt;
-    a.per_xcd = (tiles + K3_NXCD - 1) / K3_NXCD;
+    a.ncol = MODE == K3K_MX_GATEUP ? 2 * a.R : a.R;
+    a.nsl = a.part ? dense_slices(tiles, a.K, a.R, a.T, a.ncol, part_bytes) : 1;
+    const int items = tiles * a.nsl;
+    a.per_xcd = (items + K3_NXCD - 1) / K3_NXCD;
     hipLaunchKernelGGL((dense_gemm_kernel<MODE, NS, BN>), dim3((unsigned)(a.per_xcd * K3_NXCD)), dim3(256),
                        0, st, a);
     K3K_LAUNCH_CHECK("dense gemm launch");
+    if (a.nsl > 1) {
+        const size_t n = (size_t)a.T * (a.R / 4);
+        const size_t blocks = (n + 255) / 256;
+        hipLaunchKernelGGL(dense_finish_kernel<MODE>, dim3(blocks < 65536 ? (unsigned)blocks : 65536u), dim3(256),
+                           0, st, a);
+        K3K_LAUNCH_CHECK("dense finish launch");
+    }
     return 0;
 }
 
-/* Token block: 64 tokens while the tiles cannot fill the chip's 256 CUs, else 128. */
+/* Token block: 128 tokens with one activation term, 64 with two (the same registers). */
 template <int MODE, int NS>
-int dispatch_dense(const DgArgs &a, hipStream_t st)
+int dispatch_dense(const DgArgs &a, size_t part_bytes, hipStream_t st)
 {
-    const int rows_per_tile = MODE == K3K_MX_GATEUP ? DG_BM / 2 : DG_BM;
-    const long tiles128 = (long)((a.R + rows_per_tile - 1) / rows_per_tile) * ((a.T + 127) / 128);
-    if (tiles128 >= 512) return launch_dense<MODE, NS, 128>(a, st);
-    return launch_dense<MODE, NS, 64>(a, st);
+    return NS == 1 ? launch_dense<MODE, NS, 128>(a, part_bytes, st) : launch_dense<MODE, NS, 64>(a, part_bytes, st);
 }
 
 }  // namespace
 
-extern "C" int k3k_dense_gemm(float *y, int ldy, int accumulate, const uint16_t *W,
-                              const uint16_t *xhi, const uint16_t *xlo, int R, int T, int K,
+extern "C" size_t k3k_dense_part_bytes(int R, int T, int K, int gateup)
+{
+    if (R <= 0 || T <= 0 || K <= 0) return 0;
+    return (size_t)8 * T * (gateup ? 2 * (size_t)R : (size_t)R) * 4;
+}
+
+extern "C" int k3k_dense_gemm(float *y, int ldy, int accumulate, const uint16_t *W, const uint16_t *xhi,
+                              const uint16_t *xlo, int R, int T, int K, float *part, size_t part_bytes,
                               void *stream)
 {
     if (R <= 0 || T <= 0) return 0;
@@ -250,13 +368,14 @@ extern "C" int k3k_dense_gemm(float *y, int ldy, int accumulate, const uint16_t 
     a.y = y;
     a.ldy = ldy;
     a.accumulate = accumulate;
-    return xlo ? dispatch_dense<K3K_MX_PLAIN, 2>(a, (hipStream_t)stream)
-               : dispatch_dense<K3K_MX_PLAIN, 1>(a, (hipStream_t)stream);
+    a.part = ((uintptr_t)part % 16 || ldy % 4 || (uintptr_t)y % 16) ? nullptr : part;
+    return xlo ? dispatch_dense<K3K_MX_PLAIN, 2>(a, part_bytes, (hipStream_t)stream)
+               : dispatch_dense<K3K_MX_PLAIN, 1>(a, part_bytes, (hipStream_t)stream);
 }
 
 extern "C" int k3k_dense_gateup(uint16_t *ahi, uint16_t *alo, const uint16_t *wg, const uint16_t *wu,
                                 const uint16_t *xhi, const uint16_t *xlo, int R, int T, int K, int act,
-                                float b1, float b2, void *stream)
+                                float b1, float b2, float *part, size_t part_bytes, void *stream)
 {
     if (R <= 0 || T <= 0) return 0;
     if (K <= 0 || K % DG_KS) return k3k_fail("dense gate/up: K must be a multiple of 64", hipErrorInvalidValue);
@@ -275,6 +394,7 @@ extern "C" int k3k_dense_gateup(uint16_t *ahi, uint16_t *alo, const uint16_t *wg
     a.act = act;
     a.b1 = b1;
     a.b2 = b2;
-    return xlo ? dispatch_dense<K3K_MX_GATEUP, 2>(a, (hipStream_t)stream)
-               : dispatch_dense<K3K_MX_GATEUP, 1>(a, (hipStream_t)stream);
+    a.part = ((uintptr_t)part % 16 || (uintptr_t)ahi % 8 || (alo && (uintptr_t)alo % 8)) ? nullptr : part;
+    return xlo ? dispatch_dense<K3K_MX_GATEUP, 2>(a, part_bytes, (hipStream_t)stream)
+               : dispatch_dense<K3K_MX_GATEUP, 1>(a, part_bytes, (hipStream_t)stream);
 }

@@ -580,7 +580,7 @@ static void mmw_dev(float *y_d, const float *x_d, int ntok, const void *W, int w
         uint16_t *xs = (uint16_t *)buf(B_XS, (size_t)ntok * in * 4);
         uint16_t *xl = xs + (size_t)ntok * in;
         check(k3k_split_bf16(xs, xl, x_d, (size_t)ntok * in, g_stream), "activation split");
-        rc = k3k_dense_gemm(y_d, ldy, 0, (const uint16_t *)dw, xs, xl, out, ntok, in, g_stream);
+        rc = k3k_dense_gemm(y_d, ldy, 0, (const uint16_t *)dw, xs, xl, out, ntok, in, NULL, 0, g_stream);
     } else if (wdt == K3_WBF16) rc = k3k_gemv_bf16(y_d, x_d, (const uint16_t *)dw, in, out, ntok, ldy, g_stream);
     else if (wdt == K3_WI8) rc = k3k_gemv_q8(y_d, x_d, dw, in, out, ntok, ldy, g_stream);
     else rc = k3k_gemv_f32(y_d, x_d, (const float *)dw, in, out, ntok, ldy, g_stream);

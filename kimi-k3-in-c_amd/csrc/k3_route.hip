@@ -111,10 +111,16 @@ constexpr int RP_KS = 32, RP_SUB = 32;     /* chunk granule and bound sub-block,
  * (16 MT tokens x 16 ME experts), the 4 waves of a workgroup 2 x 2 of those. W and x are
  * staged in LDS as fp32 (rows padded to 36 floats: the 16-byte reads of 8 consecutive
  * lanes fall on distinct banks), double buffered, with the sub-block norms. The bound is
- * accumulated in fp32, rounded up at the end by its relative error ((nsub + 4) 2^-24). */
+ * accumulated in fp32, rounded up at the end by its relative error ((nsub + 4) 2^-24).
+ *
+ * The sub-blocks are loaded two ahead into a ring of two register slots. With BUF (rows
+ * a multiple of 4 floats, 16-byte aligned, W and x under 2 GiB) every load is a buffer
+ * load with no branch around it (rows and columns past the tile's read at an offset beyond
+ * the buffer: zeros), so each wait counts exactly the loads issued after the ones it waits
+ * for and sub-block sc + 2 stays in flight while sc is multiplied and sc + 1 stored. */
 constexpr int RM_LD = 36;
 
-template <int MT, int ME>
+template <int MT, int ME, bool BUF>
 __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, float *rbound,
                                                                   const float *x, int T,
                                                                   const float *W, int hidden,
@@ -133,7 +139,12 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
     const int kb0 = ks * chunk, kb1 = min(hidden, kb0 + chunk);
     const int nsub = (kb1 - kb0 + RP_KS - 1) / RP_KS;
     const float *Wt = W + (size_t)e0 * hidden, *xt = x + (size_t)t0 * hidden;
-    float4 wst[NWP], xst[NXP];
+    float4 wst[2][NWP], xst[2][NXP];                    /* the ring: two sub-blocks */
+    k3_rsrc rsw, rsx;
+    if constexpr (BUF) {
+        rsw = k3_make_rsrc(W, (uint32_t)((size_t)n_experts * hidden * 4));
+        rsx = k3_make_rsrc(x, (uint32_t)((size_t)T * hidden * 4));
+    }
     auto fetch = [&](const float *base, int rows_valid, int r, int k) {
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (r < rows_valid) {
@@ -148,21 +159,33 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
         }
         return v;
     };
+    /* rows of a multiple of 4 floats: a piece is wholly inside or past kb1 */
+    auto fetch_buf = [&](k3_rsrc rs, int row0, int rows_valid, int r, int k) {
+        const bool in = r < rows_valid && k < kb1;
+        const uint32_t off = in ? (uint32_t)(((size_t)(row0 + r) * hidden + k) * 4) : 0x80000000u;
+        return __builtin_bit_cast(float4, k3_bload16(rs, off));
+    };
     /* piece p = tid + 256 i: row p / 8, columns 4 (p % 8) .. + 3 */
-    auto load = [&](int sc) {
+    auto load = [&](int sc, auto slot) {
+        constexpr int S = decltype(slot)::value;
         const int k0 = kb0 + sc * RP_KS + (tid & 7) * 4;
 #pragma unroll
-        for (int i = 0; i < NWP; i++) wst[i] = fetch(Wt, n_experts - e0, (tid + 256 * i) >> 3, k0);
+        for (int i = 0; i < NWP; i++)
+            wst[S][i] = BUF ? fetch_buf(rsw, e0, n_experts - e0, (tid + 256 * i) >> 3, k0)
+                            : fetch(Wt, n_experts - e0, (tid + 256 * i) >> 3, k0);
 #pragma unroll
-        for (int i = 0; i < NXP; i++) xst[i] = fetch(xt, T - t0, (tid + 256 * i) >> 3, k0);
+        for (int i = 0; i < NXP; i++)
+            xst[S][i] = BUF ? fetch_buf(rsx, t0, T - t0, (tid + 256 * i) >> 3, k0)
+                            : fetch(xt, T - t0, (tid + 256 * i) >> 3, k0);
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf, auto slot) {
+        constexpr int S = decltype(slot)::value;
         const int c = (tid & 7) * 4;
 #pragma unroll
         for (int i = 0; i < NWP; i++) {
             const int r = (tid + 256 * i) >> 3;
-            *reinterpret_cast<float4 *>(&ws[buf][r * RM_LD + c]) = wst[i];
-            float a = fabsf(wst[i].x) + fabsf(wst[i].y) + fabsf(wst[i].z) + fabsf(wst[i].w);
+            *reinterpret_cast<float4 *>(&ws[buf][r * RM_LD + c]) = wst[S][i];
+            float a = fabsf(wst[S][i].x) + fabsf(wst[S][i].y) + fabsf(wst[S][i].z) + fabsf(wst[S][i].w);
             a += __shfl_xor(a, 1, 64);
             a += __shfl_xor(a, 2, 64);
             a += __shfl_xor(a, 4, 64);
@@ -171,14 +194,16 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
 #pragma unroll
         for (int i = 0; i < NXP; i++) {
             const int r = (tid + 256 * i) >> 3;
-            *reinterpret_cast<float4 *>(&xs[buf][r * RM_LD + c]) = xst[i];
-            float m = fmaxf(fmaxf(fabsf(xst[i].x), fabsf(xst[i].y)), fmaxf(fabsf(xst[i].z), fabsf(xst[i].w)));
+            *reinterpret_cast<float4 *>(&xs[buf][r * RM_LD + c]) = xst[S][i];
+            float m = fmaxf(fmaxf(fabsf(xst[S][i].x), fabsf(xst[S][i].y)), fmaxf(fabsf(xst[S][i].z), fabsf(xst[S][i].w)));
             m = fmaxf(m, __shfl_xor(m, 1, 64));
             m = fmaxf(m, __shfl_xor(m, 2, 64));
             m = fmaxf(m, __shfl_xor(m, 4, 64));
             if ((tid & 7) == 0) xn[buf][r] = m;
         }
     };
+    using R0 = std::integral_constant<int, 0>;
+    using R1 = std::integral_constant<int, 1>;
 
     const int q = l >> 4, r16 = l & 15;
     const int trow = wt * 16 * MT, erow = we * 16 * ME;  /* the wave's first token / expert */
@@ -193,12 +218,16 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
             for (int r = 0; r < 4; r++) rb[a][b][r] = 0.0f;
         }
 
-    load(0);
-    store(0);
+    load(0, R0{});
+    load(1, R1{});
+    store(0, R0{});
     __syncthreads();
-    for (int sc = 0; sc < nsub; sc++) {
-        const int buf = sc & 1;
-        if (sc + 1 < nsub) load(sc + 1);
+    /* sub-block sc: its ring slot (sc & 1) is free once it is in LDS, so sc + 2 loads into
+     * it; then sc is multiplied out of LDS buffer sc & 1 and sc + 1 stored into the other */
+    auto step = [&](int sc, auto slot) {
+        constexpr int S = decltype(slot)::value;
+        const int buf = S;
+        load(sc + 2, slot);
         /* bound term of this sub-block from the chains' values at its start: element
          * (i, j) of block (a, b) is token trow + 16 a + 4 r + q, expert erow + 16 b + r16 */
         {
@@ -241,9 +270,17 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
                         acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b], acc[a][b], 0, 0, 0);
             }
         }
-        if (sc + 1 < nsub) store(buf ^ 1);
+        /* past the chunk the slot holds zeros (BUF) and the buffer is not read again */
+        store(buf ^ 1, std::integral_constant<int, S ^ 1>{});
         __syncthreads();
+    };
+    /* whole pairs in the loop, so that no load or store sits under a branch there */
+    int sc = 0;
+    for (; sc + 1 < nsub; sc += 2) {
+        step(sc, R0{});
+        step(sc + 1, R1{});
     }
+    if (sc < nsub) step(sc, R0{});
     /* relative error of the fp32 bound: (nsub + 4) roundings of 2^-24, the float sums of
      * |w| at most 2^-18 */
     const double up = 1.0 + 0x1p-17 + (double)(nsub + 4) * 0x1p-24;
@@ -1211,8 +1248,14 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
     } else {
         static_assert(RM_TB == 32 * 1 && RM_EB == 32 * 2, "tile of router_partial_mfma_kernel<1, 2>");
         dim3 grid((n_experts + RM_EB - 1) / RM_EB, (T + RM_TB - 1) / RM_TB, ks);
-        hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2>), grid, dim3(256), 0, st, part, rbound,
-                           x, T, W, hidden, n_experts, chunk, vec);
+        const bool buf = vec && (size_t)n_experts * hidden * 4 < 0x80000000u &&
+                         (size_t)T * hidden * 4 < 0x80000000u;
+        if (buf)
+            hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, true>), grid, dim3(256), 0, st, part,
+                               rbound, x, T, W, hidden, n_experts, chunk, vec);
+        else
+            hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, false>), grid, dim3(256), 0, st, part,
+                               rbound, x, T, W, hidden, n_experts, chunk, vec);
     }
     K3K_LAUNCH_CHECK("router_partial launch");
     return 0;

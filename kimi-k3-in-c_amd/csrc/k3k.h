@@ -214,14 +214,20 @@ int k3k_act_split(uint16_t *hi, uint16_t *lo, const float *gu, int n, int rows, 
 /* ---- dense bf16 GEMM on the matrix cores (k3_gemm.hip) ------------------------------ */
 /* y[t][r] (= or, accumulate, +=) sum_k W[r][k] * (xhi + xlo)[t][k], t < T, r < R, row stride
  * ldy: W bf16 [R][K], activations as bf16 terms [T][K] (xlo NULL: one term), K % 64 == 0,
- * operands under 2 GiB. fp32 accumulation and output. */
+ * operands under 2 GiB. fp32 accumulation and output. part (16-byte aligned, part_bytes of
+ * it; may be NULL) lets the GEMM split K into slices when its tiles cannot fill the chip:
+ * slice sums go there and are added in slice order; k3k_dense_part_bytes(R, T, K, 0) bytes
+ * allow every split it chooses. */
 int k3k_dense_gemm(float *y, int ldy, int accumulate, const uint16_t *W, const uint16_t *xhi,
-                   const uint16_t *xlo, int R, int T, int K, void *stream);
+                   const uint16_t *xlo, int R, int T, int K, float *part, size_t part_bytes,
+                   void *stream);
 /* The dense SwiGLU's first half: act(W_gate x, W_up x) for rows r < R of both [R][K]
- * matrices, written as bf16 terms ahi (and alo when not NULL) [T][R]. */
+ * matrices, written as bf16 terms ahi (and alo when not NULL) [T][R]; part as above, sized
+ * by k3k_dense_part_bytes(R, T, K, 1). */
 int k3k_dense_gateup(uint16_t *ahi, uint16_t *alo, const uint16_t *wg, const uint16_t *wu,
                      const uint16_t *xhi, const uint16_t *xlo, int R, int T, int K, int act,
-                     float b1, float b2, void *stream);
+                     float b1, float b2, float *part, size_t part_bytes, void *stream);
+size_t k3k_dense_part_bytes(int R, int T, int K, int gateup);
 int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int rows, float eps,
                 void *stream);
 int k3k_axpy_rows(float *out, const float *add, size_t n, void *stream); /* out += add */
