@@ -166,6 +166,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         constexpr int S = decltype(slot)::value;
         const int buf = S;
         gload(ks + 2, slot);
+        /* issued here, ahead of the products (the compiler would otherwise sink them below
+         * the next LDS store and wait for step ks + 1 with nothing else in flight) */
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < DG_KS; kk += 32) {
             k3_bf16x8 af[4], bf[NS][NJ];
@@ -259,28 +262,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 
 /* The slices' sums added in slice order, then the GEMM's finish: GATEUP applies the
  * activation to (gate, up) and writes its bf16 term(s); PLAIN writes or accumulates y. One
- * thread per (token, 4 consecutive rows); R % 4 == 0. */
-template <int MODE>
+ * thread per (token, 4 consecutive rows); R % 4 == 0, y and ldy 16-byte aligned. Every
+ * slice's loads are issued before the first sum. */
+template <int MODE, int NSL>
 __global__ __launch_bounds__(256) void dense_finish_kernel(DgArgs a)
 {
     const int n4 = a.R >> 2;
     const size_t total = (size_t)a.T * n4;
+    const size_t slice = (size_t)a.T * a.ncol;
     for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < total; k += (size_t)gridDim.x * blockDim.x) {
         const int t = (int)(k / n4), r = (int)(k % n4) * 4;
-        const size_t slice = (size_t)a.T * a.ncol;
-        const float *p = a.part + (size_t)t * a.ncol;
-        float4 s = *reinterpret_cast<const float4 *>(p + r);
-        float4 u = MODE == K3K_MX_GATEUP ? *reinterpret_cast<const float4 *>(p + a.R + r) : s;
-        for (int q = 1; q < a.nsl; q++) {
-            const float4 v = *reinterpret_cast<const float4 *>(p + q * slice + r);
-            s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
-            if (MODE == K3K_MX_GATEUP) {
-                const float4 w = *reinterpret_cast<const float4 *>(p + q * slice + a.R + r);
-                u.x += w.x; u.y += w.y; u.z += w.z; u.w += w.w;
-            }
+        const float *p = a.part + (size_t)t * a.ncol + r;
+        k3_f32x4 gs[NSL], us[MODE == K3K_MX_GATEUP ? NSL : 1];
+#pragma unroll
+        for (int q = 0; q < NSL; q++) {
+            gs[q] = __builtin_nontemporal_load(reinterpret_cast<const k3_f32x4 *>(p + q * slice));
+            if (MODE == K3K_MX_GATEUP) us[q] = __builtin_nontemporal_load(reinterpret_cast<const k3_f32x4 *>(p + q * slice + a.R));
+        }
+        k3_f32x4 yv = {0.f, 0.f, 0.f, 0.f};
+        float *o = MODE == K3K_MX_GATEUP ? nullptr : a.y + (size_t)t * a.ldy + r;
+        if (MODE != K3K_MX_GATEUP && a.accumulate) yv = *reinterpret_cast<const k3_f32x4 *>(o);
+        k3_f32x4 s = gs[0], u = MODE == K3K_MX_GATEUP ? us[0] : gs[0];
+#pragma unroll
+        for (int q = 1; q < NSL; q++) {                /* slice order, one rounding each */
+            s += gs[q];
+            if (MODE == K3K_MX_GATEUP) u += us[q];
         }
         if (MODE == K3K_MX_GATEUP) {
-            const float gv[4] = {s.x, s.y, s.z, s.w}, uv[4] = {u.x, u.y, u.z, u.w};
+            const float gv[4] = {s[0], s[1], s[2], s[3]}, uv[4] = {u[0], u[1], u[2], u[3]};
             uint16_t hi[4], lo[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) k3_split2(k3_act_pair(gv[e], uv[e], a.act, a.b1, a.b2), hi[e], lo[e]);
@@ -290,10 +299,8 @@ __global__ __launch_bounds__(256) void dense_finish_kernel(DgArgs a)
                 *reinterpret_cast<uint2 *>(a.alo + (size_t)t * a.R + r) =
                     make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
         } else {
-            float *o = a.y + (size_t)t * a.ldy + r;
-            const float sv[4] = {s.x, s.y, s.z, s.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = a.accumulate ? o[e] + sv[e] : sv[e];
+            if (a.accumulate) s = yv + s;
+            *reinterpret_cast<k3_f32x4 *>(o) = s;
         }
     }
 }
@@ -328,8 +335,10 @@ int launch_dense(DgArgs a, size_t part_bytes, hipStream_t st)
     if (a.nsl > 1) {
         const size_t n = (size_t)a.T * (a.R / 4);
         const size_t blocks = (n + 255) / 256;
-        hipLaunchKernelGGL(dense_finish_kernel<MODE>, dim3(blocks < 65536 ? (unsigned)blocks : 65536u), dim3(256),
-                           0, st, a);
+        const dim3 grid(blocks < 65536 ? (unsigned)blocks : 65536u);
+        if (a.nsl == 2) hipLaunchKernelGGL((dense_finish_kernel<MODE, 2>), grid, dim3(256), 0, st, a);
+        else if (a.nsl == 4) hipLaunchKernelGGL((dense_finish_kernel<MODE, 4>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((dense_finish_kernel<MODE, 8>), grid, dim3(256), 0, st, a);
         K3K_LAUNCH_CHECK("dense finish launch");
     }
     return 0;
@@ -339,7 +348,8 @@ int launch_dense(DgArgs a, size_t part_bytes, hipStream_t st)
 template <int MODE, int NS>
 int dispatch_dense(const DgArgs &a, size_t part_bytes, hipStream_t st)
 {
-    return NS == 1 ? launch_dense<MODE, NS, 128>(a, part_bytes, st) : launch_dense<MODE, NS, 64>(a, part_bytes, st);
+    if constexpr (NS == 1) return launch_dense<MODE, NS, 128>(a, part_bytes, st);
+    else return launch_dense<MODE, NS, 64>(a, part_bytes, st);
 }
 
 }  // namespace
