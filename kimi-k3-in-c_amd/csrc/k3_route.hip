@@ -124,7 +124,8 @@ template <int MT, int ME, bool BUF>
 __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, float *rbound,
                                                                   const float *x, int T,
                                                                   const float *W, int hidden,
-                                                                  int n_experts, int chunk, int vec)
+                                                                  int n_experts, int chunk, int vec,
+                                                                  int nks_xcd)
 {
     typedef double d4 __attribute__((ext_vector_type(4)));
     constexpr int TB = 32 * MT, EB = 32 * ME;           /* workgroup tile: tokens, experts */
@@ -135,7 +136,19 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
     __shared__ float xn[2][TB];                          /* max |x| over the sub-block */
     const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
     const int wt = wv >> 1, we = wv & 1;                 /* the wave's block of the tile */
-    const int e0 = blockIdx.x * EB, t0 = blockIdx.y * TB, ks = blockIdx.z;
+    /* nks_xcd > 0 (a one-dimensional grid, nks_xcd chunks): the workgroups of one chunk run
+     * on one XCD (workgroup b runs on XCD b % 8), so that its W and x pieces are fetched
+     * into that XCD's L2 once instead of once per token tile / expert tile */
+    int bx = blockIdx.x, by = blockIdx.y, ks = blockIdx.z;
+    if (nks_xcd > 0) {
+        const int nee = (n_experts + EB - 1) / EB, g = nee * ((T + TB - 1) / TB);
+        const int i = blockIdx.x / K3_NXCD;
+        ks = blockIdx.x % K3_NXCD + K3_NXCD * (i / g);
+        if (ks >= nks_xcd) return;
+        bx = (i % g) % nee;
+        by = (i % g) / nee;
+    }
+    const int e0 = bx * EB, t0 = by * TB;
     const int kb0 = ks * chunk, kb1 = min(hidden, kb0 + chunk);
     const int nsub = (kb1 - kb0 + RP_KS - 1) / RP_KS;
     const float *Wt = W + (size_t)e0 * hidden, *xt = x + (size_t)t0 * hidden;
@@ -1153,17 +1166,28 @@ extern "C" int k3k_split_bf16(uint16_t *hi, uint16_t *lo, const float *x, size_t
 }
 
 /* Matrix-core partials: a workgroup covers RM_TB tokens x RM_EB experts (one 16 x 32
- * block per wave: 92 VGPRs, four workgroups per CU). */
+ * block per wave). */
 constexpr int RM_TB = 32, RM_EB = 64;
 
 extern "C" int k3k_router_chunk(int T, int hidden, int n_experts)
 {
     if (T <= RS_T) return RS_CH;          /* one lane per (expert, 128-column chunk) */
+    const long tiles = (long)((n_experts + RM_EB - 1) / RM_EB) * ((T + RM_TB - 1) / RM_TB);
+    const long cus = k3k_cu_count() > 0 ? k3k_cu_count() : 1;
+    /* Few tiles (small batches): a chunk count that is a multiple of the XCD count, so that
+     * each chunk's workgroups run on one XCD and fetch its W and x pieces once
+     * (router_partial_mfma_kernel's grouped grid), about 1.5 workgroups per CU, chunks of at
+     * least 224 columns */
+    if (tiles * K3_NXCD <= cus) {
+        long ks = ((3 * cus) / 2 + tiles - 1) / tiles;
+        ks = (ks + K3_NXCD - 1) / K3_NXCD * K3_NXCD;
+        while (ks > K3_NXCD && hidden / ks < 224) ks -= K3_NXCD;
+        const long chunk = ((hidden + ks - 1) / ks + RP_KS - 1) / RP_KS * RP_KS;
+        if (chunk >= 224 && ((hidden + chunk - 1) / chunk) % K3_NXCD == 0) return (int)chunk;
+    }
     /* chunks a multiple of 32 columns and at least 256; among those, the split whose
      * busiest CU has the least work (workgroups per CU x columns per workgroup), the most
      * workgroups among equals (a shorter tail) up to 12 per CU (more partials to sum) */
-    const long tiles = (long)((n_experts + RM_EB - 1) / RM_EB) * ((T + RM_TB - 1) / RM_TB);
-    const long cus = k3k_cu_count() > 0 ? k3k_cu_count() : 1;
     long kmax = (hidden + 255) / 256;
     if (kmax < 1) kmax = 1;
     long best_chunk = 0, best_load = -1;
@@ -1247,15 +1271,18 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
                                rbound, x, T, W, hidden, n_experts, vec);
     } else {
         static_assert(RM_TB == 32 * 1 && RM_EB == 32 * 2, "tile of router_partial_mfma_kernel<1, 2>");
-        dim3 grid((n_experts + RM_EB - 1) / RM_EB, (T + RM_TB - 1) / RM_TB, ks);
+        const int nee = (n_experts + RM_EB - 1) / RM_EB, ntt = (T + RM_TB - 1) / RM_TB;
+        /* a chunk count that is a multiple of the XCD count: the chunks dealt to the XCDs */
+        const int xg = (ks % K3_NXCD == 0) ? ks : 0;
+        const dim3 grid = xg ? dim3((unsigned)(nee * ntt * ks)) : dim3(nee, ntt, ks);
         const bool buf = vec && (size_t)n_experts * hidden * 4 < 0x80000000u &&
                          (size_t)T * hidden * 4 < 0x80000000u;
         if (buf)
             hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, true>), grid, dim3(256), 0, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec);
+                               rbound, x, T, W, hidden, n_experts, chunk, vec, xg);
         else
             hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, false>), grid, dim3(256), 0, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec);
+                               rbound, x, T, W, hidden, n_experts, chunk, vec, xg);
     }
     K3K_LAUNCH_CHECK("router_partial launch");
     return 0;
