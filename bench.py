@@ -144,6 +144,8 @@ def time_prefill(layer, T=4096, steps=3, warmup=1):
     flops = T * K * 3 * 2 * E * I                  # 2.886 TFLOP at T=4096
     expert_ms = sum(st.get(k, (0.0, 0))[0] for k in ("gateup", "down"))
     return {"tokens": T, "ms_per_step": round(ms, 3), "tokens_per_s": round(T / ms * 1e3, 1),
+            "arithmetic": "activations rounded to bf16 (one term), weights dequantized exactly, "
+                          "bf16 MFMA with fp32 accumulation; tolerance 2e-2 relative",
             "expert_flops": flops, "expert_ms": round(expert_ms, 3),
             "expert_TFLOPs": round(flops / (expert_ms * 1e-3) / 1e12, 1) if expert_ms else None,
             "mfma_frac_of_bf16_peak": round(flops / (expert_ms * 1e-3) / 2.5e15, 4) if expert_ms else None,
@@ -238,6 +240,8 @@ def time_skewed(layer, T=512, steps=5, warmup=1):
     sh_ms = st.get("shared", (0.0, 1))[0]
     sh_flops = T * 3 * 2 * E * I
     return {"tokens": T, "ms_per_step": round(ms, 3), "tokens_per_s": round(T / ms * 1e3, 1),
+            "arithmetic": "routed and shared experts with activations rounded to bf16 (one term), "
+                          "bf16 MFMA with fp32 accumulation; tolerance 2e-2 relative",
             "routing": {"unique_experts": int((cnt > 0).sum()), "max_tokens_per_expert": int(cnt[0]),
                         "mean_tokens_per_used_expert": round(float(cnt[cnt > 0].mean()), 2),
                         "share_top1": round(float(cnt[0] / cnt.sum()), 4),
@@ -591,6 +595,8 @@ def main():
                      "kernel": "mx_moe_kernel GATEUP (fused gate/up + SiLU, tiled bank)",
                      "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": "profiles/hbm_traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE "
+                                       "passes over this bench, scaled by a copy kernel of known size",
                      "kernel_ms": round(gu_ms, 4), "algorithmic_bytes": int(gu_bytes)},
         "layer_GBps": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
         "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in stages.items()},
