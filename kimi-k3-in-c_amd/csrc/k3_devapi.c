@@ -226,6 +226,7 @@ typedef struct {
     double *part;
     float *rbound;
     int *nrecomp;
+    int *ctr;                   /* the final kernel's arrival counter, when it gathers */
     int chunk;
 } RtWs;
 
@@ -237,6 +238,7 @@ static size_t router_layout(Carve *c, RtWs *w, int T, int hidden, int n_experts)
     w->part = (double *)take(c, (ks < 2 ? 2 : ks) * T * n_experts * 8);
     w->rbound = (float *)take(c, ks * T * n_experts * 4);
     w->nrecomp = (int *)take(c, (size_t)T * 4);
+    w->ctr = (int *)take(c, 4);
     return c->off;
 }
 
@@ -247,17 +249,24 @@ size_t k3d_router_ws(int T, int hidden, int n_experts)
     return router_layout(&c, &w, T, hidden, n_experts);
 }
 
+/* gather (may be NULL): the router's final kernel also runs the expert-major gather */
 static int router_run(int *idx, float *wt, const float *x, int T, const float *W,
                       const float *bias, int hidden, int n_experts, int topk, int renorm,
-                      float routed_scale, const RtWs *w, void *stream)
+                      float routed_scale, const RtWs *w, const K3kGatherArgs *gather, void *stream)
 {
     const K3kExc *exc;
     int rc = exc_table(&exc);
     if (rc) return rc;
-    if (k3k_router_partial(w->part, w->rbound, x, T, W, hidden, n_experts, w->chunk, exc, stream))
+    K3kGatherArgs g;
+    if (gather) {
+        g = *gather;
+        g.ctr = w->ctr;
+    }
+    if (k3k_router_partial(w->part, w->rbound, x, T, W, hidden, n_experts, w->chunk,
+                           gather ? w->ctr : NULL, exc, stream))
         return fail("router_partial");
     if (k3k_router_final(idx, wt, w->nrecomp, w->part, w->rbound, w->chunk, x, W, bias, T, hidden,
-                         n_experts, topk, renorm, routed_scale, exc, stream))
+                         n_experts, topk, renorm, routed_scale, exc, gather ? &g : NULL, stream))
         return fail("router_final");
     return 0;
 }
@@ -283,7 +292,7 @@ int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const
     Carve c = {(char *)ws, 0};
     RtWs w;
     router_layout(&c, &w, T, hidden, n_experts);
-    return router_run(idx, wt, x, T, W, bias, hidden, n_experts, topk, renorm, routed_scale, &w,
+    return router_run(idx, wt, x, T, W, bias, hidden, n_experts, topk, renorm, routed_scale, &w, NULL,
                       stream);
 }
 
@@ -417,7 +426,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
                           const void *bank, int layout, int hidden, int inter, int n_experts,
                           int topk, int act, float b1, float b2, int prec, const MoeWs *w,
                           int *perm_out, int *offsets_out, int *drops_out, const RouterSel *sel,
-                          int x_split, void *stream)
+                          int x_split, int gathered, void *stream)
 {
     int *perm = perm_out ? perm_out : w->perm;
     int *offsets = offsets_out ? offsets_out : w->offsets;
@@ -488,7 +497,9 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     /* (the routed layer runs the split beside its router, on the side stream) */
     if (!x_split && k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
     const int pass_tok2 = moe_pass_tok2(pass_tok, layout, prec);
-    if (k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
+    /* (gathered: the router's final kernel has run the gather) */
+    if (!gathered &&
+        k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
                    w->pass_job2, w->pass_tp2, w->counts, w->ghist, idx, T, topk, n_experts, bank,
                    pass_tok, pass_tok2, stream))
         return fail("gather");
@@ -572,7 +583,7 @@ int k3d_moe_experts(float *out, const int *idx, const float *wt, const float *x,
     moe_layout(&c, &w, T, hidden, inter, n_experts, topk, prec);
     k3k_prof_mark(stream, K3D_STAGE_BEGIN);
     return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
-                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, 0, stream);
+                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, 0, 0, stream);
 }
 
 int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const float *router_w,
@@ -599,12 +610,13 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
         const K3kExc *exc;
         rc = exc_table(&exc);
         if (rc) return rc;
-        if (k3k_router_partial(r.part, r.rbound, x, T, router_w, hidden, n_experts, r.chunk, exc, stream))
+        if (k3k_router_partial(r.part, r.rbound, x, T, router_w, hidden, n_experts, r.chunk, NULL,
+                               exc, stream))
             return fail("router_partial");
         k3k_prof_mark(stream, K3D_STAGE_ROUTER);
         const RouterSel sel = {r.part, router_w, bias, renorm, routed_scale, exc, r.nrecomp, idx, wt};
         return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
-                              b1, b2, prec, &w, NULL, NULL, drops_out, &sel, 0, stream);
+                              b1, b2, prec, &w, NULL, NULL, drops_out, &sel, 0, 0, stream);
     }
     /* past the decode path the expert kernels take the tokens' bf16 split: it depends on x
      * alone, so it runs on the side stream beside the router (event fork / join, captured by
@@ -615,13 +627,36 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
         if (k3k_fork(stream, &side)) return fail("fork");
         if (k3k_split_bf16(w.xhi, w.xlo, x, (size_t)T * hidden, side)) return fail("split");
     }
+    /* the expert-major gather runs in the router's final kernel when it can (a launch and its
+     * gap fewer): the last of its workgroups to finish sorts every token's idx */
+    const int gathered = split && k3k_router_gathers(T, hidden, n_experts, topk);
+    K3kGatherArgs ga;
+    if (gathered) {
+        const int pass_tok = moe_pass_tok(T, hidden, inter, n_experts, topk, prec, layout);
+        ga.offsets = offsets_out ? offsets_out : w.offsets;
+        ga.perm = perm_out ? perm_out : w.perm;
+        ga.job_expert = w.job_expert;
+        ga.job_off = w.job_off;
+        ga.job_cnt = w.job_cnt;
+        ga.pass_job = w.pass_job;
+        ga.pass_tp = w.pass_tp;
+        ga.pass_job2 = w.pass_job2;
+        ga.pass_tp2 = w.pass_tp2;
+        ga.counts = w.counts;
+        ga.bank = bank;
+        ga.topk = topk;
+        ga.pass_tok = pass_tok;
+        ga.pass_tok2 = moe_pass_tok2(pass_tok, layout, prec);
+        ga.ctr = r.ctr;
+    }
     rc = router_run(idx, wt, x, T, router_w, bias, hidden, n_experts, topk, renorm, routed_scale,
-                    &r, stream);
+                    &r, gathered ? &ga : NULL, stream);
     if (rc) return rc;
     if (split && k3k_join(stream)) return fail("join");
     k3k_prof_mark(stream, K3D_STAGE_ROUTER);
     return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
-                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, split, stream);
+                          b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, split, gathered,
+                          stream);
 }
 
 /* ---- tiled expert layout ---------------------------------------------------------------- */

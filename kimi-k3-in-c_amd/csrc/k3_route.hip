@@ -125,8 +125,10 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
                                                                   const float *x, int T,
                                                                   const float *W, int hidden,
                                                                   int n_experts, int chunk, int vec,
-                                                                  int nks_xcd)
+                                                                  int nks_xcd, int *ctr)
 {
+    /* the final kernel's arrival counter starts every launch at zero */
+    if (ctr && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) *ctr = 0;
     typedef double d4 __attribute__((ext_vector_type(4)));
     constexpr int TB = 32 * MT, EB = 32 * ME;           /* workgroup tile: tokens, experts */
     constexpr int NWP = EB / 32, NXP = TB / 32;         /* float4 pieces per thread: W, x */
@@ -649,13 +651,26 @@ __global__ __launch_bounds__(256) void router_small_kernel(float4 *pre, const fl
 /* router_final_kernel: up to RF_MAXE experts, RF_MAXW waves; RF_KB chunk partials per load batch. */
 constexpr int RF_MAXE = 2048, RF_MAXW = 16, RF_KB = 32;
 
+/* The expert-major gather's operands (gather_block). ctr: the arrival counter of the
+ * router's final kernel when that kernel runs the gather itself. */
+struct GatherDev {
+    int *offsets, *perm, *job_expert, *job_off, *job_cnt, *pass_job, *pass_tp, *pass_job2, *pass_tp2;
+    int *counts;
+    const int *idx;
+    const void *bank;
+    int N, n_experts, pass_tok, pass_tok2;
+    int *ctr;
+};
+template <bool COH>
+__device__ void gather_block(const GatherDev &g);
+
 /* One workgroup per token: every thread certifies and scores SL experts (tid + nthr i) --
  * from router_small_kernel's scored records (PRE) or from the chunk partials, summed in
  * k order and certified here (certify_score) -- into LDS; then select_rounds (wave 0
  * selects, the workgroup recomputes what matters) and select_weight; renormalise and
  * scale (k3_ops.c:459-475). nrecomp[t] (optional) counts recomputes. KB: chunk partials
  * loaded per batch. */
-template <int SL, int SW, int KB, bool PRE>
+template <int SL, int SW, int KB, bool PRE, bool GATHER = false>
 __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int *idx, float *wt, int *nrecomp,
                                                             const double *part,
                                                             const float *rbound, int ksplit,
@@ -663,7 +678,8 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
                                                             const float *W, const float *bias,
                                                             int T, int hidden, int n_experts,
                                                             int topk, int renorm,
-                                                            float routed_scale, ExcTable exc)
+                                                            float routed_scale, ExcTable exc,
+                                                            GatherDev g)
 {
     __shared__ SelSmem<SW> sm;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -716,10 +732,31 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
         float w;
         select_weight<SW>(sm, mysel, topk, renorm, routed_scale, id, w);
         if (lane < topk) {
-            idx[(size_t)t * topk + lane] = id >= 0 ? id : 0;
+            if (GATHER)   /* written through to where every XCD's gather reads it */
+                __hip_atomic_store(idx + (size_t)t * topk + lane, id >= 0 ? id : 0, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            else
+                idx[(size_t)t * topk + lane] = id >= 0 ? id : 0;
             wt[(size_t)t * topk + lane] = w;
         }
         if (nrecomp && lane == 0) nrecomp[t] = nre;
+    }
+    if constexpr (GATHER) {
+        /* The workgroup that finishes last runs the gather over every token's idx: each
+         * workgroup's idx stores are acknowledged (vmcnt 0) before it counts itself in, and
+         * the last one reads idx with agent-scope loads. It leaves the counter at zero (the
+         * partial kernel zeroes it before every launch as well). */
+        __shared__ int s_last;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0)
+            s_last = __hip_atomic_fetch_add(g.ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (int)gridDim.x - 1;
+        __syncthreads();
+        if (s_last) {
+            gather_block<true>(g);
+            if (tid == 0) __hip_atomic_store(g.ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -835,38 +872,46 @@ __device__ void gather_plan(const int *cnt, int *fill, int (*wtot5)[5], int *off
     __syncthreads();
 }
 
-__global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, int *job_expert,
-                                                      int *job_off, int *job_cnt, int *pass_job,
-                                                      int *pass_tp, int *pass_job2, int *pass_tp2,
-                                                      int *counts, const int *idx, int N,
-                                                      int n_experts, const void *bank,
-                                                      int pass_tok, int pass_tok2)
+/* The one-workgroup gather (1024 threads); COH: idx was written during this launch by other
+ * workgroups (agent-scope stores), so it is read with agent-scope loads. */
+template <bool COH>
+__device__ void gather_block(const GatherDev &g)
 {
+    int *offsets = g.offsets, *perm = g.perm;
+    const int N = g.N, n_experts = g.n_experts;
+    auto idx_at = [&](int a) {
+        return COH ? __hip_atomic_load(const_cast<int *>(g.idx) + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : g.idx[a];
+    };
     __shared__ int cnt[G_MAXE];
     __shared__ int fill[G_MAXE];
     __shared__ int wtot5[16][5];
     __shared__ unsigned char pres[G_MAXE];
     __shared__ unsigned short wcnt[16][G_WCNT_E];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    /* the bank entries' presence, loaded beside the counting */
+    /* A thread's first two assignments' experts are loaded once, together with the bank
+     * entries' presence, and serve both the counting and the placement (a batch of more
+     * than 2048 assignments reads the rest again where it needs them). */
+    const int ev0 = tid < N ? idx_at(tid) : -1;
+    const int ev1 = tid + 1024 < N ? idx_at(tid + 1024) : -1;
     for (int e = tid; e < n_experts; e += 1024) {
         cnt[e] = 0;
-        pres[e] = expert_present(bank, e) ? 1 : 0;
+        pres[e] = expert_present(g.bank, e) ? 1 : 0;
     }
     __syncthreads();
     for (int a = tid; a < N; a += 1024) {
-        const int e = idx[a];
+        const int e = a == tid ? ev0 : a == tid + 1024 ? ev1 : idx_at(a);
         if (e >= 0 && e < n_experts) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    gather_plan(cnt, fill, wtot5, offsets, job_expert, job_off, job_cnt, pass_job, pass_tp,
-                pass_job2, pass_tp2, counts, n_experts, pres, pass_tok, pass_tok2);
+    gather_plan(cnt, fill, wtot5, offsets, g.job_expert, g.job_off, g.job_cnt, g.pass_job, g.pass_tp,
+                g.pass_job2, g.pass_tp2, g.counts, n_experts, pres, g.pass_tok, g.pass_tok2);
 
     /* stable placement */
     const bool wide = n_experts > G_WCNT_E;
     for (int c0 = 0; c0 < N; c0 += 1024) {
         const int a = c0 + tid;
-        const int e = a < N ? idx[a] : -1;
+        const int e = c0 == 0 ? ev0 : c0 == 1024 ? ev1 : a < N ? idx_at(a) : -1;
         const bool ok = e >= 0 && e < n_experts;
         /* rank among earlier lanes of this wave with the same expert */
         uint64_t pending = __ballot(ok);
@@ -909,6 +954,11 @@ __global__ __launch_bounds__(1024) void gather_kernel(int *offsets, int *perm, i
             }
         }
     }
+}
+
+__global__ __launch_bounds__(1024) void gather_kernel(GatherDev g)
+{
+    gather_block<false>(g);
 }
 
 /* The same gather over many workgroups, for large batches (more than GM_MIN assignments,
@@ -1235,7 +1285,7 @@ static ExcTable exc_view(const K3kExc *exc)
 
 extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, int T,
                                   const float *W, int hidden, int n_experts, int chunk,
-                                  const K3kExc *exc, void *stream)
+                                  int *ctr, const K3kExc *exc, void *stream)
 {
     if (T <= 0 || n_experts <= 0) return 0;
     if (chunk <= 0 || chunk % RP_KS) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
@@ -1279,19 +1329,52 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
                          (size_t)T * hidden * 4 < 0x80000000u;
         if (buf)
             hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, true>), grid, dim3(256), 0, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec, xg);
+                               rbound, x, T, W, hidden, n_experts, chunk, vec, xg, ctr);
         else
             hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, false>), grid, dim3(256), 0, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec, xg);
+                               rbound, x, T, W, hidden, n_experts, chunk, vec, xg, ctr);
     }
     K3K_LAUNCH_CHECK("router_partial launch");
     return 0;
 }
 
+extern "C" int k3k_router_gathers(int T, int hidden, int n_experts, int topk)
+{
+    (void)hidden;
+    return T > RS_T && n_experts <= RF_MAXE && topk <= 64 && k3k_gather_scratch(T, topk, n_experts) == 0;
+}
+
+static GatherDev gather_dev(const K3kGatherArgs *g, const int *idx, int N, int n_experts)
+{
+    GatherDev d;
+    memset(&d, 0, sizeof d);
+    if (g) {
+        d.offsets = g->offsets;
+        d.perm = g->perm;
+        d.job_expert = g->job_expert;
+        d.job_off = g->job_off;
+        d.job_cnt = g->job_cnt;
+        d.pass_job = g->pass_job;
+        d.pass_tp = g->pass_tp;
+        d.pass_job2 = g->pass_job2;
+        d.pass_tp2 = g->pass_tp2;
+        d.counts = g->counts;
+        d.bank = g->bank;
+        d.pass_tok = g->pass_tok;
+        d.pass_tok2 = g->pass_tok2;
+        d.ctr = g->ctr;
+    }
+    d.idx = idx;
+    d.N = N;
+    d.n_experts = n_experts;
+    return d;
+}
+
 extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part,
                                 const float *rbound, int chunk, const float *x, const float *W,
                                 const float *bias, int T, int hidden, int n_experts, int topk,
-                                int renorm, float routed_scale, const K3kExc *exc, void *stream)
+                                int renorm, float routed_scale, const K3kExc *exc,
+                                const K3kGatherArgs *gather, void *stream)
 {
     if (T <= 0) return 0;
     if (n_experts > RF_MAXE || topk > 64)
@@ -1302,6 +1385,24 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
     if (nw > RF_MAXW) nw = RF_MAXW;
     hipStream_t st = (hipStream_t)stream;
     const bool pre = router_small_mode(T, hidden);
+    const GatherDev gd = gather_dev(gather, idx, T * topk, n_experts);
+    if (gather) {
+        /* the selection, then the gather in the workgroup that finishes last (1024 threads) */
+        if (!k3k_router_gathers(T, hidden, n_experts, topk) || !gather->ctr || n_experts > G_MAXE ||
+            (gather->pass_tok2 > 0 && (!gather->pass_job2 || !gather->pass_tp2)))
+            return k3k_fail("router_final: the gather cannot run here", hipErrorInvalidValue);
+#define K3_RFG(SL, SW, KB)                                                                           \
+    hipLaunchKernelGGL((router_final_kernel<SL, SW, KB, false, true>), dim3(T), dim3(1024), 0, st, idx, wt, \
+                       nrecomp, part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm, \
+                       routed_scale, e, gd)
+        if (n_experts <= 512 && ks <= 16) K3_RFG(1, 8, 16);
+        else if (n_experts <= 512) K3_RFG(1, 8, RF_KB);
+        else if (n_experts <= 1024) K3_RFG(1, 32, RF_KB);
+        else K3_RFG(2, 32, RF_KB);
+#undef K3_RFG
+        K3K_LAUNCH_CHECK("router_final launch");
+        return 0;
+    }
     /* scored records (a few tokens): one wave loads them all; else the chunk partials, a lane
      * per expert, all of a lane's partials in one load batch when they are at most 16 or 32,
      * or 64 for up to 64 tokens and 512 experts (more registers, fewer waves per CU: only
@@ -1310,7 +1411,7 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
 #define K3_RF(SL, SW, KB, PRE, NT)                                                                  \
     hipLaunchKernelGGL((router_final_kernel<SL, SW, KB, PRE>), dim3(T), dim3(NT), 0, st, idx, wt, nrecomp, \
                        part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm,        \
-                       routed_scale, e)
+                       routed_scale, e, gd)
     if (pre && n_experts <= 512) K3_RF(8, 8, RF_KB, true, 64);
     else if (pre) K3_RF(32, 32, RF_KB, true, 64);
     else if (n_experts <= 512 && ks <= 16) K3_RF(1, 8, 16, false, 64 * nw);
@@ -1344,9 +1445,9 @@ extern "C" int k3k_gather(int *offsets, int *perm, int *job_expert, int *job_off
         hipLaunchKernelGGL(gather_place_kernel, dim3(nchunk), dim3(GM_C), 0, st, perm, hist, idx, N,
                            n_experts, nchunk);
     } else {
-        hipLaunchKernelGGL(gather_kernel, dim3(1), dim3(1024), 0, st, offsets, perm, job_expert,
-                           job_off, job_cnt, pass_job, pass_tp, pass_job2, pass_tp2, counts, idx, N,
-                           n_experts, bank, pass_tok, pass_tok2);
+        const K3kGatherArgs ga = {offsets, perm, job_expert, job_off, job_cnt, pass_job, pass_tp,
+                                  pass_job2, pass_tp2, counts, bank, topk, pass_tok, pass_tok2, NULL};
+        hipLaunchKernelGGL(gather_kernel, dim3(1), dim3(1024), 0, st, gather_dev(&ga, idx, N, n_experts));
     }
     K3K_LAUNCH_CHECK("gather launch");
     return 0;

@@ -164,7 +164,7 @@ int k3k_gemv_q8(float *y, const float *x, const void *W, int in, int out, int nt
 
 /* ---- router ----------------------------------------------------------------------- */
 /* Router in two launches. k3k_router_partial: per K chunk of `chunk` columns (a multiple
- * of 64, from k3k_router_chunk), the chunk's fp64 chain part[k][t][e] and a bound
+ * of 32, from k3k_router_chunk), the chunk's fp64 chain part[k][t][e] and a bound
  * rbound[k][t][e] on its intermediate magnitudes. k3k_router_final: the certified logit
  * (the reference's sequential fp64 chain recomputed where the bound cannot decide the
  * fp32 rounding and the logit matters), sigmoid with the host libm's expf, biased
@@ -174,12 +174,29 @@ int k3k_router_chunk(int T, int hidden, int n_experts);
 /* 1 when k3k_router_partial scores and certifies the logits itself (a few tokens): its
  * part then holds one 16-byte record per logit, which a selecting decode gate/up reads. */
 int k3k_router_small(int T, int hidden);
+/* The expert-major gather's outputs (k3k_gather) and its pass sizes, for the router's final
+ * kernel to run the one-workgroup gather itself in its last workgroup to finish, saving a
+ * launch. ctr: one int of scratch, zeroed by k3k_router_partial (its ctr argument) before
+ * the final kernel counts its workgroups in. */
+typedef struct {
+    int *offsets, *perm, *job_expert, *job_off, *job_cnt, *pass_job, *pass_tp, *pass_job2,
+        *pass_tp2, *counts;
+    const void *bank;
+    int topk, pass_tok, pass_tok2;
+    int *ctr;
+} K3kGatherArgs;
+/* 1 when k3k_router_final can run the gather (more than a few tokens, the one-workgroup
+ * gather's sizes). */
+int k3k_router_gathers(int T, int hidden, int n_experts, int topk);
+/* ctr (may be NULL): set to zero, for a following k3k_router_final that gathers. */
 int k3k_router_partial(double *part, float *rbound, const float *x, int T, const float *W,
-                       int hidden, int n_experts, int chunk, const K3kExc *exc, void *stream);
+                       int hidden, int n_experts, int chunk, int *ctr, const K3kExc *exc,
+                       void *stream);
+/* gather (may be NULL): also run the gather of idx, as k3k_gather would. */
 int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, const float *rbound,
                      int chunk, const float *x, const float *W, const float *bias, int T,
                      int hidden, int n_experts, int topk, int renorm, float routed_scale,
-                     const K3kExc *exc, void *stream);
+                     const K3kExc *exc, const K3kGatherArgs *gather, void *stream);
 
 /* ---- gather / combine -------------------------------------------------------------- */
 /* Stable expert-major gather of the T*topk assignments in idx. Outputs:
