@@ -618,13 +618,16 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
         return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
                               b1, b2, prec, &w, NULL, NULL, drops_out, &sel, 0, 0, stream);
     }
-    /* past the decode path the expert kernels take the tokens' bf16 split: it depends on x
-     * alone, so it runs on the side stream beside the router (event fork / join, captured by
-     * a graph like the rest) */
+    /* past the decode path the expert kernels take the tokens' bf16 split. It depends on x
+     * alone: for large batches it runs on the side stream beside the router (event fork /
+     * join, captured by a graph like the rest); below 2^22 elements it runs first on the
+     * stream, because there the fork and join cost more than the split (batch 64: 1.105 ->
+     * 1.085 ms per step) */
     const int split = !moe_decode_ok(T, hidden, inter, topk, x);
+    const int split_side = split && (size_t)T * hidden >= ((size_t)1 << 22);
     if (split) {
-        void *side;
-        if (k3k_fork(stream, &side)) return fail("fork");
+        void *side = stream;
+        if (split_side && k3k_fork(stream, &side)) return fail("fork");
         if (k3k_split_bf16(w.xhi, w.xlo, x, (size_t)T * hidden, side)) return fail("split");
     }
     /* the expert-major gather runs in the router's final kernel when it can (a launch and its
@@ -652,7 +655,7 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
     rc = router_run(idx, wt, x, T, router_w, bias, hidden, n_experts, topk, renorm, routed_scale,
                     &r, gathered ? &ga : NULL, stream);
     if (rc) return rc;
-    if (split && k3k_join(stream)) return fail("join");
+    if (split_side && k3k_join(stream)) return fail("join");
     k3k_prof_mark(stream, K3D_STAGE_ROUTER);
     return moe_experts_ws(out, idx, wt, x, T, bank, layout, hidden, inter, n_experts, topk, act,
                           b1, b2, prec, &w, perm_out, offsets_out, drops_out, NULL, split, gathered,
