@@ -61,7 +61,7 @@ static void tensor_sizes(int layout, int width, int inter, size_t sz[6])
     const int rows[3] = {inter, inter, width}, in[3] = {width, width, inter};
     for (int m = 0; m < 3; m++) {
         size_t r = (size_t)rows[m];
-        if (layout == K3_BANK_TILED) r = (r + 15) / 16 * 16;
+        if (layout == K3_BANK_TILED) r = (r + 63) / 64 * 64;   /* tile groups of 64 rows */
         sz[2 * m] = r * (size_t)in[m] / 2;
         sz[2 * m + 1] = r * (size_t)in[m] / 32;
     }

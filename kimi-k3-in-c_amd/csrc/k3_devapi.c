@@ -666,7 +666,7 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
 int k3d_mxfp4_tiled_size(int rows, int in, size_t *packed_bytes, size_t *scales_bytes)
 {
     if (rows <= 0 || in <= 0 || in % 512) return bad("k3d_mxfp4_tiled_size: need rows > 0 and in % 512 == 0");
-    const size_t prow = ((size_t)rows + 15) / 16 * 16;
+    const size_t prow = ((size_t)rows + 63) / 64 * 64;   /* groups of four 16-row tiles */
     if (packed_bytes) *packed_bytes = prow * (size_t)in / 2;
     if (scales_bytes) *scales_bytes = prow * (size_t)in / 32;
     return 0;

@@ -603,7 +603,7 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
         pm[0] = q.p2; sm[0] = q.s2;
     }
     if (!(q.p1 && q.s1 && q.p3 && q.s3 && q.p2 && q.s2)) return;   /* dropped or out of range */
-    const uint32_t prow = LAYOUT == 1 ? (uint32_t)ntile * 16u : (uint32_t)rows;
+    const uint32_t prow = LAYOUT == 1 ? k3_tile_prows(rows) : (uint32_t)rows;
     k3_rsrc rp[NM], rs[NM];
 #pragma unroll
     for (int m = 0; m < NM; m++) {
@@ -627,7 +627,7 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             if (LAYOUT == 1) {
-                const uint32_t tc = (uint32_t)tile * (uint32_t)nchunk + (uint32_t)c;
+                const uint32_t tc = k3_tile_idx(tile, c, nchunk);
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     qa[S][m][i] = k3_bload16<WPOL>(rp[m], in ? tc * 4096u + (uint32_t)i * 1024u + (uint32_t)lane * 16u : OOB);
@@ -797,7 +797,7 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
     ExpertQDev q = {};
     if (eix >= 0 && eix < a.n_experts) q = bank[eix];
     const bool valid = q.p1 && q.s1 && q.p3 && q.s3 && q.p2 && q.s2;
-    const uint32_t prow = LAYOUT == 1 ? (uint32_t)ntile * 16u : (uint32_t)rows;
+    const uint32_t prow = LAYOUT == 1 ? k3_tile_prows(rows) : (uint32_t)rows;
     const k3_rsrc rp = k3_make_rsrc(q.p2, valid ? prow * (uint32_t)(K >> 1) : 0u);
     const k3_rsrc rs = k3_make_rsrc(q.s2, valid ? prow * (uint32_t)nblk : 0u);
     const int row = min(tile * 16 + r16, rows - 1);
@@ -810,7 +810,7 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
         constexpr int S = decltype(slot)::value;
         const bool in = c < c1;
         if (LAYOUT == 1) {
-            const uint32_t tc = (uint32_t)tile * (uint32_t)nchunk + (uint32_t)c;
+            const uint32_t tc = k3_tile_idx(tile, c, nchunk);
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 qa[S][i] = k3_bload16<WPOL>(rp, in ? tc * 4096u + (uint32_t)i * 1024u + (uint32_t)lane * 16u : OOB);
@@ -929,9 +929,10 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
  *   LAYOUT 0, row-major (the reference's): per step a lane loads its block's 16 bytes
  *     (a wave: 16 rows x 64 contiguous bytes), per chunk one 16-byte load of the row's
  *     16 scale bytes, of which it uses one per step;
- *   LAYOUT 1, tiled (mx_tile_kernel): the bytes of a 16-row tile's chunk stored in lane
- *     order, so a wave's load is 1 KB contiguous and a lane's four scale bytes of the
- *     chunk are one 4-byte load.
+ *   LAYOUT 1, tiled (mx_tile_kernel, k3_tile_idx): the bytes of a 16-row tile's chunk
+ *     stored in lane order, so a wave's load is 1 KB contiguous and a lane's four scale
+ *     bytes of the chunk are one 4-byte load; the four tiles of a group lie side by side
+ *     chunk after chunk.
  * The pass's activation rows (hi, lo) for the chunk are staged once in LDS by the whole
  * workgroup (double buffered), one wave-uniform row-half per wave instruction and only for
  * the pass's real tokens; B lanes of token columns past the pass read a row of zeros.
@@ -983,7 +984,7 @@ void mx_moe_kernel(K3kMxArgs a)
         const int ntok = min(PT, a.job_cnt[j] - tok0);
         const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[e];
         /* one buffer descriptor per matrix (wave-uniform); per-lane byte offsets */
-        const uint32_t prow = LAYOUT == 1 ? (uint32_t)((rows + 15) & ~15) : (uint32_t)rows;
+        const uint32_t prow = LAYOUT == 1 ? k3_tile_prows(rows) : (uint32_t)rows;
         const uint32_t pbytes = prow * rstride;
         const uint32_t sbytes = prow * nblk;
         k3_rsrc rp0, rp1, rs0, rs1;
@@ -1005,8 +1006,8 @@ void mx_moe_kernel(K3kMxArgs a)
                 soff[m] = (uint32_t)r * (uint32_t)nblk;
             } else {
                 const int t = min((rb * rpg + wv * rpw) / 16 + mt, ntile - 1);
-                poff[m] = (uint32_t)t * (uint32_t)nchunk * 4096u + (uint32_t)lane * 16u;
-                soff[m] = (uint32_t)t * (uint32_t)nchunk * 256u + (uint32_t)lane * 4u;
+                poff[m] = k3_tile_idx(t, 0, nchunk) * 4096u + (uint32_t)lane * 16u;
+                soff[m] = k3_tile_idx(t, 0, nchunk) * 256u + (uint32_t)lane * 4u;
             }
         }
         /* staging: wave wv copies row-halves wv, wv+NW, ...; lane = 16-byte piece */
@@ -1072,7 +1073,7 @@ void mx_moe_kernel(K3kMxArgs a)
         auto load_step = [&](int c, int d, auto slot) {
             constexpr int S = decltype(slot)::value;
             const uint32_t bo = LAYOUT == 0 ? (uint32_t)c * 256u + (uint32_t)d * 64u
-                                            : ((uint32_t)c * 4u + (uint32_t)d) * 1024u;
+                                            : (uint32_t)c * K3_TILE_CSTRIDE + (uint32_t)d * 1024u;
 #pragma unroll
             for (int m = 0; m < MT; m++)
                 qa[S][d][m] = k3_bload16<WPOL>(m < RT || MODE != K3K_MX_GATEUP ? rp0 : rp1,
@@ -1086,7 +1087,7 @@ void mx_moe_kernel(K3kMxArgs a)
                     const uint4 v = k3_bload16<WPOL>(rs, c < nchunk ? soff[m] + (uint32_t)c * 16u : OOB);
                     ss[4 * m] = v.x; ss[4 * m + 1] = v.y; ss[4 * m + 2] = v.z; ss[4 * m + 3] = v.w;
                 } else {
-                    ss[m] = k3_bload4<WPOL>(rs, c < nchunk ? soff[m] + (uint32_t)c * 256u : OOB);
+                    ss[m] = k3_bload4<WPOL>(rs, c < nchunk ? soff[m] + (uint32_t)c * K3_TILE_SCSTRIDE : OOB);
                 }
             }
         };
@@ -1323,7 +1324,7 @@ void mx_prefill_kernel(K3kMxArgs a)
         const int tok0 = a.pass_tp[pass] * PT;
         const int ntok = __builtin_amdgcn_readfirstlane(min(PT, a.job_cnt[j] - tok0));
         const ExpertQDev q = reinterpret_cast<const ExpertQDev *>(a.bank)[e];
-        const uint32_t prow = (uint32_t)((rows + 15) & ~15);
+        const uint32_t prow = k3_tile_prows(rows);
         const uint32_t pbytes = prow * rstride;
         const uint32_t sbytes = prow * nblk;
         k3_rsrc rp0, rp1, rs0, rs1;
@@ -1341,8 +1342,8 @@ void mx_prefill_kernel(K3kMxArgs a)
         for (int m = 0; m < MT; m++) {
             const int mt = (MODE == K3K_MX_GATEUP) ? (m % RT) : m;
             const int t = min((rb * rpg + wv * rpw) / 16 + mt, ntile - 1);
-            ptile[m] = (uint32_t)t * (uint32_t)nchunk * 4096u;
-            stile[m] = (uint32_t)t * (uint32_t)nchunk * 256u;
+            ptile[m] = k3_tile_idx(t, 0, nchunk) * 4096u;
+            stile[m] = k3_tile_idx(t, 0, nchunk) * 256u;
         }
         /* DMA sources: instruction i of this wave fills slots 64 (wv + NW i) + lane */
         const uint32_t xbytes = (uint32_t)a.n_xrows * (uint32_t)K * 2u;
@@ -1368,7 +1369,9 @@ void mx_prefill_kernel(K3kMxArgs a)
         uint4 bv[NB];                         /* B fragments of the current sub-step */
         auto load_step = [&](int c, int d, auto slot) {
             constexpr int S = decltype(slot)::value;
-            const uint32_t bo = (uint32_t)min(c * SPC + d, nstage * SPC - 1) * 1024u;   /* 1 KB per tile */
+            /* the 128-column step s of the tile: chunk s / 4, step s % 4 */
+            const uint32_t s = (uint32_t)min(c * SPC + d, nstage * SPC - 1);
+            const uint32_t bo = (s >> 2) * K3_TILE_CSTRIDE + (s & 3u) * 1024u;
             const uint32_t vo = (MODE == K3K_MX_GATEUP || c < nstage) ? lvoff : OOB;
 #pragma unroll
             for (int m = 0; m < MT; m++)
@@ -1378,7 +1381,7 @@ void mx_prefill_kernel(K3kMxArgs a)
          * (c clamped: past the end re-reads the last stage) */
         auto load_scales = [&](int c, auto slot) {
             constexpr int S = decltype(slot)::value;
-            const uint32_t so = (uint32_t)(min(c, nstage - 1) * SPC >> 2) * 256u;
+            const uint32_t so = (uint32_t)(min(c, nstage - 1) * SPC >> 2) * K3_TILE_SCSTRIDE;
             const uint32_t vo = (MODE == K3K_MX_GATEUP || c < nstage) ? lsoff : OOB;
 #pragma unroll
             for (int m = 0; m < MT; m++)
@@ -1581,15 +1584,16 @@ __global__ void mx_dequant_kernel(float *out, const uint8_t *packed, const uint8
     }
 }
 
-/* Row-major MXFP4 -> the tiled layout read by mx_moe_kernel<..., LAYOUT=1>. For row tile t
- * (16 rows), K chunk c (16 blocks of 32) and lane l = 16g + r (r = row in tile):
- *   codes:  tpacked[((t*nchunk + c)*4 + d)*1024 + 16l ..+16] = block 4d+g of row 16t+r
- *   scales: tscales[(t*nchunk + c)*256 + 4l + d]             = scale of that block
- * Rows past `rows` (padding of the last tile) are zero codes with scale byte 0. */
+/* Row-major MXFP4 -> the tiled layout read by the LAYOUT 1 kernels. For row tile t (16
+ * rows), K chunk c (16 blocks of 32), i = k3_tile_idx(t, c) and lane l = 16g + r (r = row
+ * in tile):
+ *   codes:  tpacked[(i*4 + d)*1024 + 16l ..+16] = block 4d+g of row 16t+r
+ *   scales: tscales[i*256 + 4l + d]             = scale of that block
+ * Rows past `rows` (up to the next multiple of 64) are zero codes with scale byte 0. */
 __global__ void mx_tile_kernel(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
                                const uint8_t *scales, int rows, int K)
 {
-    const int nchunk = K / 512, nblk = K / 32, ntile = (rows + 15) / 16;
+    const int nchunk = K / 512, nblk = K / 32, ntile = (int)(k3_tile_prows(rows) / 16);
     const size_t n = (size_t)ntile * nchunk * 64;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x) {
@@ -1606,10 +1610,10 @@ __global__ void mx_tile_kernel(uint8_t *tpacked, uint8_t *tscales, const uint8_t
                 v = *reinterpret_cast<const uint4 *>(packed + (size_t)row * (K / 2) + (size_t)blk * 16);
                 sb = scales[(size_t)row * nblk + blk];
             }
-            *reinterpret_cast<uint4 *>(tpacked + ((tc * 4 + d) * 1024) + (size_t)l * 16) = v;
+            *reinterpret_cast<uint4 *>(tpacked + (((size_t)k3_tile_idx(t, c, nchunk) * 4 + d) * 1024) + (size_t)l * 16) = v;
             sw |= sb << (8 * d);
         }
-        *reinterpret_cast<uint32_t *>(tscales + tc * 256 + (size_t)l * 4) = sw;
+        *reinterpret_cast<uint32_t *>(tscales + (size_t)k3_tile_idx(t, c, nchunk) * 256 + (size_t)l * 4) = sw;
     }
 }
 
@@ -1741,7 +1745,7 @@ extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
     if (a->n_assign <= 0) return 0;
     if (a->K % 512 || a->K > 16 * 512 || a->n_assign > 16 || a->layout > 1 ||
         (mode == K3K_MX_GATEUP && (uintptr_t)a->xf32 % 16) ||
-        (size_t)((a->rows + 15) / 16 * 16) * (a->K / 2) >= 0x80000000u)
+        (size_t)k3_tile_prows(a->rows) * (a->K / 2) >= 0x80000000u)
         return k3k_fail("mx_decode: shape", hipErrorInvalidValue);
     /* 4 tiles per workgroup, K over 2 waves per tile, when that gives >= 256 workgroups;
      * otherwise (one or two assignments) 1 tile per workgroup, K over up to 16 waves
@@ -1803,7 +1807,7 @@ extern "C" int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream)
     if (a->n_assign <= 0) return 0;
     if (a->K % 512 || a->K > 16 * 512 || a->n_assign > 16 || a->layout > 1 || a->topk < 1 ||
         a->n_assign % a->topk || !a->wt ||
-        (size_t)((a->rows + 15) / 16 * 16) * (a->K / 2) >= 0x80000000u)
+        (size_t)k3_tile_prows(a->rows) * (a->K / 2) >= 0x80000000u)
         return k3k_fail("mx_decode_combine: shape", hipErrorInvalidValue);
     /* waves: topk slots x K shares, at most 16 */
     const int nchunk = a->K / 512;
@@ -1839,7 +1843,7 @@ extern "C" int k3k_mx_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *pa
 {
     if (rows <= 0) return 0;
     if (K <= 0 || K % 512) return k3k_fail("mx_tile: K % 512 != 0", hipErrorInvalidValue);
-    const size_t n = (size_t)((rows + 15) / 16) * (K / 512) * 64;
+    const size_t n = (size_t)(k3_tile_prows(rows) / 16) * (K / 512) * 64;
     const size_t blocks = (n + 255) / 256;
     hipLaunchKernelGGL(mx_tile_kernel, dim3(blocks < 16384 ? (unsigned)blocks : 16384u), dim3(256),
                        0, (hipStream_t)stream, tpacked, tscales, packed, scales, rows, K);

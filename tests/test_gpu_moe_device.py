@@ -25,18 +25,19 @@ def bits(a):
 
 
 def tile_layout(packed, scales, rows, K):
-    """The tiled layout, restated with numpy: tile t (16 rows), chunk c (16 blocks), step d,
-    lane l = 16g + r holds block 4d+g of row 16t+r; its four scale bytes (d = 0..3) are
-    contiguous at [(t*nchunk + c)*256 + 4l]."""
-    ntile, nchunk, nblk = (rows + 15) // 16, K // 512, K // 32
-    P = np.zeros((ntile * 16, K // 2), np.uint8)
-    S = np.zeros((ntile * 16, nblk), np.uint8)
+    """The tiled layout, restated with numpy: rows padded to a multiple of 64, tiles of 16
+    rows in groups of 4 (u = tile in group); in group q, chunk c (16 blocks), tile u, step d,
+    lane l = 16g + r holds block 4d+g of row 64q+16u+r; its four scale bytes (d = 0..3) are
+    contiguous at [((q*nchunk + c)*4 + u)*256 + 4l]."""
+    ngrp, nchunk, nblk = (rows + 63) // 64, K // 512, K // 32
+    P = np.zeros((ngrp * 64, K // 2), np.uint8)
+    S = np.zeros((ngrp * 64, nblk), np.uint8)
     P[:rows] = packed.reshape(rows, K // 2)
     S[:rows] = scales.reshape(rows, nblk)
-    Pb = P.reshape(ntile, 16, nchunk, 4, 4, 16)          # t, r, c, d, g, byte
-    tp = Pb.transpose(0, 2, 3, 4, 1, 5).reshape(-1)      # t, c, d, (g, r), byte
-    Sb = S.reshape(ntile, 16, nchunk, 4, 4)              # t, r, c, d, g
-    ts = Sb.transpose(0, 2, 4, 1, 3).reshape(-1)         # t, c, (g, r), d
+    Pb = P.reshape(ngrp, 4, 16, nchunk, 4, 4, 16)        # q, u, r, c, d, g, byte
+    tp = Pb.transpose(0, 3, 1, 4, 5, 2, 6).reshape(-1)   # q, c, u, d, (g, r), byte
+    Sb = S.reshape(ngrp, 4, 16, nchunk, 4, 4)            # q, u, r, c, d, g
+    ts = Sb.transpose(0, 3, 1, 5, 2, 4).reshape(-1)      # q, c, u, (g, r), d
     return tp, ts
 
 
