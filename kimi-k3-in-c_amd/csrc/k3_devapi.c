@@ -302,6 +302,7 @@ typedef struct {
     int *offsets, *perm, *job_expert, *job_off, *job_cnt, *pass_job, *pass_tp, *counts, *ghist;
     int *pass_job2, *pass_tp2;
     float *contrib;
+    float *gu;                  /* decode path: gate and up sums [N][2][inter], or NULL */
     int max_passes, max_passes2;
 } MoeWs;
 
@@ -370,6 +371,8 @@ static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n
         w->ghist = gs ? (int *)take(c, gs * 4) : NULL;
     }
     w->contrib = (float *)take(c, N * hidden * 4);
+    /* the decode path's gate and up sums, when gate and up take workgroups of their own */
+    w->gu = N <= 16 ? (float *)take(c, N * 2 * (size_t)inter * 4) : NULL;
     return c->off;
 }
 
@@ -470,6 +473,11 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
             a.wt_out = sel->wt;
             a.nrecomp = sel->nrecomp;
         }
+        /* one tile per workgroup (a few assignments): gate and up in workgroups of their own,
+         * their fp32 sums taken up by the down + combine kernel */
+        if (!sel && w->gu &&
+            k3k_mx_decode_split_ok(T * topk, topk, a.nsplit, hidden, inter, inter, hidden))
+            a.gu = w->gu;
         if (k3k_mx_decode(K3K_MX_GATEUP, &a, stream)) return fail("mx_decode gateup");
         a.sel = 0;
         k3k_prof_mark(stream, K3D_STAGE_GATEUP);

@@ -500,11 +500,14 @@ __global__ __launch_bounds__(1024) void mx_gemv_small_kernel(K3kMxArgs a, int kw
  * few tokens): the workgroup first selects its token's experts from the router's scored
  * records (select_rounds), so no separate selection kernel runs. Two activation
  * terms share one MFMA: column 0 is the hi term, column 1 the lo term, added at the end. */
-template <int MODE, int NS, int LAYOUT, int TPW, bool SEL = false>
+template <int MODE, int NS, int LAYOUT, int TPW, bool SEL = false, bool SPLIT = false>
 __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* [NS][K], zeros[512] */
-    constexpr int NM = MODE == K3K_MX_GATEUP ? 2 : 1;              /* gate + up, or down */
+    /* SPLIT (GATEUP, one tile per workgroup): a workgroup takes gate or up of its tile and
+     * writes the fp32 sum to a.gu; otherwise gate + up, or down */
+    static_assert(!SPLIT || (MODE == K3K_MX_GATEUP && TPW == 1 && !SEL), "split gate/up");
+    constexpr int NM = MODE == K3K_MX_GATEUP && !SPLIT ? 2 : 1;
     /* activation pieces per thread: K <= 8192, the host keeps 64 TPW ks XPT >= 2048 */
     constexpr int XPT = TPW == 4 ? 4 : 8;
     constexpr int WPOL = LAYOUT == 1 ? K3_LD_NT : K3_LD_DEFAULT;
@@ -514,7 +517,9 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
     const int r16 = lane & 15, g = lane >> 4;
     const int K = a.K, nblk = K >> 5, rows = a.rows, ntile = (rows + 15) >> 4, nchunk = K >> 9;
     const int ngrp = (ntile + TPW - 1) / TPW;
-    const int asg = blockIdx.x / ngrp, tg = blockIdx.x % ngrp;
+    const int bx = SPLIT ? (int)blockIdx.x >> 1 : (int)blockIdx.x;
+    const int which = SPLIT ? (int)blockIdx.x & 1 : 0;      /* SPLIT: 0 gate, 1 up */
+    const int asg = bx / ngrp, tg = bx % ngrp;
     const int tw = tg * TPW + wv % TPW, ks = wv / TPW;
     const int tile = min(tw, ntile - 1);                    /* past the last tile: discarded */
     const int c0 = ks * nchunk / KS, c1 = (ks + 1) * nchunk / KS;
@@ -596,7 +601,9 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
     ExpertQDev q = {};
     if (eix >= 0 && eix < a.n_experts) q = bank[eix];
     const uint8_t *pm[NM], *sm[NM];
-    if (MODE == K3K_MX_GATEUP) {
+    if (SPLIT) {
+        pm[0] = which ? q.p3 : q.p1; sm[0] = which ? q.s3 : q.s1;
+    } else if (MODE == K3K_MX_GATEUP) {
         pm[0] = q.p1; sm[0] = q.s1;
         pm[NM - 1] = q.p3; sm[NM - 1] = q.s3;
     } else {
@@ -736,7 +743,12 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
             }
         }
         const int base = tw * 16 + 4 * g;
-        if (MODE == K3K_MX_GATEUP) {
+        if (SPLIT) {
+            float *o = a.gu + ((size_t)asg * 2 + which) * rows;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                if (base + jj < rows) o[base + jj] = sum[0][jj];
+        } else if (MODE == K3K_MX_GATEUP) {
 #pragma unroll
             for (int jj = 0; jj < 4; jj++)
                 if (base + jj < rows) {
@@ -764,7 +776,7 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
  * (k3_ops.c:641-642). An absent slot's wave reads through an empty descriptor (zeros) and
  * its sum is left out. Two activation terms share one MFMA (columns 0 and 1), each term's
  * shares are added in order, then hi + lo. */
-template <int NS, int LAYOUT>
+template <int NS, int LAYOUT, bool GU = false>
 __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* [topk][NS][K], zeros[512] */
@@ -831,7 +843,49 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
     /* this wave's slot and columns of the activation terms into [slot][term][K] (the waves
      * of one slot stage disjoint column ranges), and the row of zeros (every wave writes the
      * same zeros): no workgroup barrier before the products */
-    {
+    if constexpr (GU) {
+        /* from the gate and up sums (fp32): act(gate, up) and its bf16 terms, as the gate/up
+         * kernel's epilogue forms them; a piece is 8 columns */
+        const int nq = (c1 - c0) * 64;
+        const k3_rsrc rg = k3_make_rsrc(a.gu, (uint32_t)a.n_assign * 2u * (uint32_t)K * 4u);
+        const uint32_t gb = ((uint32_t)(t * topk + j) * 2u * (uint32_t)K + (uint32_t)c0 * 512u) * 4u;
+        const uint32_t ub = gb + (uint32_t)K * 4u;
+        for (int i0 = 0; i0 < nq; i0 += 128) {
+            uint4 gv[2][2], uv[2][2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t o = (uint32_t)(i0 + lane + 64 * u) * 32u;
+                gv[u][0] = k3_bload16(rg, gb + o);
+                gv[u][1] = k3_bload16(rg, gb + o + 16u);
+                uv[u][0] = k3_bload16(rg, ub + o);
+                uv[u][1] = k3_bload16(rg, ub + o + 16u);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int i = i0 + lane + 64 * u;
+                if (i >= nq) continue;
+                const float gf[8] = {__uint_as_float(gv[u][0].x), __uint_as_float(gv[u][0].y), __uint_as_float(gv[u][0].z),
+                                     __uint_as_float(gv[u][0].w), __uint_as_float(gv[u][1].x), __uint_as_float(gv[u][1].y),
+                                     __uint_as_float(gv[u][1].z), __uint_as_float(gv[u][1].w)};
+                const float uf[8] = {__uint_as_float(uv[u][0].x), __uint_as_float(uv[u][0].y), __uint_as_float(uv[u][0].z),
+                                     __uint_as_float(uv[u][0].w), __uint_as_float(uv[u][1].x), __uint_as_float(uv[u][1].y),
+                                     __uint_as_float(uv[u][1].z), __uint_as_float(uv[u][1].w)};
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    uint16_t h0, l0, h1, l1;
+                    k3_split2(k3_act_pair(gf[2 * e], uf[2 * e], a.act, a.b1, a.b2), h0, l0);
+                    k3_split2(k3_act_pair(gf[2 * e + 1], uf[2 * e + 1], a.act, a.b1, a.b2), h1, l1);
+                    hw[e] = h0 | ((uint32_t)h1 << 16);
+                    lw[e] = l0 | ((uint32_t)l1 << 16);
+                }
+                *reinterpret_cast<uint4 *>(&xs[((size_t)j * NS) * K + c0 * 512 + 8 * i]) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                if (NS == 2)
+                    *reinterpret_cast<uint4 *>(&xs[((size_t)j * NS + 1) * K + c0 * 512 + 8 * i]) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            }
+        }
+        reinterpret_cast<uint4 *>(&xs[(size_t)topk * NS * K])[lane] = make_uint4(0, 0, 0, 0);
+    } else {
         const int nq = (c1 - c0) * 64;                      /* 16-byte pieces per term */
         const uint32_t bytes = (uint32_t)a.n_assign * (uint32_t)K * 2u;
         const uint32_t src = (uint32_t)(t * topk + j) * (uint32_t)K + (uint32_t)c0 * 512u;
@@ -1750,14 +1804,17 @@ extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
     /* 4 tiles per workgroup, K over 2 waves per tile, when that gives >= 256 workgroups;
      * otherwise (one or two assignments) 1 tile per workgroup, K over up to 16 waves
      * (at least 4, which the activation staging needs) */
-    const int nm = mode == K3K_MX_GATEUP ? 2 : 1;
     const int ntile = (a->rows + 15) / 16, nchunk = a->K / 512;
     const bool wide = (long)a->n_assign * ((ntile + 3) / 4) >= 256 || nchunk < 4;
+    /* gate and up in workgroups of their own, sums to a.gu (one tile per workgroup) */
+    const bool split = mode == K3K_MX_GATEUP && a->gu && !a->sel;
+    if (split && wide) return k3k_fail("mx_decode: split gate/up needs few assignments", hipErrorInvalidValue);
+    const int nm = mode == K3K_MX_GATEUP && !split ? 2 : 1;
     const int tpw = wide ? 4 : 1;
     const int ks = wide ? 2 : (nchunk < 16 ? nchunk : 16);
     size_t lds = (size_t)a->nsplit * a->K * 2 + 1024;
     if (lds < (size_t)(ks - 1) * tpw * nm * 1024) lds = (size_t)(ks - 1) * tpw * nm * 1024;
-    const int grid = a->n_assign * ((ntile + tpw - 1) / tpw);
+    const int grid = a->n_assign * ((ntile + tpw - 1) / tpw) * (split ? 2 : 1);
     void (*kern)(K3kMxArgs);
     const bool ns2 = a->nsplit == 2, tiled = a->layout == 1;
 #define K3_DEC(MODE, TPW)                                                                          \
@@ -1774,6 +1831,11 @@ extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
             return k3k_fail("mx_decode: selection arguments", hipErrorInvalidValue);
         if (wide) K3_DEC_SEL(4);
         else K3_DEC_SEL(1);
+    } else if (split) {
+        kern = tiled ? (ns2 ? mx_decode_kernel<K3K_MX_GATEUP, 2, 1, 1, false, true>
+                            : mx_decode_kernel<K3K_MX_GATEUP, 1, 1, 1, false, true>)
+                     : (ns2 ? mx_decode_kernel<K3K_MX_GATEUP, 2, 0, 1, false, true>
+                            : mx_decode_kernel<K3K_MX_GATEUP, 1, 0, 1, false, true>);
     } else if (mode == K3K_MX_GATEUP) {
         if (wide) K3_DEC(K3K_MX_GATEUP, 4);
         else K3_DEC(K3K_MX_GATEUP, 1);
@@ -1802,6 +1864,14 @@ extern "C" int k3k_mx_decode_combine_ok(int n_assign, int topk, int nsplit, int 
     return !wide && topk >= 1 && topk <= 16 && (size_t)topk * nsplit * K * 2 + 1024 <= K3_DC_LDS_MAX;
 }
 
+extern "C" int k3k_mx_decode_split_ok(int n_assign, int topk, int nsplit, int K, int rows, int K_down,
+                                      int rows_down)
+{
+    const long ntile = (rows + 15) / 16;
+    const bool wide = (long)n_assign * ((ntile + 3) / 4) >= 256 || K / 512 < 4;
+    return !wide && k3k_mx_decode_combine_ok(n_assign, topk, nsplit, K_down, rows_down);
+}
+
 extern "C" int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream)
 {
     if (a->n_assign <= 0) return 0;
@@ -1819,16 +1889,24 @@ extern "C" int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream)
     const size_t lds = (size_t)a->topk * a->nsplit * a->K * 2 + 1024;
     void (*kern)(K3kMxArgs);
     const bool ns2 = a->nsplit == 2, tiled = a->layout == 1;
-    kern = tiled ? (ns2 ? mx_decode_combine_kernel<2, 1> : mx_decode_combine_kernel<1, 1>)
-                 : (ns2 ? mx_decode_combine_kernel<2, 0> : mx_decode_combine_kernel<1, 0>);
+    if (a->gu)      /* activations from the gate and up sums */
+        kern = tiled ? (ns2 ? mx_decode_combine_kernel<2, 1, true> : mx_decode_combine_kernel<1, 1, true>)
+                     : (ns2 ? mx_decode_combine_kernel<2, 0, true> : mx_decode_combine_kernel<1, 0, true>);
+    else
+        kern = tiled ? (ns2 ? mx_decode_combine_kernel<2, 1> : mx_decode_combine_kernel<1, 1>)
+                     : (ns2 ? mx_decode_combine_kernel<2, 0> : mx_decode_combine_kernel<1, 0>);
     static bool attr = false;
     if (!attr) {
-        const void *ks4[4] = {reinterpret_cast<const void *>(mx_decode_combine_kernel<2, 1>),
+        const void *ks8[8] = {reinterpret_cast<const void *>(mx_decode_combine_kernel<2, 1>),
                               reinterpret_cast<const void *>(mx_decode_combine_kernel<1, 1>),
                               reinterpret_cast<const void *>(mx_decode_combine_kernel<2, 0>),
-                              reinterpret_cast<const void *>(mx_decode_combine_kernel<1, 0>)};
-        for (int i = 0; i < 4; i++) {
-            const hipError_t e = hipFuncSetAttribute(ks4[i], hipFuncAttributeMaxDynamicSharedMemorySize, K3_DC_LDS_MAX);
+                              reinterpret_cast<const void *>(mx_decode_combine_kernel<1, 0>),
+                              reinterpret_cast<const void *>(mx_decode_combine_kernel<2, 1, true>),
+                              reinterpret_cast<const void *>(mx_decode_combine_kernel<1, 1, true>),
+                              reinterpret_cast<const void *>(mx_decode_combine_kernel<2, 0, true>),
+                              reinterpret_cast<const void *>(mx_decode_combine_kernel<1, 0, true>)};
+        for (int i = 0; i < 8; i++) {
+            const hipError_t e = hipFuncSetAttribute(ks8[i], hipFuncAttributeMaxDynamicSharedMemorySize, K3_DC_LDS_MAX);
             if (e != hipSuccess) return k3k_fail("mx_decode_combine: LDS attribute", e);
         }
         attr = true;

@@ -118,6 +118,12 @@ typedef struct {
     int *idx_out;
     float *wt_out;
     int *nrecomp;
+    /* Decode with few assignments (k3k_mx_decode_split_ok): gu [n_assign][2][inter] fp32.
+     * k3k_mx_decode GATEUP then gives gate and up workgroups of their own and writes the two
+     * fp32 sums there (twice the workgroups: one assignment's 128 tiles leave half the CUs
+     * idle otherwise); k3k_mx_decode_combine forms act(gate, up) and its bf16 terms from them
+     * while staging (the same functions, the same result). NULL: the activation terms. */
+    float *gu;
 } K3kMxArgs;
 
 int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
@@ -131,6 +137,10 @@ int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream);
 int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream);
 /* where k3k_mx_decode_combine is used (faster than the two kernels, LDS fits) */
 int k3k_mx_decode_combine_ok(int n_assign, int topk, int nsplit, int K, int rows);
+/* where the decode gate/up splits gate and up over workgroups (gu, no in-kernel selection):
+ * few enough assignments for one tile per workgroup, and a down + combine launch after it */
+int k3k_mx_decode_split_ok(int n_assign, int topk, int nsplit, int K, int rows, int K_down,
+                           int rows_down);
 
 /* Whether PLAIN may take fp32 activations (xf32): one or two tokens whose bf16 terms fit in
  * 64 KB of LDS, K <= 16384, x 16-byte aligned, the packed matrix under 2 GiB. */

@@ -136,13 +136,18 @@ def test_moe_device_layouts_vs_oracle(gpu, orc, small_layer, prec):
                                          (2, 7, 1, 1024, 1536), (1, 1, 0, 1024, 1536),
                                          (2, 8, 0, 2048, 4096), (2, 8, 1, 2048, 4096),
                                          (1, 2, 1, 1024, 2048), (2, 1, 0, 1024, 2048),
-                                         (1, 1, 0, 1024, 2048)])
+                                         (1, 1, 0, 1024, 2048), (1, 1, 0, 2048, 2048),
+                                         (1, 2, 1, 2048, 2048), (1, 4, 0, 2048, 2048)])
 def test_moe_device_decode_path(gpu, orc, k3, T, K, prec, E, I):
     """At most 16 assignments (T * topk) take the decode kernels straight from the router's
     idx, without the gather: one tile per workgroup with K over up to 16 waves for few
     assignments, four tiles with K over two waves when they fill the chip (the 2048 x 4096
     cases); down and the combine in one kernel for one or two assignments (the 1-slot
-    case), else down into per-slot rows and the combine kernel. Outputs
+    case), else down into per-slot rows and the combine kernel. With one tile per
+    workgroup, K of at least four chunks and down + combine in one kernel (the 2048 x 2048
+    cases), gate and up take workgroups of their own and down forms the activation from
+    their fp32 sums; the run with the router's selection inside gate/up (no split) must
+    give the same bits. Outputs
     against the oracle's per-slot sum (1e-4 * ||ref||inf with two-term
     activations, 2e-2 relative with one), row-major and tiled banks bit-identical, a
     NaN-scaled expert, and a dropped expert that contributes nothing and is counted."""
