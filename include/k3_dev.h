@@ -79,8 +79,9 @@ int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const
  *   K3D_LAYOUT_TILED: the same bytes regrouped per tile of 16 rows x 512 columns in the
  *     order the expert kernel reads them (k3d_mxfp4_tile), the four tiles of each group of
  *     64 rows side by side chunk after chunk; rows are padded to a multiple of 64, in must
- *     be a multiple of 512. Same arithmetic, results bit-identical to ROWS; the expert
- *     kernel streams it at a higher fraction of HBM bandwidth. */
+ *     be a multiple of 512. A block with scale byte 255 (NaN; zero in the reference) is
+ *     stored as zero codes with scale byte 127. Same arithmetic, results bit-identical to
+ *     ROWS; the expert kernel streams it at a higher fraction of HBM bandwidth. */
 enum { K3D_LAYOUT_ROWS = 0, K3D_LAYOUT_TILED = 1 };
 int k3d_mxfp4_tiled_size(int rows, int in, size_t *packed_bytes, size_t *scales_bytes);
 int k3d_mxfp4_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,

@@ -686,7 +686,9 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
                                   : (i == 0 ? sq[S][m].x : i == 1 ? sq[S][m].y : i == 2 ? sq[S][m].z : sq[S][m].w) >> (8 * g);
                 uint32_t ss = sw & 0xffu;
                 qm[m] = qa[S][m][i];
-                if (ss == 255u) {                           /* NaN byte: the block is 0 */
+                /* NaN byte: the block is 0 (a tiled bank stores such a block as zero codes
+                 * with scale 127 already) */
+                if (LAYOUT == 0 && ss == 255u) {
                     qm[m] = make_uint4(0, 0, 0, 0);
                     ss = 127u;
                 }
@@ -925,7 +927,8 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
                               : (i == 0 ? sq[S].x : i == 1 ? sq[S].y : i == 2 ? sq[S].z : sq[S].w) >> (8 * g);
             uint32_t ss = sw & 0xffu;
             uint4 qm = qa[S][i];
-            if (ss == 255u) {                               /* NaN byte: the block is 0 */
+            /* NaN byte: the block is 0 (tiled: stored as zero codes, scale 127) */
+            if (LAYOUT == 0 && ss == 255u) {
                 qm = make_uint4(0, 0, 0, 0);
                 ss = 127u;
             }
@@ -1191,7 +1194,8 @@ void mx_moe_kernel(K3kMxArgs a)
                 for (int m = 0; m < MT; m++) {
                     const uint32_t sraw = LAYOUT == 0 ? (sq[4 * m + d] >> (8 * g)) & 0xFFu
                                                       : (sq[m] >> (8 * d)) & 0xFFu;
-                    const bool nanb = sraw == 255u;              /* NaN byte: the block is 0 */
+                    /* NaN byte: the block is 0 (a tiled bank stores it as zeros, scale 127) */
+                    const bool nanb = LAYOUT == 0 && sraw == 255u;
                     const uint32_t keep = nanb ? 0u : ~0u;       /* a mask, not a branch */
                     qq[m] = qa[S][d][m];
                     qq[m].x &= keep;
@@ -1449,11 +1453,11 @@ void mx_prefill_kernel(K3kMxArgs a)
         auto deq = [&](const uint4 (&qs)[SPC][MT], const uint32_t *sw, int c, int u, k3_bf16x8 *dst) {
 #pragma unroll
             for (int m = 0; m < MT; m++) {
+                /* a NaN-scale block is stored as zero codes with scale 127 in the tiled bank */
                 const uint32_t sraw = (sw[m] >> (8 * ((c * SPC + (u >> 2)) & 3))) & 0xFFu;
-                const bool nanb = sraw == 255u;               /* NaN byte: the block is 0 */
                 const uint4 qv = qs[u >> 2][m];
                 const uint32_t codes = (u & 3) == 0 ? qv.x : (u & 3) == 1 ? qv.y : (u & 3) == 2 ? qv.z : qv.w;
-                dst[m] = k3_dequant8_bf16(nanb ? 0u : codes, k3_e8m0_operand(nanb ? 127u : sraw));
+                dst[m] = k3_dequant8_bf16(codes, k3_e8m0_operand(sraw));
             }
         };
 
@@ -1643,7 +1647,9 @@ __global__ void mx_dequant_kernel(float *out, const uint8_t *packed, const uint8
  * in tile):
  *   codes:  tpacked[(i*4 + d)*1024 + 16l ..+16] = block 4d+g of row 16t+r
  *   scales: tscales[i*256 + 4l + d]             = scale of that block
- * Rows past `rows` (up to the next multiple of 64) are zero codes with scale byte 0. */
+ * A block whose scale byte is 255 (NaN, zero in the reference) is stored as zero codes with
+ * scale byte 127, which contributes the same zero. Rows past `rows` (up to the next
+ * multiple of 64) are zero codes with scale byte 0. */
 __global__ void mx_tile_kernel(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
                                const uint8_t *scales, int rows, int K)
 {
@@ -1663,6 +1669,12 @@ __global__ void mx_tile_kernel(uint8_t *tpacked, uint8_t *tscales, const uint8_t
             if (row < rows) {
                 v = *reinterpret_cast<const uint4 *>(packed + (size_t)row * (K / 2) + (size_t)blk * 16);
                 sb = scales[(size_t)row * nblk + blk];
+            }
+            /* NaN scale: the block contributes 0. Stored as zero codes with scale 2^0, so
+             * the kernels that read this layout need no test for it. */
+            if (sb == 255u) {
+                v = make_uint4(0, 0, 0, 0);
+                sb = 127u;
             }
             *reinterpret_cast<uint4 *>(tpacked + (((size_t)k3_tile_idx(t, c, nchunk) * 4 + d) * 1024) + (size_t)l * 16) = v;
             sw |= sb << (8 * d);

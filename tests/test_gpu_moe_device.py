@@ -28,12 +28,16 @@ def tile_layout(packed, scales, rows, K):
     """The tiled layout, restated with numpy: rows padded to a multiple of 64, tiles of 16
     rows in groups of 4 (u = tile in group); in group q, chunk c (16 blocks), tile u, step d,
     lane l = 16g + r holds block 4d+g of row 64q+16u+r; its four scale bytes (d = 0..3) are
-    contiguous at [((q*nchunk + c)*4 + u)*256 + 4l]."""
+    contiguous at [((q*nchunk + c)*4 + u)*256 + 4l]. A block with scale byte 255 (NaN) is
+    stored as zero codes with scale byte 127."""
     ngrp, nchunk, nblk = (rows + 63) // 64, K // 512, K // 32
     P = np.zeros((ngrp * 64, K // 2), np.uint8)
     S = np.zeros((ngrp * 64, nblk), np.uint8)
     P[:rows] = packed.reshape(rows, K // 2)
     S[:rows] = scales.reshape(rows, nblk)
+    nan = S == 255
+    P.reshape(ngrp * 64, nblk, 16)[nan] = 0
+    S[nan] = 127
     Pb = P.reshape(ngrp, 4, 16, nchunk, 4, 4, 16)        # q, u, r, c, d, g, byte
     tp = Pb.transpose(0, 3, 1, 4, 5, 2, 6).reshape(-1)   # q, c, u, d, (g, r), byte
     Sb = S.reshape(ngrp, 4, 16, nchunk, 4, 4)            # q, u, r, c, d, g
