@@ -175,28 +175,98 @@ struct SelSmem {
     int list[RF_LIST];
     double res[RF_LIST];
     __attribute__((aligned(16))) double prod[2][RF_BLK];
+    uint64_t cand[64];                             /* two-level selection: the waves' keys */
+    uint64_t last;                                 /* its k-th key and count */
+    int nsel;
+    int wcnt[16];                                  /* listed experts per wave */
 };
 
 /* The reference's rule topk times (largest choice, lowest index among equals, strictly
- * above -inf, none left: idx 0, weight 0; k3_ops.c:459-467) over the scored experts in sm,
- * by wave 0 alone: lane l holds the keys of experts l + 64 i (SW of them) and the largest
- * of its keys; each extraction is one wave maximum over those (wave_max_key_fast), after
- * which the lane that held it drops the key and takes its next largest; lane j keeps the
- * j-th selected key. Uncertified logits that matter (selected, or able to reach the
- * selection) are listed by ballots, recomputed by the whole workgroup with the reference's
- * chain (chain_block) and rescored, and the selection is redone until none is left.
- * Called by every thread after sm is written and a barrier; returns the selected key in
- * lanes 0..topk-1 of wave 0 (0: none), and the number of recomputes in nre. */
+ * above -inf, none left: idx 0, weight 0; k3_ops.c:459-467) over the scored experts in sm.
+ * Keys are unique (the expert's index in the low word), so the selection is the topk
+ * largest keys in order, however they are found:
+ *  - two levels, when the ng = ceil(n_experts / 64) groups of 64 experts fit the
+ *    workgroup's waves and ng * topk <= 64: wave g takes the topk largest keys of group g
+ *    (one key per lane, each extraction one wave maximum, wave_max_key_fast), then wave 0
+ *    the topk largest of those ng * topk candidates (one per lane);
+ *  - else wave 0 alone: lane l holds the keys of experts l + 64 i (SW of them) and the
+ *    largest of its keys; after each extraction the lane that held it drops the key and
+ *    takes its next largest.
+ * Lane j of wave 0 keeps the j-th selected key. Uncertified logits that matter (selected,
+ * i.e. a key at least the last selected one, or able to reach the selection) are listed in
+ * expert order by ballots, recomputed by the whole workgroup with the reference's chain
+ * (chain_block) and rescored, and the selection is redone until none is left. Called by
+ * every thread after sm is written and a barrier; returns the selected key in lanes
+ * 0..topk-1 of wave 0 (0: none), and the number of recomputes in nre. */
 template <int SW>
 __device__ uint64_t select_rounds(SelSmem<SW> &sm, const float *x, const float *W,
                                   const float *bias, int hidden, int n_experts, int topk,
                                   const ExcTable &exc, int &nre)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = (int)blockDim.x >> 6;
+    const int ng = (n_experts + 63) >> 6;
+    const bool two = ng <= nw && ng <= SW && ng * topk <= 64;
+    auto key_of = [&](int e) {
+        const float c = sm.c[e];
+        return (e < n_experts && c > -INFINITY) ? ((uint64_t)choice_order(c) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e)
+                                                : 0ull;
+    };
     nre = 0;
     uint64_t mysel = 0ull;
     for (int round = 0; round <= n_experts; round++) {
-        if (wv == 0) {
+        if (two) {
+            /* level 1: group wv's topk largest keys (0 once none is left) */
+            if (wv < ng) {
+                uint64_t k = key_of(64 * wv + lane);
+                for (int j = 0; j < topk; j++) {
+                    const uint64_t m = wave_max_key_fast(k);
+                    if (lane == 0) sm.cand[wv * topk + j] = m;
+                    if (k == m) k = 0ull;
+                }
+            }
+            __syncthreads();
+            /* level 2: the topk largest candidates */
+            if (wv == 0) {
+                uint64_t k = lane < ng * topk ? sm.cand[lane] : 0ull;
+                int nsel = 0;
+                uint64_t last = 0ull;
+                mysel = 0ull;
+                for (int j = 0; j < topk; j++) {
+                    const uint64_t m = wave_max_key_fast(k);
+                    if (m == 0ull) break;           /* no finite choice left */
+                    nsel++;
+                    last = m;
+                    if (lane == j) mysel = m;
+                    if (k == m) k = 0ull;
+                }
+                if (lane == 0) {
+                    sm.nsel = nsel;
+                    sm.last = last;
+                }
+            }
+            __syncthreads();
+            /* every wave lists its group's uncertified logits that matter, in expert order */
+            const int nsel = sm.nsel;
+            const uint64_t last = sm.last;
+            const float ckth = nsel > 0 ? key_choice(last) : -INFINITY;
+            bool need = false;
+            if (wv < ng) {
+                const int e = 64 * wv + lane;
+                need = e < n_experts && sm.unc[e] && (nsel < topk || key_of(e) >= last || sm.cmax[e] >= ckth);
+            }
+            const uint64_t bm = __ballot(need);
+            if (lane == 0) sm.wcnt[wv] = __popcll(bm);
+            __syncthreads();
+            int base = 0, total = 0;
+            for (int w = 0; w < nw; w++) {
+                const int cw = sm.wcnt[w];
+                if (w < wv) base += cw;
+                total += cw;
+            }
+            const int slot = base + __popcll(bm & ((1ull << lane) - 1ull));
+            if (need && slot < RF_LIST) sm.list[slot] = 64 * wv + lane;
+            if (tid == 0) sm.nlist = min(total, RF_LIST);
+        } else if (wv == 0) {
             uint64_t key[SW];
             uint64_t head = 0ull;
 #pragma unroll
