@@ -1343,6 +1343,7 @@ void mx_prefill_kernel(K3kMxArgs a)
     constexpr int WAIT_STAGE_LDS = (NLD & 15) | (7 << 4) | ((NLD >> 4) << 14);   /* and lgkmcnt 0 */
     __shared__ __attribute__((aligned(1024))) uint4 bs0[NSL];
     __shared__ __attribute__((aligned(1024))) uint4 bs1[NSL];
+    __shared__ int orow_sh[PT];                               /* the pass's output rows */
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1481,8 +1482,13 @@ void mx_prefill_kernel(K3kMxArgs a)
              * weights counts exactly the loads issued after them instead of draining the
              * queue; the stage count is even. The previous item's last DMA (zeros) has
              * landed and every wave is past its reads before stages 0 and 1 are fetched. */
+            /* the output rows of the pass's tokens, loaded under the wait below and kept in
+             * LDS once every wave is past the previous item's epilogue, so that this item's
+             * epilogue stores wait for nothing */
+            const int prow = tid < ntok ? a.perm[off + tok0 + tid] : 0;
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
+            if (tid < PT) orow_sh[tid] = prow;
             dma_b(0, P0{});
             dma_b(1, P1{});
             load_scales(0, P0{});
@@ -1562,7 +1568,7 @@ void mx_prefill_kernel(K3kMxArgs a)
         for (int nb = 0; nb < NB; nb++) {
             const int tk = nb * 16 + r16;
             if (tk >= ntok) continue;
-            const int orow = a.perm[off + tok0 + tk];
+            const int orow = orow_sh[tk];
             for (int m = 0; m < RT; m++) {
                 const int base = rb * rpg + wv * rpw + 16 * m + 4 * g;
                 if (MODE == K3K_MX_GATEUP) {
