@@ -117,7 +117,7 @@ def time_layer(layer, T, steps, warmup, nbatch=4):
 
 
 def time_prefill(layer, T=4096, steps=3, warmup=1):
-    """Prefill layer (config 3): T tokens, bf16 activations, 48-token expert passes on the
+    """Prefill layer (config 3): T tokens, bf16 activations, 96-token expert passes on the
     matrix cores. Eager calls; the stage profile comes from the timed calls themselves."""
     L = k3amd.lib()
     x = k3amd.DevBuf(T * E * 4).upload(wl.tokens(T, tag="bench.prefill"))
