@@ -274,6 +274,42 @@ def test_router_device_ties_and_nonfinite(gpu, orc):
         assert list(idx[t][3:]) == [0, 0, 0] and not wt[t][3:].any()
 
 
+@pytest.mark.parametrize("T", [3, 9])
+def test_router_device_ties_across_groups(gpu, orc, T):
+    """384 experts, top-8: the selection runs in two levels (each wave the top 8 of its 64
+    experts, then wave 0 over the candidates). Equal choices in different groups (experts
+    2, 70 and 200 share a row, scaled up so that they are chosen) still go to the lowest
+    index first; NaN and -inf biases in other groups are never chosen; with three finite
+    candidates in three groups the rest are idx 0, weight 0. T = 3 scores in the small
+    router, T = 9 in the matrix-core partials."""
+    say(f"case: router ties across expert groups T={T}")
+    rng = np.random.default_rng(11 + T)
+    N, hidden, K = 384, 512, 8
+    W = (rng.standard_normal((N, hidden)) * 0.02).astype(np.float32)
+    W[2] = W[2] * 4.0
+    W[70] = W[2]
+    W[200] = W[2]
+    X = rng.standard_normal((T, hidden)).astype(np.float32)
+    X[:, :] = np.abs(X) * np.sign(W[2])[None, :]       # the shared row scores high
+    bias = np.zeros(N, np.float32)
+    bias[130] = np.nan
+    bias[320] = -np.inf
+    for b in (None, bias):
+        idx, wt = gpu.router_device(X, W, b, K)
+        for t in range(T):
+            i2, w2 = orc.router(X[t], W, b, K)
+            assert np.array_equal(idx[t], i2), (t, idx[t], i2)
+            assert np.array_equal(bits(wt[t]), bits(w2)), t
+            assert list(idx[t][:3]) == [2, 70, 200], idx[t]
+    few = np.full(N, -np.inf, np.float32)
+    few[[5, 150, 383]] = 0.0
+    idx, wt = gpu.router_device(X, W, few, K)
+    for t in range(T):
+        i2, w2 = orc.router(X[t], W, few, K)
+        assert np.array_equal(idx[t], i2) and np.array_equal(bits(wt[t]), bits(w2))
+        assert list(idx[t][3:]) == [0] * 5 and not wt[t][3:].any()
+
+
 @pytest.mark.parametrize("hidden", [1024, 7168])
 @pytest.mark.parametrize("ntok", [2, 40, 200])
 @pytest.mark.parametrize("scale", [1.0, -16.0])
