@@ -433,6 +433,108 @@ __global__ __launch_bounds__(1024) void mx_gemv_chunk_kernel(K3kMxArgs a, int kw
     }
 }
 
+/* mx_gemv_pair_kernel: mx_gemv_chunk_kernel on 8-row tiles, for matrices with fewer than
+ * one 16-row tile per CU (K % 1024 == 0, kw = K / 1024 <= 8 waves): twice the workgroups,
+ * each lane loading what it loads there. Wave w takes chunks 2w and 2w + 1 of the tile's
+ * 8 rows in one MFMA sequence: A rows 0-7 hold chunk 2w, rows 8-15 chunk 2w + 1, against
+ * B columns 0.. (chunk 2w's terms) and 8.. (chunk 2w + 1's). Each chunk's product is the
+ * chunk kernel's MFMA sequence at the same k positions, and the chunks' sums are added in
+ * chunk order, so y is the chunk kernel's, bit for bit. */
+template <int NS>
+__global__ __launch_bounds__(512) void mx_gemv_pair_kernel(K3kMxArgs a, int kw)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* chunk c: [ntok NS + 1][512] */
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4, h = r16 >> 3, j8 = r16 & 7;
+    const int K = a.K, nblk = K >> 5, rows = a.rows, ntok = a.ntok;
+    const int ncol = ntok * NS, nch = 2 * kw;
+    const int tile = blockIdx.x;
+    /* lane L stages columns 8L .. 8L+7 of both chunks for each token */
+    float4 xv[2][2][2];
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+                xv[c][t][hh] = t < ntok ? *reinterpret_cast<const float4 *>(a.xf32 + (size_t)t * K + (2 * wv + c) * 512 +
+                                                                             8 * lane + 4 * hh)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    /* lane (g, r16): row j8 of the tile, chunk 2w + h */
+    uint4 q[4];
+    const int row = min(tile * 8 + j8, rows - 1);           /* rows past the end: discarded */
+    const int ch = 2 * wv + h;
+    const k3_rsrc rp = k3_make_rsrc(a.packed, (uint32_t)rows * (uint32_t)(K >> 1));
+    const k3_rsrc rs = k3_make_rsrc(a.scales, (uint32_t)rows * (uint32_t)nblk);
+    const uint32_t pb = (uint32_t)row * (uint32_t)(K >> 1) + (uint32_t)ch * 256u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = k3_bload16(rp, pb + (uint32_t)(4 * i + g) * 16u);
+    const uint4 sv = k3_bload16(rs, (uint32_t)row * (uint32_t)nblk + (uint32_t)ch * 16u);
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        uint16_t *wx = xs + (size_t)(2 * wv + c) * (ncol + 1) * 512;   /* column j: wx + 512 j; zeros: wx + 512 ncol */
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            if (t >= ntok) break;
+            uint16_t hb[8], lb[8];
+            const float f[8] = {xv[c][t][0].x, xv[c][t][0].y, xv[c][t][0].z, xv[c][t][0].w,
+                                xv[c][t][1].x, xv[c][t][1].y, xv[c][t][1].z, xv[c][t][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) k3_split2(f[e], hb[e], lb[e]);
+            *reinterpret_cast<uint4 *>(wx + (t * NS) * 512 + 8 * lane) =
+                make_uint4(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16),
+                           hb[4] | ((uint32_t)hb[5] << 16), hb[6] | ((uint32_t)hb[7] << 16));
+            if (NS == 2)
+                *reinterpret_cast<uint4 *>(wx + (t * NS + 1) * 512 + 8 * lane) =
+                    make_uint4(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16),
+                               lb[4] | ((uint32_t)lb[5] << 16), lb[6] | ((uint32_t)lb[7] << 16));
+        }
+        *reinterpret_cast<uint4 *>(wx + ncol * 512 + 8 * lane) = make_uint4(0, 0, 0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();
+    /* B column r16: column j8 of chunk 2w + h (zeros past its terms) */
+    const uint16_t *bcol = xs + (size_t)(2 * wv + h) * (ncol + 1) * 512 + min(j8, ncol) * 512;
+    const uint32_t scw[4] = {sv.x, sv.y, sv.z, sv.w};
+    k3_f32x4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int blk = 4 * i + g;                          /* MX block of the chunk */
+        uint32_t ss = (scw[i] >> (8 * g)) & 0xffu;
+        uint4 qq = q[i];
+        if (ss == 255u) {                                   /* NaN byte: the block is 0 */
+            qq = make_uint4(0, 0, 0, 0);
+            ss = 127u;
+        }
+        const float so = k3_e8m0_operand(ss);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t codes = p == 0 ? qq.x : p == 1 ? qq.y : p == 2 ? qq.z : qq.w;
+            const uint4 bv = *reinterpret_cast<const uint4 *>(bcol + blk * 32 + 8 * p);
+            acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3_dequant8_bf16(codes, so), k3_as_bf16x8(bv), acc[p], 0, 0, 0);
+        }
+    }
+    /* lane (g, r16): rows 4g..4g+3 of column r16; chunk 2w's rows are 0-7 in columns 0-7,
+     * chunk 2w + 1's rows 8-15 in columns 8-15; a token's value is its columns' sum */
+    k3_f32x4 v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    if (NS == 2) {
+        k3_f32x4 nx;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) nx[jj] = __shfl_down(v[jj], 1, 16);
+        v += nx;
+    }
+    float *red = reinterpret_cast<float *>(xs + (size_t)nch * (ncol + 1) * 512);   /* [nch][ntok][8] */
+    if ((g >> 1) == h && j8 < ncol && j8 % NS == 0)
+        *reinterpret_cast<float4 *>(&red[(ch * ntok + j8 / NS) * 8 + 4 * (g & 1)]) = make_float4(v[0], v[1], v[2], v[3]);
+    __syncthreads();
+    if (tid < ntok * 8) {
+        const int t = tid >> 3, rr = tid & 7;
+        float sum = red[t * 8 + rr];
+        for (int c = 1; c < nch; c++) sum += red[(c * ntok + t) * 8 + rr];
+        if (tile * 8 + rr < rows) a.y[(size_t)t * a.ldy + tile * 8 + rr] = sum;
+    }
+}
+
 /* mx_gemv_small_kernel: any K % 32 == 0 (row-major), runs of at most SMAX steps per wave
  * (kw <= 16). A lane loads block 4s+g of its row and that block's scale byte; lanes past
  * the wave's run or past K take the offset 2^31, beyond the buffer's size (< 2^31), where a
@@ -1711,13 +1813,18 @@ extern "C" int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream)
             if (lds < (size_t)kw * 1024) lds = (size_t)kw * 1024;
             /* chunked: per wave ntok nsplit + 1 columns of 512 bf16, then the sums */
             if (chunked) lds = (size_t)kw * (a->ntok * a->nsplit + 1) * 1024 + (size_t)kw * a->ntok * 64;
-            const int grid = (a->rows + 15) / 16;
+            /* fewer 16-row tiles than CUs: 8-row tiles, two chunks per wave */
+            const bool pair = chunked && a->K % 1024 == 0 && (a->rows + 15) / 16 < cus;
+            const int grid = pair ? (a->rows + 7) / 8 : (a->rows + 15) / 16;
             void (*kern)(K3kMxArgs, int);
-            if (chunked)
+            if (pair)
+                kern = a->nsplit == 2 ? mx_gemv_pair_kernel<2> : mx_gemv_pair_kernel<1>;
+            else if (chunked)
                 kern = a->nsplit == 2 ? mx_gemv_chunk_kernel<2> : mx_gemv_chunk_kernel<1>;
             else
                 kern = a->nsplit == 2 ? mx_gemv_small_kernel<2, 8> : mx_gemv_small_kernel<1, 8>;
-            hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kw), lds, st, *a, kw);
+            const int wpb = pair ? kw / 2 : kw;             /* waves per workgroup */
+            hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * wpb), lds, st, *a, wpb);
             K3K_LAUNCH_CHECK("mx_gemv_small launch");
             return 0;
         }

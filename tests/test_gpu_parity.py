@@ -91,6 +91,43 @@ def test_gemv_device_tokens(gpu, orc, ntok, prec, rows, inn):
             assert np.linalg.norm(Y[t] - want) / np.linalg.norm(want) <= TOL_BF16
 
 
+@pytest.mark.parametrize("ntok,prec", [(1, 0), (2, 0), (1, 1), (2, 1)])
+def test_gemv_eight_row_tiles_bit_identical(gpu, orc, ntok, prec):
+    """A matrix with fewer 16-row tiles than the chip has CUs (2048 x 7168) runs 8-row tiles
+    with two 512-column chunks per wave; 4096 rows run 16-row tiles. Rows are independent,
+    so the first 2048 rows alone give the 4096-row matrix's first 2048 outputs bit for bit;
+    both against the oracle too."""
+    say(f"case: gemv 8-row vs 16-row tiles ntok={ntok} prec={prec}")
+    inn, big, small = 7168, 4096, 2048
+    rng = np.random.default_rng(77 + ntok + 10 * prec)
+    pk = rng.integers(0, 256, big * inn // 2, dtype=np.uint8)
+    sc = rng.integers(118, 128, big * inn // 32, dtype=np.uint8)
+    sc[rng.integers(0, sc.size, 16)] = 255
+    X = rng.standard_normal((ntok, inn)).astype(np.float32)
+    L = gpu.lib()
+
+    def run(rows):
+        p, s = pk[:rows * inn // 2], sc[:rows * inn // 32]
+        dp, ds = gpu.DevBuf(p.nbytes).upload(p), gpu.DevBuf(s.nbytes).upload(s)
+        dx, dy = gpu.DevBuf(X.nbytes).upload(X), gpu.DevBuf(ntok * rows * 4)
+        ws = gpu.DevBuf(max(L.k3d_matmul_mxfp4_ws(ntok, inn), 16))
+        try:
+            gpu.check(L.k3d_matmul_mxfp4(dy.ptr, dx.ptr, ntok, dp.ptr, ds.ptr, inn, rows, prec,
+                                         ws.ptr, ws.nbytes, None), "k3d_matmul_mxfp4")
+            return dy.download(np.empty((ntok, rows), np.float32))
+        finally:
+            for b in (dp, ds, dx, dy, ws):
+                b.free()
+
+    Yb, Ys = run(big), run(small)
+    assert np.array_equal(bits(Ys), bits(Yb[:, :small]))
+    want = orc.matmul_mxfp4(X[0], pk[:small * inn // 2], sc[:small * inn // 32], inn, small)
+    if prec == 0:
+        assert max_err_rel_inf(Ys[0], want) <= TOL
+    else:
+        assert np.linalg.norm(Ys[0] - want) / np.linalg.norm(want) <= TOL_BF16
+
+
 def test_dense_gemv_f32_bf16_identical(gpu, orc):
     """k3_matmul_bf16 equals k3_matmul on the widened weights bit for bit, over arbitrary
     finite bf16 patterns (the reference's own check, test_ops.c:811-848)."""
