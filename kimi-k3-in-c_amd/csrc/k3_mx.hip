@@ -940,6 +940,24 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
     };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
+    /* GU: the first pieces of the gate and up sums are requested before the weights, so
+     * that waiting for them (loads complete in order) leaves the weight loads in flight */
+    const k3_rsrc rg = k3_make_rsrc(a.gu, GU ? (uint32_t)a.n_assign * 2u * (uint32_t)K * 4u : 0u);
+    const uint32_t gb = ((uint32_t)(t * topk + j) * 2u * (uint32_t)K + (uint32_t)c0 * 512u) * 4u;
+    const uint32_t ub = gb + (uint32_t)K * 4u;
+    uint4 gv0[2][2], uv0[2][2];
+    auto load_gu = [&](int i0, uint4 (&gv)[2][2], uint4 (&uv)[2][2]) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint32_t o = (uint32_t)(i0 + lane + 64 * u) * 32u;
+            gv[u][0] = k3_bload16(rg, gb + o);
+            gv[u][1] = k3_bload16(rg, gb + o + 16u);
+            uv[u][0] = k3_bload16(rg, ub + o);
+            uv[u][1] = k3_bload16(rg, ub + o + 16u);
+        }
+    };
+    if constexpr (GU) load_gu(0, gv0, uv0);
+    __builtin_amdgcn_sched_barrier(0);
     load(c0, P0{});                                         /* in the loop's order */
     __builtin_amdgcn_sched_barrier(0);
     load(c0 + 1, P1{});
@@ -951,18 +969,18 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
         /* from the gate and up sums (fp32): act(gate, up) and its bf16 terms, as the gate/up
          * kernel's epilogue forms them; a piece is 8 columns */
         const int nq = (c1 - c0) * 64;
-        const k3_rsrc rg = k3_make_rsrc(a.gu, (uint32_t)a.n_assign * 2u * (uint32_t)K * 4u);
-        const uint32_t gb = ((uint32_t)(t * topk + j) * 2u * (uint32_t)K + (uint32_t)c0 * 512u) * 4u;
-        const uint32_t ub = gb + (uint32_t)K * 4u;
         for (int i0 = 0; i0 < nq; i0 += 128) {
             uint4 gv[2][2], uv[2][2];
+            if (i0 == 0) {
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint32_t o = (uint32_t)(i0 + lane + 64 * u) * 32u;
-                gv[u][0] = k3_bload16(rg, gb + o);
-                gv[u][1] = k3_bload16(rg, gb + o + 16u);
-                uv[u][0] = k3_bload16(rg, ub + o);
-                uv[u][1] = k3_bload16(rg, ub + o + 16u);
+                for (int u = 0; u < 2; u++)
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        gv[u][h] = gv0[u][h];
+                        uv[u][h] = uv0[u][h];
+                    }
+            } else {
+                load_gu(i0, gv, uv);
             }
 #pragma unroll
             for (int u = 0; u < 2; u++) {
