@@ -31,6 +31,7 @@ import k3amd  # noqa: E402
 import workloads as wl  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_FLOPS = 2.5e15
 E, I, N, K = wl.HIDDEN, wl.INTER, wl.N_EXPERTS, wl.TOPK
 MAT_BYTES = I * E // 2 + I * E // 32          # one 2048x7168 MXFP4 matrix: 7,798,784 B
 EXPERT_BYTES = 3 * MAT_BYTES                   # 23,396,352 B
@@ -62,6 +63,10 @@ class Layer:
         self.layout = layout
         self.bank = k3amd.DevBank(Lazy(), E, I, layout)
         self.router = k3amd.DevBuf(ROUTER_BYTES).upload(wl.router_weights())
+
+    def free(self):
+        self.bank.free()
+        self.router.free()
 
     def run(self, x, out, idx, wt, T, ws, prec=0, stream=None, bias=None):
         k3amd.check(k3amd.lib().k3d_moe_routed(
@@ -232,6 +237,17 @@ def time_skewed(layer, T=512, steps=5, warmup=1):
     step()
     k3amd.check(L.k3d_sync(None))
     st = prof.end()
+    # one more step with per-workgroup stamps of the routed expert kernels
+    sbuf = k3amd.DevBuf(1 << 20)
+    k3amd.check(L.k3d_stamps_begin(sbuf.ptr, sbuf.nbytes), "k3d_stamps_begin")
+    step()
+    k3amd.check(L.k3d_sync(None))
+    kinds, grids = (C.c_int * 64)(), (C.c_int * 64)()
+    nst = C.c_int()
+    k3amd.check(L.k3d_stamps_end(kinds, grids, 64, C.byref(nst)), "k3d_stamps_end")
+    nwg = sum(grids[i] for i in range(min(nst.value, 64)))
+    stamps = sbuf.download(np.empty((nwg, 3), np.uint64))
+    sbuf.free()
     h = idx.download(np.empty((T, K), np.int32))
     for b in (x, bias, d1, d3, d2, out, idx, wt, ws, sws):
         b.free()
@@ -239,10 +255,31 @@ def time_skewed(layer, T=512, steps=5, warmup=1):
     ms = (t1 - t0) / steps * 1e3
     sh_ms = st.get("shared", (0.0, 1))[0]
     sh_flops = T * 3 * 2 * E * I
+    routed_ms = sum(st.get(k, (0.0, 0))[0] for k in ("gateup", "down"))
+    u = int((cnt > 0).sum())
+    routed_bytes = u * EXPERT_BYTES
+    routed_flops = T * K * 3 * 2 * E * I
+    bound_ms = max(routed_bytes / (PEAK_HBM_GBS * 1e9), routed_flops / PEAK_BF16_FLOPS) * 1e3
+    step_bytes = routed_bytes + 3 * I * E * 2 + ROUTER_BYTES + 2 * T * E * 4
+    step_flops = routed_flops + sh_flops
+    step_bound_ms = max(step_bytes / (PEAK_HBM_GBS * 1e9), step_flops / PEAK_BF16_FLOPS) * 1e3
     return {"tokens": T, "ms_per_step": round(ms, 3), "tokens_per_s": round(T / ms * 1e3, 1),
             "arithmetic": "routed and shared experts with activations rounded to bf16 (one term), "
                           "bf16 MFMA with fp32 accumulation; tolerance 2e-2 relative",
-            "routing": {"unique_experts": int((cnt > 0).sum()), "max_tokens_per_expert": int(cnt[0]),
+            "skew": "selection bias 2.5 * rank^-1.2 over a seeded expert permutation (the form of "
+                    "the reference's e_score_correction_bias: it steers which experts are chosen, "
+                    "the combine weights stay the unbiased scores); with top-8 of distinct experts "
+                    "no expert can hold more than 1/8 of the assignments, so Zipf(1.2)'s top-3 "
+                    "share of 41.8 % is capped at 37.5 %",
+            "roofline": {"bound": "max(hbm, mfma)",
+                         "routed_stage_ms": round(routed_ms, 4),
+                         "routed_bound_ms": round(bound_ms, 4),
+                         "routed_frac": round(bound_ms / routed_ms, 4) if routed_ms else None,
+                         "routed_bytes": routed_bytes, "routed_flops": routed_flops,
+                         "step_bound_ms": round(step_bound_ms, 4),
+                         "step_frac": round(step_bound_ms / ms, 4)},
+            "per_cu_busy": cu_busy(stamps),
+            "routing": {"unique_experts": u, "max_tokens_per_expert": int(cnt[0]),
                         "mean_tokens_per_used_expert": round(float(cnt[cnt > 0].mean()), 2),
                         "share_top1": round(float(cnt[0] / cnt.sum()), 4),
                         "share_top3": round(float(cnt[:3].sum() / cnt.sum()), 4),
@@ -251,6 +288,76 @@ def time_skewed(layer, T=512, steps=5, warmup=1):
             "shared_expert_ms": round(sh_ms, 4),
             "shared_expert_TFLOPs": round(sh_flops / (sh_ms * 1e-3) / 1e12, 1) if sh_ms else None,
             "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st.items()}}
+
+
+def cu_busy(stamps):
+    """Per-CU busy time of the stamped expert launches of one step (k3d_stamps_*): a CU is
+    busy while any of its workgroups runs (the union of their [start, end] intervals on the
+    100 MHz clock), over all launches of the step; min / median / max over the CUs that
+    ran one, beside the span from the first start to the last end."""
+    if len(stamps) == 0:
+        return None
+    t0, t1, hw = stamps[:, 0].astype(np.int64), stamps[:, 1].astype(np.int64), stamps[:, 2]
+    xcc = (hw >> np.uint64(32)).astype(np.int64)
+    hid = (hw & np.uint64(0xFFFFFFFF)).astype(np.int64)
+    key = xcc * 256 + ((hid >> 8) & 0xFF)             # XCC, shader engine / array, CU
+    busy = []
+    for k in np.unique(key):
+        sel = np.argsort(t0[key == k])
+        a, b = t0[key == k][sel], t1[key == k][sel]
+        tot, cs, ce = 0, a[0], b[0]
+        for s_, e_ in zip(a[1:], b[1:]):
+            if s_ > ce:
+                tot += ce - cs
+                cs, ce = s_, e_
+            else:
+                ce = max(ce, e_)
+        busy.append((tot + ce - cs) / 100.0)           # 100 MHz ticks -> us
+    busy = np.array(busy)
+    span = (t1.max() - t0.min()) / 100.0
+    return {"cus": int(len(busy)), "workgroups": int(len(stamps)), "span_us": round(float(span), 1),
+            "busy_us": {"min": round(float(busy.min()), 1), "median": round(float(np.median(busy)), 1),
+                        "max": round(float(busy.max()), 1)},
+            "busy_frac_of_span": {"min": round(float(busy.min() / span), 3),
+                                  "median": round(float(np.median(busy) / span), 3)}}
+
+
+def time_k3_moe(T=1, steps=20, n_experts=896, distinct=32):
+    """Kimi K3's MoE layer at its real shape through the reference-compatible k3_moe
+    (hidden 7168, latent 3584, moe_inter 3072, 896 experts, top-16 with a selection bias,
+    two shared experts, bf16 trunk: router, down-projection, routed experts, latent RMSNorm,
+    up-projection, shared expert), the routed experts served from the library's HBM bank
+    behind K3ExpertSrc (896 slots of 17,547,264 B, 15.7 GB; `distinct` generated experts
+    placed under all 896 ids, each slot its own copy in HBM) and the trunk weights
+    registered resident. Wall clock per call of T tokens, including the copy of x to the
+    device and of out back; tokens rotate over 8 batches."""
+    L = k3amd.lib()
+    cfg, W, ex = wl.latent_layer(E, 3584, 3072, n_experts, 16, tag="bench.k3", n_generated=distinct)
+    runs = [wl.expert_run(ex[e]) for e in range(distinct)]
+    bank = k3amd.HbmBank(1, n_experts, 3584, 3072, n_experts, k3amd.K3D_LAYOUT_TILED, None)
+    try:
+        for e in range(n_experts):
+            bank.put_run(0, e, runs[e % distinct])
+        for k in ("gate", "bias", "latent_norm", "down", "up", "sh1", "sh3", "sh2"):
+            k3amd.dev_register(W[k])
+        xs = [wl.tokens(T, E, tag=f"bench.k3.x.{b}") for b in range(8)]
+        for b in range(3):
+            k3amd.moe(xs[b], cfg, W, 1, bank.src, 0 if T == 1 else 1)
+        st0 = bank.stats()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            k3amd.moe(xs[i % 8], cfg, W, 1, bank.src, 0 if T == 1 else 1)
+        t1 = time.perf_counter()
+        moved = bank.stats()["bytes_uploaded"] - st0["bytes_uploaded"]
+        for k in ("gate", "bias", "latent_norm", "down", "up", "sh1", "sh3", "sh2"):
+            L.k3_dev_unregister(W[k].ctypes.data)
+    finally:
+        bank.destroy()
+    ms = (t1 - t0) / steps * 1e3
+    return {"entry": "k3_moe" if T == 1 else "k3_moe_prefill", "tokens": T, "hidden": E,
+            "latent": 3584, "moe_inter": 3072, "experts": n_experts, "topk": 16, "n_shared": 2,
+            "trunk": "bf16", "ms_per_call": round(ms, 3), "tokens_per_s": round(T / ms * 1e3, 1),
+            "bank_GB": round(n_experts * 17547264 / 1e9, 2), "weight_bytes_uploaded_while_timed": int(moved)}
 
 
 def time_back_to_back(launch, ncalls, per_graph=64, reps=8):
@@ -282,13 +389,16 @@ def time_back_to_back(launch, ncalls, per_graph=64, reps=8):
     return (t1 - t0) / (reps * per_graph) * 1e6
 
 
-def time_gemv(steps=200, copies=128):
-    """2048x7168 MXFP4 GEMV, one token, rotating over `copies` distinct weight copies
+def time_gemv(steps=200, copies=128, rows=2048, inn=E, scale_byte=None):
+    """rows x inn MXFP4 GEMV, one token, rotating over `copies` distinct weight copies
     (>= 1 GB, well past the last-level cache) so every launch streams from HBM. Kernel time
-    from HIP events around each launch; throughput from back-to-back launches in a graph."""
+    from HIP events around each launch; throughput from back-to-back launches in a graph.
+    scale_byte: every E8M0 byte that value (the reference kernel benchmark's 127) instead of
+    the configured distribution."""
     L = k3amd.lib()
-    packed, scales, x = wl.gemv_inputs()
-    rows, inn = packed.shape[0], packed.shape[1] * 2
+    packed, scales, x = wl.gemv_inputs(rows, inn)
+    if scale_byte is not None:
+        scales = np.full_like(scales, scale_byte)
     pk_b, sc_b = packed.nbytes, scales.nbytes
     stride = (pk_b + sc_b + 4095) // 4096 * 4096
     w = k3amd.DevBuf(copies * stride)
@@ -316,7 +426,7 @@ def time_gemv(steps=200, copies=128):
     b2b = time_back_to_back(launch, copies)
     for b in (w, dx, dy, ws):
         b.free()
-    algo = pk_b + sc_b + inn * 4 + rows * 4        # weights + x + y: 7,835,648 B
+    algo = pk_b + sc_b + inn * 4 + rows * 4        # weights + x + y (7,835,648 B at 2048 x 7168)
     ms, n = st.get("gemv", (0.0, 0))
     kern_ms = ms / max(n, 1)
     return {"shape": [rows, inn], "copies_rotated": copies, "algorithmic_bytes": algo,
@@ -392,6 +502,11 @@ def cpu_baseline(T_sample=8, budget_s=10.0):
             "sample": f"{T_sample} tokens of the batch-64 decode layer (router + 8 experts each, "
                       f"SiLU), {len(times)} reps after one warm-up, median; spread "
                       f"{min(times):.3f}-{max(times):.3f} s",
+            "composition": "k3_router per token, then k3_moe's per-token routed loop (k3_ops.c:"
+                           "576-643) with z := x: three k3_matmul_mxfp4 calls per (token, slot). "
+                           "The reference's expert-major k3_moe_prefill chunk makes the same "
+                           "per-(token, slot) GEMV calls (it has no batched MXFP4 kernel) and only "
+                           "reorders them, reusing each expert about 1.8x at batch 64",
             "ms_per_token": round(med / T_sample * 1e3, 2)}
 
 
@@ -497,8 +612,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--only", nargs="+", default=None,
-                    help="time only these workloads (decode64 batch1 gemv trunk ffn prefill "
-                         "skewed) and print their figures instead of the benchmark line")
+                    help="time only these workloads (decode64 batch1 gemv gemv_ref trunk ffn "
+                         "prefill skewed k3moe k3moe64) and print their figures instead of the "
+                         "benchmark line")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (calibrates the HBM "
                          "byte counters of a profiler run) and exit")
@@ -531,6 +647,12 @@ def main():
                              "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st.items()}}
             elif name == "gemv":
                 res[name] = time_gemv()
+            elif name == "gemv_ref":
+                res[name] = time_gemv(copies=192, rows=3072, inn=3584, scale_byte=127)
+            elif name == "k3moe":
+                res[name] = time_k3_moe(1)
+            elif name == "k3moe64":
+                res[name] = time_k3_moe(64, steps=5)
             elif name == "trunk":
                 res[name] = time_trunk_gemv()
             elif name == "ffn":
@@ -565,6 +687,8 @@ def main():
     log(f"bench: batch-1 layer {b1_ms:.3f} ms/step")
     gemv = time_gemv()
     log(f"bench: gemv {gemv}")
+    gemv_ref = time_gemv(copies=192, rows=3072, inn=3584, scale_byte=127)
+    log(f"bench: gemv (reference benchmark shape) {gemv_ref}")
     trunk = time_trunk_gemv()
     log(f"bench: trunk gemv {trunk}")
     ffn = time_expert_ffn(layer)
@@ -573,6 +697,9 @@ def main():
     log(f"bench: prefill {prefill}")
     skewed = time_skewed(layer)
     log(f"bench: skewed {skewed}")
+    layer.free()
+    k3moe = time_k3_moe(1)
+    log(f"bench: k3_moe at the K3 shape {k3moe}")
     line = {
         "metric": "MoE-layer tokens/s + achieved HBM GB/s (MXFP4 expert GEMV), batch 1 & 64",
         "value": round(tok_s, 1),
@@ -604,10 +731,14 @@ def main():
                    "layer_GBps": round(b1_bytes / (b1_ms * 1e-3) / 1e9, 1),
                    "stages_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in st1.items()}},
         "gemv_2048x7168": gemv,
+        "gemv_3072x3584_refbench": dict(gemv_ref, inputs="the reference kernel benchmark's "
+                                        "shape and scale bytes (all 127, bench_kernels.c:129-140); "
+                                        "codes and x from the library's generator"),
         "trunk_gemv_bf16_12288x7168": trunk,
         "expert_ffn_decode": ffn,
         "prefill_4096": prefill,
         "skewed_512_shared": skewed,
+        "k3_moe_decode_k3_shape": k3moe,
     }
     if cb is not None:
         line["cpu_baseline"] = cb

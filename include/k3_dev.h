@@ -8,7 +8,17 @@
  * pointer, work is enqueued on the caller's HIP stream (NULL = the null stream) and the
  * call returns without synchronising. None of them allocates: scratch comes from a
  * caller-provided workspace of the size the matching *_ws() function reports. They
- * return 0, or a negative value with a message available from k3d_error().
+ * return 0, or a negative value with a message available from k3d_error() (kept per host
+ * thread).
+ *
+ * Work that runs beside the caller's (the activation split beside the router, the hot
+ * experts' passes of a skewed prefill batch) goes to a side stream that belongs to the
+ * caller's stream, forked from it and joined back into it by events of its own; so calls
+ * from several host threads on different streams, at once, never share a stream or an
+ * event, and each gives the result it gives alone. A stream's side stream is made by
+ * k3d_stream_create (the null stream's by k3d_init), or by the first call on a stream made
+ * elsewhere; at most 256 caller streams at once. Calls that overlap on one stream, or
+ * share a workspace, race.
  *
  * Each names the reference function whose arithmetic it performs.
  */
@@ -49,6 +59,19 @@ int k3d_graph_destroy(void *exec);
 enum { K3D_STAGE_BEGIN = 0, K3D_STAGE_ROUTER = 1, K3D_STAGE_GATHER = 2, K3D_STAGE_GATEUP = 3,
        K3D_STAGE_DOWN = 4, K3D_STAGE_COMBINE = 5, K3D_STAGE_GEMV = 6, K3D_STAGE_SHARED = 7,
        K3D_STAGE_COUNT = 8 };
+/* Per-workgroup stamps of the batched expert kernels (mx_moe_kernel, mx_prefill_kernel), a
+ * profiling aid beside the stage profiler: between k3d_stamps_begin and k3d_stamps_end, each
+ * launch of those kernels writes, for each of its workgroups, three u64 into the device
+ * buffer dbuf, launch after launch: the workgroup's start and end on the 100 MHz clock and
+ * the hardware id it ran on (XCC id << 32 | the HW_ID register: CU in bits 8-11, shader
+ * array 12, shader engine 13-15). Launches that no longer fit are not stamped. k3d_stamps_end
+ * gives the kinds (K3D_STAMP_*) and grids of the stamped launches in order (up to max; *n =
+ * their number) and stops stamping. Not for graph capture: the buffer region is chosen when a
+ * call enqueues its work. */
+enum { K3D_STAMP_MOE_GATEUP = 1, K3D_STAMP_MOE_DOWN = 2, K3D_STAMP_PREFILL_GATEUP = 3,
+       K3D_STAMP_PREFILL_DOWN = 4 };
+int k3d_stamps_begin(void *dbuf, size_t bytes);
+int k3d_stamps_end(int *kinds, int *grids, int max, int *n);
 int k3d_prof_begin(int max_marks);
 int k3d_prof_mark(void *stream, int stage);
 int k3d_prof_end(double *ms, int *count, int n_stages);

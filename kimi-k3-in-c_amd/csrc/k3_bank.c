@@ -21,7 +21,9 @@
  * The host MoE entry points (k3_moe, k3_moe_prefill) recognise a bank's source and run
  * the experts straight from the slots: after warm-up a call moves no weight bytes over
  * PCIe. During such a call every slot it has fetched is pinned, so a later get() of the
- * same call cannot evict an expert the call still has to compute.
+ * same call cannot evict an expert the call still has to compute. When a call names more
+ * experts than the bank has slots, the call computes what it has fetched before the get()
+ * that would need one more slot, then releases its slots (k3_bank_full, k3_bank_call).
  */
 #include "k3.h"
 #include "k3_bank.h"
@@ -184,6 +186,18 @@ static int src_get(K3ExpertSrc *self, int layer, int expert, K3ExpertQ *out)
     return rc;
 }
 
+/* Whether admitting `expert` now needs a slot the current call cannot give: it is not
+ * pinned by the call and every slot is. */
+static int call_full(const K3DevBank *b, int layer, int expert)
+{
+    if (!b->in_call || !key_ok(b, layer, expert)) return 0;
+    const int slot = b->slot_of[layer * b->n_experts + expert];
+    if (slot >= 0 && b->pin[slot] == b->epoch) return 0;
+    for (int s = 0; s < b->nslot; s++)
+        if (b->key_of[s] < 0 || b->pin[s] != b->epoch) return 0;
+    return 1;
+}
+
 static int src_getmany(K3ExpertSrc *self, int layer, const int *experts, int n)
 {
     K3DevBank *b = (K3DevBank *)self->ctx;
@@ -198,8 +212,11 @@ static int src_getmany(K3ExpertSrc *self, int layer, const int *experts, int n)
         if (nm) b->upstream->getmany(b->upstream, layer, miss, nm);
         free(miss);
     }
+    /* a hint: admissions stop where the call has pinned every slot (its later get()s make
+     * room by computing what is fetched first) */
     int got = 0;
-    for (int i = 0; i < n; i++) got += ensure(b, layer, experts[i], NULL) == 0;
+    for (int i = 0; i < n; i++)
+        if (!call_full(b, layer, experts[i])) got += ensure(b, layer, experts[i], NULL) == 0;
     k3h_unlock();
     return got;
 }
@@ -382,6 +399,15 @@ int k3_bank_layout(const K3ExpertSrc *src, int width, int inter)
     const K3DevBank *b = (const K3DevBank *)src->ctx;
     if (b->width != width || b->inter != inter) return -2;
     return b->layout;
+}
+
+int k3_bank_full(const K3ExpertSrc *src, int layer, int expert)
+{
+    if (!src || src->get != src_get) return 0;
+    k3h_lock();
+    const int r = call_full((const K3DevBank *)src->ctx, layer, expert);
+    k3h_unlock();
+    return r;
 }
 
 void k3_bank_call(K3ExpertSrc *src, int begin)

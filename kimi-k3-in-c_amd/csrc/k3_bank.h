@@ -28,6 +28,9 @@ int k3_bank_layout(const K3ExpertSrc *src, int width, int inter);
 /* Brackets one MoE call on a bank's source (no effect on other sources): slots fetched
  * between begin (1) and end (0) are not evicted before the end. */
 void k3_bank_call(K3ExpertSrc *src, int begin);
+/* 1 when src is a bank inside a call, `expert` is not among the slots the call holds and
+ * the call holds every slot: get() would fail until the call releases its slots. */
+int k3_bank_full(const K3ExpertSrc *src, int layer, int expert);
 
 #ifdef __cplusplus
 }

@@ -15,7 +15,7 @@
 extern const int k3_expf_exc_n;
 extern const uint32_t k3_expf_exc[];
 
-static char g_msg[512];
+static __thread char g_msg[512];   /* the last error, per thread */
 
 static int fail(const char *what)
 {
@@ -75,6 +75,8 @@ int k3d_prof_end(double *ms, int *count, int n_stages)
     return k3k_prof_collect(ms, count, n_stages) ? fail("prof_end") : 0;
 }
 int k3d_prof_mark(void *stream, int stage) { return k3k_prof_mark(stream, stage) ? fail("prof_mark") : 0; }
+int k3d_stamps_begin(void *dbuf, size_t bytes) { return k3k_stamps_enable(dbuf, bytes); }
+int k3d_stamps_end(int *kinds, int *grids, int max, int *n) { return k3k_stamps_collect(kinds, grids, max, n); }
 
 /* The libm exception table of the router score and its bucket index, uploaded once per
  * process. */

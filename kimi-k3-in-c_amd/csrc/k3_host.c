@@ -588,6 +588,8 @@ static void mmw_dev(float *y_d, const float *x_d, int ntok, const void *W, int w
 }
 
 /* ---------------------------------------------------- streamed-expert fetching ---- */
+#define MOE_DEV_BLOCK 1024    /* tokens per device pass of the experts (bounds contrib) */
+
 /* The experts of one MoE call, fetched through K3ExpertSrc in exactly the order the
  * reference calls it, so a source sees the same get / getmany / resident sequence and the
  * same drops are counted:
@@ -606,12 +608,57 @@ typedef struct {
     const K3MoeW *w;
     int L, I, N, K, T;
     int bank_layout;          /* -1: the source hands out host pointers; else K3_BANK_* */
-    QPtr *bank;               /* [N] device pointers of the fetched experts */
+    QPtr *bank;               /* [N] device pointers of the experts fetched since the last pass */
     char *arena;
     size_t off;
     int *hidx, *didx;
     float *hwt;
+    /* the device passes: assignments computed so far, one pass's routing, the device
+     * aggregate [T][L], latent activations, routing and weights */
+    unsigned char *done;
+    int *pidx;
+    int passes;
+    float *dacc;
+    const float *dz;
+    int *di;
+    float *dwt;
+    float b1, b2;
 } Fetch;
+
+/* One device pass over the assignments whose experts have been fetched since the last pass
+ * and that no earlier pass has computed (every other slot -1: it contributes nothing). The
+ * first pass writes the aggregate, later ones add onto it. */
+static void run_fetched(Fetch *f)
+{
+    const int L = f->L, K = f->K, T = f->T;
+    const size_t TK = (size_t)T * K;
+    int any = 0;
+    for (size_t a = 0; a < TK; a++) {
+        const int e = f->didx[a];
+        const int ready = !f->done[a] && e >= 0 && e < f->N && f->bank[e].p1;
+        f->pidx[a] = ready ? e : -1;
+        if (ready) {
+            f->done[a] = 1;
+            any = 1;
+        }
+    }
+    if (!any && f->passes > 0) return;
+    float *dst = f->passes == 0 ? f->dacc : (float *)buf(B_SDN, (size_t)T * L * 4);
+    check(k3k_h2d(f->di, f->pidx, TK * 4, g_stream), "host to device copy");
+    check(k3k_h2d(f->dwt, f->hwt, TK * 4, g_stream), "host to device copy");
+    const int layout = f->bank_layout >= 0 ? f->bank_layout : K3D_LAYOUT_ROWS;
+    for (int b0 = 0; b0 < T; b0 += MOE_DEV_BLOCK) {
+        const int nb = T - b0 < MOE_DEV_BLOCK ? T - b0 : MOE_DEV_BLOCK;
+        const size_t o = (size_t)b0 * K;
+        run_bank(dst + (size_t)b0 * L, f->pidx + o, f->di + o, f->dwt + o, f->dz + (size_t)b0 * L, nb,
+                 f->bank, L, f->I, f->N, K, K3_ACT_SITU, f->b1, f->b2, 0, layout);
+    }
+    if (f->passes > 0) {
+        check(k3k_axpy_rows(f->dacc, dst, (size_t)T * L, g_stream), "aggregate");
+        check(k3k_sync(g_stream), "synchronize");
+    }
+    f->passes++;
+}
 
 static int fetch(Fetch *f, int e, int via_resident)
 {
@@ -619,6 +666,15 @@ static int fetch(Fetch *f, int e, int via_resident)
     K3ExpertQ q;
     memset(&q, 0, sizeof q);
     int miss;
+    /* An HBM bank whose slots this call all holds: compute what is fetched, release the
+     * slots, then fetch (the reference's cache multiplies each expert before its next get,
+     * so it never needs more than topk + 1 slots; k3_cache.c:305) */
+    if (!via_resident && f->bank_layout >= 0 && k3_bank_full(s, f->w->layer, e)) {
+        run_fetched(f);
+        k3_bank_call(s, 0);
+        k3_bank_call(s, 1);
+        memset(f->bank, 0, (size_t)f->N * sizeof(QPtr));
+    }
     if (via_resident) miss = !s->resident || !s->resident(s, f->w->layer, e, &q);
     else miss = s->get(s, f->w->layer, e, &q) != 0;
     /* a source that reports success with a missing tensor is treated as a failed fetch
@@ -702,7 +758,6 @@ static void fetch_chunk(Fetch *f, int t0, int n, int *uniq, unsigned char *seen)
  * the fetch order and drop accounting of k3_moe_prefill's expert-major chunks over
  * k3_moe's per-token one. idx/wt receive what the reference leaves there: the last
  * token's routing after a per-token pass, nothing after a batched chunk. */
-#define MOE_DEV_BLOCK 1024    /* tokens per device pass of the experts (bounds contrib) */
 
 static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T,
                        int *idx_last, float *wt_last, int batched)
@@ -757,6 +812,13 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
         f.hidx = hidx;
         f.didx = didx;
         f.hwt = hwt;
+        f.dacc = dacc;
+        f.dz = dz;
+        f.di = di;
+        f.dwt = dwt;
+        f.b1 = c->situ_b1;
+        f.b2 = c->situ_b2;
+        for (size_t a = 0; a < TK; a++) didx[a] = -1;
         f.bank_layout = k3_bank_layout(w->src, L, I);
         if (f.bank_layout == -2) {
             fprintf(stderr, "k3: FATAL, k3_moe: the HBM expert bank holds experts of another "
@@ -764,9 +826,11 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
             abort();
         }
         f.bank = (QPtr *)calloc((size_t)N, sizeof(QPtr));
+        f.done = (unsigned char *)calloc(TK, 1);
+        f.pidx = (int *)malloc(TK * sizeof(int));
         int *uniq = (int *)malloc(TK * sizeof(int));
         unsigned char *seen = (unsigned char *)calloc((size_t)N, 1);
-        if (!f.bank || !uniq || !seen) {
+        if (!f.bank || !f.done || !f.pidx || !uniq || !seen) {
             fprintf(stderr, "k3: FATAL, host allocation in k3_moe failed.\n");
             abort();
         }
@@ -796,18 +860,13 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
             for (int t = 0; t < T; t++) fetch_token(&f, t);
             wrote_last = 1;
         }
-        /* the routing the device uses: kept slots, renormalised weights */
-        check(k3k_h2d(di, didx, TK * 4, g_stream), "host to device copy");
-        check(k3k_h2d(dwt, hwt, TK * 4, g_stream), "host to device copy");
-        const int layout = f.bank_layout >= 0 ? f.bank_layout : K3D_LAYOUT_ROWS;
-        for (int b0 = 0; b0 < T; b0 += MOE_DEV_BLOCK) {
-            const int nb = T - b0 < MOE_DEV_BLOCK ? T - b0 : MOE_DEV_BLOCK;
-            const size_t o = (size_t)b0 * K;
-            run_bank(dacc + (size_t)b0 * L, didx + o, di + o, dwt + o, dz + (size_t)b0 * L, nb,
-                     f.bank, L, I, N, K, K3_ACT_SITU, c->situ_b1, c->situ_b2, 0, layout);
-        }
+        /* the assignments not computed yet, on the routing the device uses: kept slots,
+         * renormalised weights */
+        run_fetched(&f);
         k3_bank_call(w->src, 0);
         free(f.bank);
+        free(f.done);
+        free(f.pidx);
         free(uniq);
         free(seen);
     } else {

@@ -1147,6 +1147,7 @@ void mx_moe_kernel(K3kMxArgs a)
     const int n_items = (*a.n_passes) * n_rb;
     /* requires K % 512 == 0: the host routes other K to mx_gemm_kernel */
 
+    const unsigned long long t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0ull;
     for (int i = tid; i < 2 * NS * LDT / 8; i += 64 * NW) {
         const int bh = i / (LDT / 8), o = i % (LDT / 8);
         *reinterpret_cast<uint4 *>(&bsh[bh / NS][bh % NS][PT][o * 8]) = make_uint4(0, 0, 0, 0);
@@ -1393,13 +1394,16 @@ void mx_moe_kernel(K3kMxArgs a)
             }
         }
     }
+    if (a.stamps && tid == 0) k3_stamp_end(a.stamps, t_start);
 }
 
 template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT, int DEPTH = 1, int NB = 1>
 int launch_moe(const K3kMxArgs *a, int grid, hipStream_t st)
 {
+    K3kMxArgs b = *a;
+    b.stamps = k3k_stamps_take(MODE == K3K_MX_GATEUP ? 1 : 2, grid);
     hipLaunchKernelGGL((mx_moe_kernel<MODE, MT, NS, PT, NB, NW, WPE, LAYOUT, DEPTH>), dim3(grid), dim3(64 * NW),
-                       0, st, *a);
+                       0, st, b);
     K3K_LAUNCH_CHECK("mx_moe launch");
     return 0;
 }
@@ -1494,6 +1498,7 @@ void mx_prefill_kernel(K3kMxArgs a)
      * offset select would cost it registers it does not have. The wave-uniform part of
      * each address stays clamped inside the buffer. */
     constexpr uint32_t OOB = 0x80000000u;
+    const unsigned long long t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0ull;
 
     for (int item = li; item < n_items; item += nlw) {
         const int rb = item % n_rb, pass = pbeg + item / n_rb;
@@ -1718,12 +1723,15 @@ void mx_prefill_kernel(K3kMxArgs a)
             }
         }
     }
+    if (a.stamps && tid == 0) k3_stamp_end(a.stamps, t_start);
 }
 
 template <int MODE, int MT, int NB, int SPC, int NW>
 int launch_prefill(const K3kMxArgs *a, int grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((mx_prefill_kernel<MODE, MT, NB, SPC, NW>), dim3(grid), dim3(64 * NW), 0, st, *a);
+    K3kMxArgs b = *a;
+    b.stamps = k3k_stamps_take(MODE == K3K_MX_GATEUP ? 3 : 4, grid);
+    hipLaunchKernelGGL((mx_prefill_kernel<MODE, MT, NB, SPC, NW>), dim3(grid), dim3(64 * NW), 0, st, b);
     K3K_LAUNCH_CHECK("mx_prefill launch");
     return 0;
 }

@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
                                                                   const float *x, int T,
                                                                   const float *W, int hidden,
                                                                   int n_experts, int chunk, int vec,
-                                                                  int nks_xcd, int *ctr)
+                                                                  int deal, int *ctr)
 {
     /* the final kernel's arrival counter starts every launch at zero */
     if (ctr && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) *ctr = 0;
@@ -138,17 +138,34 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
     __shared__ float xn[2][TB];                          /* max |x| over the sub-block */
     const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
     const int wt = wv >> 1, we = wv & 1;                 /* the wave's block of the tile */
-    /* nks_xcd > 0 (a one-dimensional grid, nks_xcd chunks): the workgroups of one chunk run
-     * on one XCD (workgroup b runs on XCD b % 8), so that its W and x pieces are fetched
-     * into that XCD's L2 once instead of once per token tile / expert tile */
+    /* A one-dimensional grid dealt to the XCDs (workgroup b runs on XCD b % 8), so that
+     * each W and x piece is fetched into one XCD's L2 once instead of once per token tile /
+     * expert tile:
+     *   deal 1 (a chunk count that is a multiple of 8): the workgroups of one chunk run on
+     *     one XCD;
+     *   deal 2: the (chunk, token tile) pairs, chunk-major, in eight contiguous ranges, one
+     *     per XCD; an XCD walks its pairs in order, the expert tiles of a pair one after
+     *     another (they share the pair's x piece), the token tiles of a chunk one after
+     *     another (they share the chunk's W pieces). */
     int bx = blockIdx.x, by = blockIdx.y, ks = blockIdx.z;
-    if (nks_xcd > 0) {
-        const int nee = (n_experts + EB - 1) / EB, g = nee * ((T + TB - 1) / TB);
-        const int i = blockIdx.x / K3_NXCD;
-        ks = blockIdx.x % K3_NXCD + K3_NXCD * (i / g);
-        if (ks >= nks_xcd) return;
-        bx = (i % g) % nee;
-        by = (i % g) / nee;
+    if (deal) {
+        const int nee = (n_experts + EB - 1) / EB, ntt = (T + TB - 1) / TB;
+        const int nks = (hidden + chunk - 1) / chunk;
+        const int i = blockIdx.x / K3_NXCD, xcd = blockIdx.x % K3_NXCD;
+        if (deal == 1) {
+            const int g = nee * ntt;
+            ks = xcd + K3_NXCD * (i / g);
+            if (ks >= nks) return;
+            bx = (i % g) % nee;
+            by = (i % g) / nee;
+        } else {
+            const int per = (nks * ntt + K3_NXCD - 1) / K3_NXCD, pi = i / nee;
+            const int pr = xcd * per + pi;
+            if (pi >= per || pr >= nks * ntt) return;
+            ks = pr / ntt;
+            by = pr % ntt;
+            bx = i % nee;
+        }
     }
     const int e0 = bx * EB, t0 = by * TB;
     const int kb0 = ks * chunk, kb1 = min(hidden, kb0 + chunk);
@@ -743,17 +760,20 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
     }
     if constexpr (GATHER) {
         /* The workgroup that finishes last runs the gather over every token's idx: each
-         * workgroup's idx stores are acknowledged (vmcnt 0) before it counts itself in, and
-         * the last one reads idx with agent-scope loads. It leaves the counter at zero (the
-         * partial kernel zeroes it before every launch as well). */
+         * workgroup's idx stores are acknowledged (vmcnt 0) before it counts itself in with
+         * an agent-scope release, and the last one acquires at agent scope (the count is
+         * acq_rel) before it reads idx with agent-scope loads, so every idx store
+         * happens-before the gather's loads. It leaves the counter at zero (the partial
+         * kernel zeroes it before every launch as well). */
         __shared__ int s_last;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0)
-            s_last = __hip_atomic_fetch_add(g.ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            s_last = __hip_atomic_fetch_add(g.ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
                      (int)gridDim.x - 1;
         __syncthreads();
         if (s_last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             gather_block<true>(g);
             if (tid == 0) __hip_atomic_store(g.ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -1322,17 +1342,19 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
     } else {
         static_assert(RM_TB == 32 * 1 && RM_EB == 32 * 2, "tile of router_partial_mfma_kernel<1, 2>");
         const int nee = (n_experts + RM_EB - 1) / RM_EB, ntt = (T + RM_TB - 1) / RM_TB;
-        /* a chunk count that is a multiple of the XCD count: the chunks dealt to the XCDs */
-        const int xg = (ks % K3_NXCD == 0) ? ks : 0;
-        const dim3 grid = xg ? dim3((unsigned)(nee * ntt * ks)) : dim3(nee, ntt, ks);
+        /* dealt to the XCDs: whole chunks when their count is a multiple of the XCD count,
+         * else ranges of (chunk, token tile) pairs */
+        const int deal = ks % K3_NXCD == 0 ? 1 : 2;
+        const int per = (ks * ntt + K3_NXCD - 1) / K3_NXCD;
+        const dim3 grid = deal == 1 ? dim3((unsigned)(nee * ntt * ks)) : dim3((unsigned)(K3_NXCD * per * nee));
         const bool buf = vec && (size_t)n_experts * hidden * 4 < 0x80000000u &&
                          (size_t)T * hidden * 4 < 0x80000000u;
         if (buf)
             hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, true>), grid, dim3(256), 0, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec, xg, ctr);
+                               rbound, x, T, W, hidden, n_experts, chunk, vec, deal, ctr);
         else
             hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, false>), grid, dim3(256), 0, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec, xg, ctr);
+                               rbound, x, T, W, hidden, n_experts, chunk, vec, deal, ctr);
     }
     K3K_LAUNCH_CHECK("router_partial launch");
     return 0;

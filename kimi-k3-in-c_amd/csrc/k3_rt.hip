@@ -6,11 +6,13 @@
 #include "k3_common.h"
 #include "k3k.h"
 
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
-static char g_err[512];
+/* the last error, per thread */
+static thread_local char g_err[512];
 static int g_ready = 0;
 static int g_cus = 0;
 
@@ -124,6 +126,84 @@ extern "C" int k3k_sync(void *stream)
     return e == hipSuccess ? 0 : k3k_fail("synchronize", e);
 }
 
+/* ---- side streams --------------------------------------------------------------------
+ * Work that may run beside the caller's (the activation split beside the router, the hot
+ * experts' pass list) goes to a side stream of the caller's stream: one per caller stream,
+ * created with the default priority, non-blocking, with its own fork and join events.
+ * Work is forked after what is already queued on the caller's stream and joined back into
+ * it; both are event waits, so a stream being captured into a graph captures the side work
+ * too, and calls that overlap on different caller streams never share a stream or an
+ * event. Entries are made by k3k_side_init (the null stream, at initialisation), by
+ * k3k_stream_create, or on a caller stream's first fork; k3k_stream_destroy removes its
+ * stream's entry. */
+#define K3_SIDE_MAX 256
+struct K3Side {
+    hipStream_t caller, side;
+    hipEvent_t fork, join;
+};
+static K3Side g_side[K3_SIDE_MAX];
+static int g_nside = 0;
+static pthread_mutex_t g_side_mu = PTHREAD_MUTEX_INITIALIZER;
+
+/* The entry of caller stream s (made if absent), or NULL with the error set. */
+static K3Side *side_of(hipStream_t s)
+{
+    pthread_mutex_lock(&g_side_mu);
+    K3Side *r = nullptr;
+    for (int i = 0; i < g_nside; i++)
+        if (g_side[i].caller == s) {
+            r = &g_side[i];
+            break;
+        }
+    if (!r) {
+        if (g_nside == K3_SIDE_MAX) {
+            k3k_fail("side stream: more than 256 caller streams", hipErrorInvalidValue);
+        } else {
+            K3Side n = {s, nullptr, nullptr, nullptr};
+            hipError_t e = hipStreamCreateWithFlags(&n.side, hipStreamNonBlocking);
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming);
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&n.join, hipEventDisableTiming);
+            if (e == hipSuccess) {
+                g_side[g_nside] = n;
+                r = &g_side[g_nside++];
+            } else {
+                k3k_fail("side stream: create", e);
+                if (n.join) (void)hipEventDestroy(n.join);
+                if (n.fork) (void)hipEventDestroy(n.fork);
+                if (n.side) (void)hipStreamDestroy(n.side);
+            }
+        }
+    }
+    pthread_mutex_unlock(&g_side_mu);
+    return r;
+}
+
+extern "C" int k3k_side_init(void)
+{
+    if (k3k_init()) return -1;
+    return side_of(nullptr) ? 0 : -1;
+}
+
+extern "C" int k3k_fork(void *stream, void **side)
+{
+    K3Side *sd = side_of((hipStream_t)stream);
+    if (!sd) return -1;
+    hipError_t e = hipEventRecord(sd->fork, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(sd->side, sd->fork, 0);
+    if (e != hipSuccess) return k3k_fail("fork", e);
+    *side = sd->side;
+    return 0;
+}
+
+extern "C" int k3k_join(void *stream)
+{
+    K3Side *sd = side_of((hipStream_t)stream);
+    if (!sd) return -1;
+    hipError_t e = hipEventRecord(sd->join, sd->side);
+    if (e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)stream, sd->join, 0);
+    return e == hipSuccess ? 0 : k3k_fail("join", e);
+}
+
 extern "C" void *k3k_stream_create(void)
 {
     hipStream_t s = nullptr;
@@ -132,59 +212,32 @@ extern "C" void *k3k_stream_create(void)
         k3k_fail("hipStreamCreate", e);
         return nullptr;
     }
+    if (!side_of(s)) {
+        (void)hipStreamDestroy(s);
+        return nullptr;
+    }
     return (void *)s;
 }
 
 extern "C" int k3k_stream_destroy(void *stream)
 {
     if (!stream) return 0;
+    pthread_mutex_lock(&g_side_mu);
+    for (int i = 0; i < g_nside; i++)
+        if (g_side[i].caller == (hipStream_t)stream) {
+            (void)hipStreamSynchronize(g_side[i].side);
+            (void)hipEventDestroy(g_side[i].fork);
+            (void)hipEventDestroy(g_side[i].join);
+            (void)hipStreamDestroy(g_side[i].side);
+            g_side[i] = g_side[--g_nside];
+            break;
+        }
+    pthread_mutex_unlock(&g_side_mu);
     hipError_t e = hipStreamDestroy((hipStream_t)stream);
     return e == hipSuccess ? 0 : k3k_fail("hipStreamDestroy", e);
 }
 
 /* ---- HIP graphs: capture the work enqueued on a stream once, replay it with one launch */
-/* A second stream for work that may run beside the caller's (the hot experts' pass list):
- * created on first use with the default priority, non-blocking, with two events. Work is
- * forked after what is already queued on the caller's stream and joined back into it; both
- * are event waits, so a stream being captured into a graph captures the side work too.
- * Calls that overlap on different caller streams would share it: the library serialises
- * on one stream per instance. */
-static hipStream_t g_side = nullptr;
-static hipEvent_t g_fork = nullptr, g_join = nullptr;
-
-/* Creates the side stream and its events (once); k3d_init calls it so that no later entry
- * point creates anything. */
-extern "C" int k3k_side_init(void)
-{
-    if (k3k_init()) return -1;
-    if (!g_side) {
-        hipError_t e = hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking);
-        if (e != hipSuccess) return k3k_fail("fork: hipStreamCreate", e);
-        e = hipEventCreateWithFlags(&g_fork, hipEventDisableTiming);
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&g_join, hipEventDisableTiming);
-        if (e != hipSuccess) return k3k_fail("fork: hipEventCreate", e);
-    }
-    return 0;
-}
-
-extern "C" int k3k_fork(void *stream, void **side)
-{
-    if (k3k_side_init()) return -1;
-    hipError_t e = hipEventRecord(g_fork, (hipStream_t)stream);
-    if (e == hipSuccess) e = hipStreamWaitEvent(g_side, g_fork, 0);
-    if (e != hipSuccess) return k3k_fail("fork", e);
-    *side = g_side;
-    return 0;
-}
-
-extern "C" int k3k_join(void *stream)
-{
-    if (!g_side) return k3k_fail("join without fork", hipErrorInvalidValue);
-    hipError_t e = hipEventRecord(g_join, g_side);
-    if (e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)stream, g_join, 0);
-    return e == hipSuccess ? 0 : k3k_fail("join", e);
-}
-
 extern "C" int k3k_graph_begin(void *stream)
 {
     if (!stream) return k3k_fail("graph capture needs a created stream", hipErrorInvalidValue);
@@ -293,5 +346,46 @@ extern "C" int k3k_prof_collect(double *ms, int *count, int n_stages)
     }
     g_prof_on = 0;
     g_ev_n = 0;
+    return 0;
+}
+
+/* ---- per-workgroup stamps of the expert kernels (profiling) -------------------------- */
+namespace {
+unsigned long long *g_st_buf = nullptr;
+size_t g_st_cap = 0, g_st_used = 0;          /* in u64 */
+constexpr int K3_ST_MAXL = 4096;
+int g_st_kind[K3_ST_MAXL], g_st_grid[K3_ST_MAXL], g_st_n = 0;
+}  // namespace
+
+extern "C" int k3k_stamps_enable(void *dbuf, size_t bytes)
+{
+    g_st_buf = (unsigned long long *)dbuf;
+    g_st_cap = dbuf ? bytes / 8 : 0;
+    g_st_used = 0;
+    g_st_n = 0;
+    return 0;
+}
+
+extern "C" unsigned long long *k3k_stamps_take(int kind, int grid)
+{
+    if (!g_st_buf || grid <= 0 || g_st_n >= K3_ST_MAXL || g_st_used + 3 * (size_t)grid > g_st_cap)
+        return nullptr;
+    unsigned long long *p = g_st_buf + g_st_used;
+    g_st_used += 3 * (size_t)grid;
+    g_st_kind[g_st_n] = kind;
+    g_st_grid[g_st_n] = grid;
+    g_st_n++;
+    return p;
+}
+
+extern "C" int k3k_stamps_collect(int *kinds, int *grids, int max, int *n)
+{
+    const int m = g_st_n < max ? g_st_n : max;
+    for (int i = 0; i < m; i++) {
+        if (kinds) kinds[i] = g_st_kind[i];
+        if (grids) grids[i] = g_st_grid[i];
+    }
+    if (n) *n = g_st_n;
+    k3k_stamps_enable(nullptr, 0);
     return 0;
 }

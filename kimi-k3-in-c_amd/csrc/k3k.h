@@ -124,7 +124,18 @@ typedef struct {
      * idle otherwise); k3k_mx_decode_combine forms act(gate, up) and its bf16 terms from them
      * while staging (the same functions, the same result). NULL: the activation terms. */
     float *gu;
+    /* Per-workgroup stamps of the batched expert kernels (k3k_stamps_take), [grid][3] u64:
+     * start and end (s_memrealtime, 100 MHz) and the hardware id (XCC_ID << 32 | HW_ID), or
+     * NULL. The launchers fill it in. */
+    unsigned long long *stamps;
 } K3kMxArgs;
+
+/* Per-workgroup stamps (a profiling aid): while enabled, each launch of mx_moe_kernel /
+ * mx_prefill_kernel takes the next grid * 3 u64 of the device buffer, in launch order;
+ * collect returns the launches' kinds (K3D_STAMP_*) and grids and disables. */
+int k3k_stamps_enable(void *dbuf, size_t bytes);
+unsigned long long *k3k_stamps_take(int kind, int grid);
+int k3k_stamps_collect(int *kinds, int *grids, int max, int *n);
 
 int k3k_mx_gemm(int mode, const K3kMxArgs *a, void *stream);
 

@@ -123,6 +123,8 @@ def _declare(L):
     d("k3d_graph_end", I, P, P)
     d("k3d_graph_launch", I, P, P)
     d("k3d_graph_destroy", I, P)
+    d("k3d_stamps_begin", I, P, SZ)
+    d("k3d_stamps_end", I, P, P, I, P)
     d("k3d_prof_begin", I, I)
     d("k3d_prof_mark", I, P, I)
     d("k3d_prof_end", I, P, P, I)

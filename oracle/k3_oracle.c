@@ -342,6 +342,67 @@ void orc_expert_ffn(float *out, const float *x, const OrcExpertQ *q, int hidden,
     free(dn);
 }
 
+/* orc_expert_ffn for n tokens of one expert, expert-major (the reference's prefill order,
+ * k3_ops.c:742-794): each matrix is dequantized once (orc_mxfp4_dequant: E2M1 x 2^(s-127)
+ * folded in fp32, exact, byte 255 -> 0) and every weight row is dotted against all n
+ * tokens while it is in cache, out[t] = down(act(gate x_t, up x_t)) with no combine
+ * weight. The dot product is dot16_f32: fp64 fma into 16 lanes by element index mod 16,
+ * then the reduction (l[m]+l[8+m])+(l[4+m]+l[12+m]) and (q0+q2)+(q1+q3), the operation
+ * order of row_flat (the reference's flat-row path, k3_ops.c:1435-1532); with every scale
+ * byte below 255, or finite activations, the products and sums are those of
+ * orc_matmul_mxfp4 (a skipped chunk adds nothing, a zero weight adds +-0), so each output
+ * equals orc_expert_ffn's. Test helper for full batch sizes: it is the per-token oracle
+ * reordered, and the tests check the two against each other. */
+#define FM_R 8       /* rows and tokens per cache tile */
+#define FM_T 16
+
+void orc_expert_ffn_many(float *out, const float *x, int n, const OrcExpertQ *q, int hidden,
+                         int inter, int act, float b1, float b2)
+{
+    const size_t big = (size_t)hidden * inter;
+    float *w = (float *)malloc(big * sizeof(float));
+    float *gu = (float *)malloc((size_t)n * 2 * inter * sizeof(float));
+    float *a = (float *)malloc((size_t)n * inter * sizeof(float));
+    if (!w || !gu || !a) fatal("oracle allocation", n);
+    for (int m = 0; m < 2; m++) {
+        const unsigned char *pk = m == 0 ? q->p1 : q->p3, *sc = m == 0 ? q->s1 : q->s3;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+        for (int r = 0; r < inter; r++)
+            orc_mxfp4_dequant(w + (size_t)r * hidden, pk + (size_t)r * (hidden / 2),
+                              sc + (size_t)r * ((hidden + 31) / 32), 1, hidden / 2, 32);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+        for (int r0 = 0; r0 < inter; r0 += FM_R)
+            for (int t0 = 0; t0 < n; t0 += FM_T)          /* a tile of tokens stays in cache */
+                for (int r = r0; r < r0 + FM_R && r < inter; r++)
+                    for (int t = t0; t < t0 + FM_T && t < n; t++)
+                        gu[(size_t)t * 2 * inter + (size_t)m * inter + r] =
+                            (float)dot16_f32(w + (size_t)r * hidden, x + (size_t)t * hidden, hidden);
+    }
+    for (int t = 0; t < n; t++) act_apply(a + (size_t)t * inter, gu + (size_t)t * 2 * inter, inter, act, b1, b2);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int r = 0; r < hidden; r++)
+        orc_mxfp4_dequant(w + (size_t)r * inter, q->p2 + (size_t)r * (inter / 2),
+                          q->s2 + (size_t)r * ((inter + 31) / 32), 1, inter / 2, 32);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int r0 = 0; r0 < hidden; r0 += FM_R)
+        for (int t0 = 0; t0 < n; t0 += FM_T)
+            for (int r = r0; r < r0 + FM_R && r < hidden; r++)
+                for (int t = t0; t < t0 + FM_T && t < n; t++)
+                    out[(size_t)t * hidden + r] =
+                        (float)dot16_f32(w + (size_t)r * inter, a + (size_t)t * inter, inter);
+    free(w);
+    free(gu);
+    free(a);
+}
+
 void orc_moe_routed(float *out, int *idx, float *wt, const float *x, int T,
                     const float *router_w, const float *bias, const OrcExpertQ *bank,
                     int hidden, int inter, int n_experts, int topk, int renorm,

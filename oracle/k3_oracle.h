@@ -50,6 +50,12 @@ void orc_rmsnorm(float *y, const float *x, const float *w, int n, float eps);
 void orc_expert_ffn(float *out, const float *x, const OrcExpertQ *q, int hidden, int inter,
                     int act, float b1, float b2, float wt);
 
+/* The same expert for n tokens x[n][hidden], expert-major: out[t] = down(act(gate x_t,
+ * up x_t)) (no combine weight), each matrix dequantized once; equal to orc_expert_ffn per
+ * token (a reordering of the same operations; tests pin the two together). */
+void orc_expert_ffn_many(float *out, const float *x, int n, const OrcExpertQ *q, int hidden,
+                         int inter, int act, float b1, float b2);
+
 /* Routed MoE layer over T tokens: k3_moe's routed loop (k3_ops.c:576-643) with z := x
  * and no latent/shared tail. bank[e] addresses expert e. idx/wt are [T][topk]. */
 void orc_moe_routed(float *out, int *idx, float *wt, const float *x, int T,

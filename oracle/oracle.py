@@ -122,9 +122,34 @@ class Oracle(_Checker):
         self._fill_bf16 = self._fn("orc_fill_bf16", None, P, C.c_size_t, C.c_uint)
         self._threads = self._fn("orc_threads", I)
         self._latent = self._fn("orc_moe_latent", None, P, P, P, P, I)
+        self._ffn_many = self._fn("orc_expert_ffn_many", None, P, P, I, C.POINTER(ExpertQ), I, I,
+                                  I, F, F)
 
     def threads(self):
         return self._threads()
+
+    def expert_ffn_many(self, X, ex, hidden, inter, act=1, b1=4.0, b2=25.0):
+        """orc_expert_ffn (combine weight 1) for every row of X, expert-major."""
+        X = _f32(X).reshape(-1, hidden)
+        out = np.empty((X.shape[0], hidden), np.float32)
+        q = ExpertQ(*[a.ctypes.data for a in ex.t])
+        self._ffn_many(_p(out), _p(X), X.shape[0], C.byref(q), hidden, inter, act, b1, b2)
+        return out
+
+    def moe_outputs(self, X, idx, wt, bank, hidden, inter, act=1, b1=4.0, b2=25.0):
+        """out[t] = 0 + sum_j wt[t][j] * expert_ffn(idx[t][j], x[t]), j ascending, in fp32
+        (k3_moe's routed loop, k3_ops.c:628-642), the experts evaluated expert-major.
+        bank[e]: the host expert e (needed for every e in idx)."""
+        X = _f32(X).reshape(-1, hidden)
+        T, K = idx.shape
+        contrib = np.empty((T, K, hidden), np.float32)
+        for e in np.unique(idx):
+            ts, js = np.nonzero(idx == e)
+            contrib[ts, js] = self.expert_ffn_many(X[ts], bank[int(e)], hidden, inter, act, b1, b2)
+        out = np.zeros((T, hidden), np.float32)
+        for j in range(K):
+            out = out + wt[:, j:j + 1].astype(np.float32) * contrib[:, j]
+        return out
 
     def expert_ffn(self, x, ex, hidden, inter, act=1, b1=4.0, b2=25.0, wt=1.0):
         out = np.empty(hidden, np.float32)
@@ -200,6 +225,23 @@ class Oracle(_Checker):
         return out
 
 
+def q8_rows(rng, inn, out):
+    """Random k3_matmul_q8 weights: each row a float32 scale then inn int8 values."""
+    sc = (rng.random(out) * 0.02 + 0.001).astype(np.float32)
+    q = rng.integers(-128, 128, (out, inn), dtype=np.int64).astype(np.int8)
+    W = np.empty((out, 4 + inn), np.uint8)
+    W[:, :4] = sc.view(np.uint8).reshape(out, 4)
+    W[:, 4:] = q.view(np.uint8)
+    return W, sc, q
+
+
+def q8_exact(x, sc, q):
+    """k3_matmul_q8 in exact arithmetic: (sum_i q[o][i] * x[i]) * scale[o], in fp64
+    (every product and the sum of 7168 of them are exact in fp64 up to one rounding per
+    addition of magnitudes far below 2^53 ulps of the result)."""
+    return (q.astype(np.float64) @ np.asarray(x, np.float64)) * sc.astype(np.float64)
+
+
 class Ref(_Checker):
     """The compiled reference. Available wherever oracle/_ref was built."""
     prefix = "k3_"
@@ -219,6 +261,15 @@ class Ref(_Checker):
         self._moe = self.comp.ref_moe_routed
         self._moe.restype = I
         self._moe.argtypes = [P, P, P, P, I, P, P, P, I, I, I, I, I, F, I, F, F]
+
+    def matmul_q8(self, x, Wq, inn, out):
+        """k3_matmul_q8 (k3_ops.c:1221-1289): rows of [f32 scale][int8 x inn]."""
+        fn = self.lib.k3_matmul_q8
+        fn.restype = None
+        fn.argtypes = [P, P, P, I, I]
+        y = np.empty(out, np.float32)
+        fn(_p(y), _p(_f32(x)), _p(_u8(Wq)), inn, out)
+        return y
 
     def expert_ffn(self, x, ex, hidden, inter, act=1, b1=4.0, b2=25.0, wt=1.0):
         out = np.empty(hidden, np.float32)

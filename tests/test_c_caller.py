@@ -35,6 +35,20 @@ def test_c_caller_builds_against_the_header(tmp_path):
     assert need <= _syms(LIB, "--defined-only")
 
 
+def test_integration_snippet_compiles(tmp_path):
+    """The resident-weights example of the integration guide compiles against the header
+    with the exported signatures."""
+    subprocess.run(["gcc", "-std=c99", "-O2", "-Wall", "-Wextra", "-Werror", "-c",
+                    "-I" + os.path.join(os.path.dirname(HERE), "include"),
+                    os.path.join(CDIR, "k3_resident_snippet.c"), "-o", str(tmp_path / "s.o")],
+                   check=True)
+    src = open(os.path.join(CDIR, "k3_resident_snippet.c")).read()
+    guide = open(os.path.join(os.path.dirname(HERE), "INTEGRATION.md")).read()
+    for line in ("k3_dev_register(w->gate, (size_t)c->n_experts * c->hidden * sizeof(float));",
+                 "k3_moe(out, x, w, c, T, idx, wt, scratch);"):
+        assert line in src and line in guide
+
+
 @pytest.mark.gpu
 def test_c_caller_outputs(gpu, orc, tmp_path):
     assert os.path.exists(BIN), "tests/c/k3_caller is built by __graft_entry__.build()"

@@ -91,3 +91,34 @@ def test_shared_expert_config4_shape(gpu, orc, wl, T, prec):
         want = y0[t] + s
         assert max_err_rel_inf(got[t], want) <= tol, t
         assert max_err_rel_inf(got[t] - y0[t], s) <= (tol if prec == 0 else 2e-2), t
+
+
+@pytest.mark.parametrize("inn,out", [(7168, 3584), (300, 17), (16, 3)])
+def test_matmul_q8(gpu, k3, inn, out):
+    """k3_matmul_q8 (the draft model's int8 rows, k3_mmw's K3_WI8 branch; reference
+    k3_ops.c:1221-1289, no exactness contract there): within 1e-4 ||ref||inf of the fp64
+    closed form, which the compiled reference matches to 1e-5 (tests/test_oracle.py), and
+    of the compiled reference itself where it is built."""
+    from oracle import Ref, q8_exact, q8_rows
+    say(f"case: k3_matmul_q8 {out}x{inn}")
+    rng = np.random.default_rng(inn + out)
+    W, sc, q = q8_rows(rng, inn, out)
+    x = rng.standard_normal(inn).astype(np.float32)
+    got = k3.matmul_q8(x, W, inn, out)
+    assert max_err_rel_inf(got, q8_exact(x, sc, q)) <= TOL
+    if Ref.available():
+        assert max_err_rel_inf(got, Ref().matmul_q8(x, W, inn, out)) <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_trunk_o_projection(gpu, orc, T):
+    """The KDA/MLA o-projection shape (12288 -> 7168, bf16) through k3_matmul_bf16 and the
+    device entry, against the oracle."""
+    say(f"case: bf16 gemv 7168x12288 (o-projection), T={T}")
+    W = orc.fill_bf16(12288 * 7168, 4321).reshape(7168, 12288)
+    X = np.stack([orc.fill_f(12288, 50 + t) for t in range(T)])
+    want = np.stack([orc.matmul_bf16(X[t], W) for t in range(T)])
+    got = dev_matmul(gpu, X, W)
+    for t in range(T):
+        assert max_err_rel_inf(got[t], want[t]) <= TOL, t
+    assert max_err_rel_inf(gpu.matmul_bf16(X[0], W), want[0]) <= TOL

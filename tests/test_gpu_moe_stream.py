@@ -189,6 +189,30 @@ def test_k3_moe_hbm_bank_eviction(gpu, orc, wl, k3layer):
         bank.destroy()
 
 
+@pytest.mark.parametrize("slots,T,prefill", [(20, 3, 0), (20, 3, 1), (20, 65, 1), (10, 2, 0), (10, 2, 1)])
+def test_k3_moe_hbm_bank_overflow(gpu, orc, wl, k3layer, slots, T, prefill):
+    """One call naming more distinct experts than the bank has slots: several tokens at
+    top-16 over 20 slots (between tokens, or inside a 64-token chunk), and 10 slots, fewer
+    than one token's 16 experts. The call computes what it has fetched, releases its slots
+    and goes on: no drops, no failed admissions, the oracle's result."""
+    say(f"case: k3_moe HBM bank of {slots} slots, T={T} prefill={prefill}")
+    cfg, W, experts = k3layer
+    up = PySource(experts)
+    bank = gpu.HbmBank(1, N_EXPERTS, 3584, 3072, slots, 1, up.ptr)
+    try:
+        x = wl.tokens(T, 7168, tag=f"gpuq.overflow.{T}")
+        idx = np.stack([orc.router(x[t], W["gate"], W["bias"], TOPK)[0] for t in range(T)])
+        assert len(set(idx.ravel().tolist())) > slots
+        got = gpu.moe(x, cfg, W, 1, bank.src, prefill)
+        want = oracle_moe_q(orc, x, cfg, W, 1, PySource(experts), prefill)
+        assert want[3] == 0
+        compare(got + ([],), want + ([],), check_calls=False)
+        st = bank.stats()
+        assert st["failures"] == 0 and st["resident"] <= slots
+    finally:
+        bank.destroy()
+
+
 def test_k3_moe_threads(gpu, orc, wl, k3layer):
     """Two host threads calling the library at once (the reference's kernels are
     re-entrant): each result equals the one computed alone."""

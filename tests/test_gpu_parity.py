@@ -196,6 +196,39 @@ def test_expert_ffn_decode(gpu, wl, gold, act):
     assert max_err_rel_inf(out, gold["expert_silu" if act == 1 else "expert_situ"]) <= TOL
 
 
+@pytest.mark.parametrize("act", [1, 0])
+def test_expert_ffn_decode_tiled_timed_path(gpu, wl, gold, act):
+    """The call the benchmark times for one expert's FFN: k3d_moe_experts with one
+    assignment (combine weight 0.125) on a tiled 7168 -> 2048 bank (gate and up in
+    workgroups of their own, then down + combine in one kernel), against the compiled
+    reference's golden, with the expert placed at entry 3 of a 6-entry table."""
+    import ctypes as C
+    say(f"case: expert ffn, tiled timed path, act={act}")
+    L = gpu.lib()
+    E, I, N = wl.HIDDEN, wl.INTER, 6
+    bank = gpu.DevBank([None, None, None, wl.expert(0), None, None], E, I, gpu.K3D_LAYOUT_TILED)
+    x = gpu.DevBuf(E * 4).upload(wl.expert_input())
+    out = gpu.DevBuf(E * 4)
+    idx = gpu.DevBuf(4).upload(np.array([3], np.int32))
+    wt = gpu.DevBuf(4).upload(np.array([0.125], np.float32))
+    drops = gpu.DevBuf(4)
+    ws = gpu.DevBuf(L.k3d_moe_ws(1, E, I, N, 1, 0))
+    try:
+        out.upload(np.full(E, np.nan, np.float32))
+        gpu.check(L.k3d_moe_experts(out.ptr, idx.ptr, wt.ptr, x.ptr, 1, bank.table.ptr,
+                                    gpu.K3D_LAYOUT_TILED, E, I, N, 1, act, 4.0, 25.0, 0, ws.ptr,
+                                    ws.nbytes, None, None, drops.ptr, None), "k3d_moe_experts")
+        gpu.check(L.k3d_sync(None))
+        got = out.download(np.empty(E, np.float32))
+        nd = int(drops.download(np.empty(1, np.int32))[0])
+    finally:
+        for b in (x, out, idx, wt, drops, ws):
+            b.free()
+        bank.free()
+    assert nd == 0
+    assert max_err_rel_inf(got, gold["expert_silu" if act == 1 else "expert_situ"]) <= TOL
+
+
 def test_moe_routed_8_tokens_golden(gpu, wl, gold):
     say("case: moe routed T=8 vs golden")
     W = wl.router_weights()

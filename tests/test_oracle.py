@@ -274,3 +274,65 @@ def test_oracle_matches_compiled_reference_random(orc, ref):
     assert np.array_equal(i1, i2) and np.array_equal(bits(w1), bits(w2))
     Wb = (rng.integers(0, 65536, (31, 257)).astype(np.uint16) & 0x7F7F)
     assert np.array_equal(bits(orc.matmul_bf16(x[:257], Wb)), bits(ref.matmul_bf16(x[:257], Wb)))
+
+
+def test_nan_scale_group_skips_nonfinite_activations(orc, ref):
+    """A group whose E8M0 byte is 255 is skipped whole (k3_ops.c:1478, 1536): an Inf or NaN
+    activation inside it leaves the row finite, while one inside a group of a finite scale
+    makes the row non-finite (0 * Inf = NaN, 1.5 * Inf = Inf). Oracle and compiled reference
+    agree bit for bit; the rows that skip every non-finite activation equal the same GEMV
+    with those activations set to zero."""
+    rng = np.random.default_rng(255)
+    rows, inn = 6, 128
+    pk = rng.integers(0, 256, rows * inn // 2, dtype=np.uint8)
+    sc = rng.integers(120, 128, rows * inn // 32, dtype=np.uint8).reshape(rows, inn // 32)
+    x = rng.standard_normal(inn).astype(np.float32)
+    x[40], x[45] = np.inf, np.nan                    # both in group 1 (columns 32..63)
+    sc[[0, 2, 5], 1] = 255                           # rows 0, 2, 5 skip group 1
+    y = orc.matmul_mxfp4(x, pk, sc.ravel(), inn, rows)
+    assert np.array_equal(bits(y), bits(ref.matmul_mxfp4(x, pk, sc.ravel(), inn, rows)))
+    assert np.isfinite(y[[0, 2, 5]]).all() and not np.isfinite(y[[1, 3, 4]]).any()
+    x0 = x.copy()
+    x0[[40, 45]] = 0.0
+    y0 = orc.matmul_mxfp4(x0, pk, sc.ravel(), inn, rows)
+    assert np.array_equal(bits(y[[0, 2, 5]]), bits(y0[[0, 2, 5]]))
+
+
+def test_q8_closed_form_matches_compiled_reference(ref):
+    """k3_matmul_q8 (k3_ops.c:1221-1289) has no exactness contract (fp32 accumulation in the
+    AVX2 reduction order): the compiled reference is within 1e-5 ||y||inf of the fp64 closed
+    form (sum of int8 * x, then the row's scale), which the GPU test compares against; a
+    row scale taken from the wrong end of the row would miss it by far."""
+    from oracle import q8_exact, q8_rows
+    rng = np.random.default_rng(8)
+    for inn, out in ((7168, 96), (300, 17), (16, 3)):
+        W, sc, q = q8_rows(rng, inn, out)
+        x = rng.standard_normal(inn).astype(np.float32)
+        want = q8_exact(x, sc, q)
+        got = ref.matmul_q8(x, W, inn, out)
+        assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+        wrong = q8_exact(x, W[:, -4:].copy().view(np.float32).ravel(), q)
+        assert np.abs(wrong - want).max() > 1e-2 * np.abs(want).max()
+
+
+def test_expert_major_oracle_equals_per_token(orc, wl):
+    """orc_expert_ffn_many (each expert dequantized once, all its tokens, the full-batch
+    GPU tests' reference) equals orc_expert_ffn token by token bit for bit, and
+    moe_outputs (expert-major, combine in slot order) equals orc_moe_routed's token-major
+    loop on the same routing, bit for bit: the expert-major form only reorders the
+    reference's operations."""
+    rng = np.random.default_rng(5)
+    for E, I, T in ((7168, 2048, 3), (1024, 512, 19)):
+        ex = wl.expert(7, E, I)
+        X = rng.standard_normal((T, E)).astype(np.float32)
+        many = orc.expert_ffn_many(X, ex, E, I, act=1)
+        one = np.stack([orc.expert_ffn(X[t], ex, E, I, act=1) for t in range(T)])
+        assert np.array_equal(bits(many), bits(one))
+        sit = orc.expert_ffn_many(X, ex, E, I, act=0)
+        assert np.array_equal(bits(sit[0]), bits(orc.expert_ffn(X[0], ex, E, I, act=0)))
+    E, I, N, K, T = 512, 256, 12, 3, 23
+    bank = [wl.expert(e, E, I) for e in range(N)]
+    W = (rng.standard_normal((N, E)) * 0.05).astype(np.float32)
+    X = rng.standard_normal((T, E)).astype(np.float32)
+    out, idx, wt = orc.moe_routed(X, W, None, bank, E, I, K)
+    assert np.array_equal(bits(orc.moe_outputs(X, idx, wt, bank, E, I)), bits(out))

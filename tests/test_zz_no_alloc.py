@@ -3,7 +3,9 @@
 array) against k3d_moe_routed with a caller workspace, through the C ABI: two calls in a
 row on the same layer, the second on a smaller batch, then a one-token call (the decode
 path whose gate/up kernel selects the experts), each bit for bit equal to the workspace
-form; a batch whose scratch exceeds the static array is refused with an error."""
+form; a batch whose scratch exceeds the static array is refused with an error. At Kimi K3's
+expert shape (3584 -> 3072 -> 3584, 896 experts, top-16) a 64-token decode batch fits the
+array and gives the workspace form's bits."""
 import sys
 
 import numpy as np
@@ -26,8 +28,9 @@ def bank(gpu, wl):
     b.free()
 
 
-def run(gpu, bank, X, W, static, want_perm):
+def run(gpu, bank, X, W, static, want_perm, shape=(E, I, N, K)):
     L = gpu.lib()
+    E, I, N, K = shape
     T = X.shape[0]
     bufs = {"x": gpu.DevBuf(X.nbytes).upload(X), "w": gpu.DevBuf(W.nbytes).upload(W),
             "out": gpu.DevBuf(T * E * 4), "idx": gpu.DevBuf(T * K * 4), "wt": gpu.DevBuf(T * K * 4),
@@ -101,3 +104,23 @@ def test_static_refuses_oversized_batch(gpu, wl, bank):
     finally:
         for b in bufs:
             b.free()
+
+
+def test_static_at_k3_shape(gpu, k3, wl):
+    L = gpu.lib()
+    shape = (3584, 3072, 896, 16)
+    E3, I3, N3, K3 = shape
+    assert L.k3d_moe_ws(64, E3, I3, N3, K3, 0) <= L.k3d_static_ws_bytes()
+    say("setup: 896-entry tiled bank at 3584 x 3072, 64 experts present")
+    experts = [k3.gen_expert(E3, I3, 61, e) if e < 64 else None for e in range(N3)]
+    bank = gpu.DevBank(experts, E3, I3, gpu.K3D_LAYOUT_TILED)
+    try:
+        W = wl.router_weights(N3, E3, tag="noalloc.k3.router")
+        for T in (64, 1):
+            say(f"case: static vs workspace at the K3 shape, T={T}")
+            X = wl.tokens(T, E3, tag=f"noalloc.k3.x.{T}")
+            got = run(gpu, bank, X, W, True, T > 1, shape)
+            want = run(gpu, bank, X, W, False, T > 1, shape)
+            same(got, want)
+    finally:
+        bank.free()
