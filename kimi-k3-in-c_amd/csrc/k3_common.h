@@ -215,16 +215,21 @@ __device__ __forceinline__ float k3_act_pair_fast(float g, float u, int act, flo
     return (b1 * tg * sg) * (b2 * tu);
 }
 
-/* The end of a stamped workgroup (K3kMxArgs.stamps): its start t0 and end on the 100 MHz
- * clock and the hardware id (XCC_ID << 32 | HW_ID: CU in bits 8-11, shader array 12, shader
- * engine 13-15), three u64 at its workgroup's slot. */
-__device__ __forceinline__ void k3_stamp_end(unsigned long long *stamps, unsigned long long t0)
+/* Per-workgroup stamps (K3kMxArgs.stamps): three u64 at the workgroup's slot, its start
+ * and end on the 100 MHz clock and the hardware id (XCC_ID << 32 | HW_ID: CU in bits 8-11,
+ * shader array 12, shader engine 13-15). The start is stored when it is taken, so that no
+ * register holds it through the kernel. */
+__device__ __forceinline__ void k3_stamp_begin(unsigned long long *stamps)
+{
+    stamps[3 * (size_t)blockIdx.x] = __builtin_amdgcn_s_memrealtime();
+}
+
+__device__ __forceinline__ void k3_stamp_end(unsigned long long *stamps)
 {
     unsigned long long *p = stamps + 3 * (size_t)blockIdx.x;
     const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
     const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);     /* HW_REG_HW_ID */
     const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);   /* HW_REG_XCC_ID */
-    p[0] = t0;
     p[1] = t1;
     p[2] = ((unsigned long long)xcc << 32) | hw;
 }

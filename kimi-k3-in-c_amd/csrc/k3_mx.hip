@@ -1147,7 +1147,12 @@ void mx_moe_kernel(K3kMxArgs a)
     const int n_items = (*a.n_passes) * n_rb;
     /* requires K % 512 == 0: the host routes other K to mx_gemm_kernel */
 
-    const unsigned long long t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0ull;
+    /* the stamps pointer waits in LDS: held in registers through the loop it would spill */
+    __shared__ unsigned long long *stamp_sh;
+    if (tid == 0) {
+        stamp_sh = a.stamps;
+        if (a.stamps) k3_stamp_begin(a.stamps);
+    }
     for (int i = tid; i < 2 * NS * LDT / 8; i += 64 * NW) {
         const int bh = i / (LDT / 8), o = i % (LDT / 8);
         *reinterpret_cast<uint4 *>(&bsh[bh / NS][bh % NS][PT][o * 8]) = make_uint4(0, 0, 0, 0);
@@ -1394,7 +1399,10 @@ void mx_moe_kernel(K3kMxArgs a)
             }
         }
     }
-    if (a.stamps && tid == 0) k3_stamp_end(a.stamps, t_start);
+    if (tid == 0) {
+        unsigned long long *sp = stamp_sh;
+        if (sp) k3_stamp_end(sp);
+    }
 }
 
 template <int MODE, int MT, int NS, int PT, int NW, int WPE, int LAYOUT, int DEPTH = 1, int NB = 1>
@@ -1498,7 +1506,12 @@ void mx_prefill_kernel(K3kMxArgs a)
      * offset select would cost it registers it does not have. The wave-uniform part of
      * each address stays clamped inside the buffer. */
     constexpr uint32_t OOB = 0x80000000u;
-    const unsigned long long t_start = a.stamps ? __builtin_amdgcn_s_memrealtime() : 0ull;
+    /* the stamps pointer waits in LDS: held in registers through the loop it would spill */
+    __shared__ unsigned long long *stamp_sh;
+    if (tid == 0) {
+        stamp_sh = a.stamps;
+        if (a.stamps) k3_stamp_begin(a.stamps);
+    }
 
     for (int item = li; item < n_items; item += nlw) {
         const int rb = item % n_rb, pass = pbeg + item / n_rb;
@@ -1723,7 +1736,10 @@ void mx_prefill_kernel(K3kMxArgs a)
             }
         }
     }
-    if (a.stamps && tid == 0) k3_stamp_end(a.stamps, t_start);
+    if (tid == 0) {
+        unsigned long long *sp = stamp_sh;
+        if (sp) k3_stamp_end(sp);
+    }
 }
 
 template <int MODE, int MT, int NB, int SPC, int NW>
@@ -2005,14 +2021,25 @@ extern "C" int k3k_mx_decode(int mode, const K3kMxArgs *a, void *stream)
 #define K3_DC_LDS_MAX (160 * 1024 - 4096)
 
 /* The fused kernel is used where it is faster than mx_decode_kernel DOWN + the combine
- * kernel (measured: one or two assignments, 7168 x 2048 -- 18.3 against 20.3 us for one
- * expert's FFN; at eight it is slower, 24 against 19 us) and the slots' activation terms
- * of one token fit in its LDS. */
+ * kernel and the slots' activation terms of one token fit in its LDS: one or two
+ * assignments (7168 x 2048: 18.3 against 20.3 us for one expert's FFN), and one token of
+ * up to eight slots with one K share per slot (eight waves), so that two workgroups fit a
+ * CU and every tile's workgroup is resident at once. */
+static int dc_shares(int topk, int K)
+{
+    const int nchunk = K / 512;
+    int ks = (topk <= 2 ? 16 : 8) / topk;
+    if (ks < 1) ks = 1;
+    return ks > nchunk ? nchunk : ks;
+}
+
 extern "C" int k3k_mx_decode_combine_ok(int n_assign, int topk, int nsplit, int K, int rows)
 {
     const long ntile = (rows + 15) / 16;
     const bool wide = (long)n_assign * ((ntile + 3) / 4) >= 256 || K / 512 < 4;
-    return !wide && topk >= 1 && topk <= 16 && (size_t)topk * nsplit * K * 2 + 1024 <= K3_DC_LDS_MAX;
+    const bool one_token = n_assign == topk && topk <= 8 && K / 512 >= 1;
+    return (!wide || one_token) && topk >= 1 && topk <= 16 &&
+           (size_t)topk * nsplit * K * 2 + 1024 <= K3_DC_LDS_MAX;
 }
 
 extern "C" int k3k_mx_decode_split_ok(int n_assign, int topk, int nsplit, int K, int rows, int K_down,
@@ -2030,10 +2057,8 @@ extern "C" int k3k_mx_decode_combine(const K3kMxArgs *a, void *stream)
         a->n_assign % a->topk || !a->wt ||
         (size_t)k3_tile_prows(a->rows) * (a->K / 2) >= 0x80000000u)
         return k3k_fail("mx_decode_combine: shape", hipErrorInvalidValue);
-    /* waves: topk slots x K shares, at most 16 */
-    const int nchunk = a->K / 512;
-    int ks = 16 / a->topk;
-    if (ks > nchunk) ks = nchunk;
+    /* waves: topk slots x K shares, at most 16 (at most 8 from three slots) */
+    const int ks = dc_shares(a->topk, a->K);
     const int T = a->n_assign / a->topk, ntile = (a->rows + 15) / 16;
     if ((size_t)a->topk * a->nsplit * a->K * 2 + 1024 > K3_DC_LDS_MAX)
         return k3k_fail("mx_decode_combine: LDS", hipErrorInvalidValue);
