@@ -152,7 +152,9 @@ void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
 
 /* Sigmoid router, one token: selection on score+bias, weights from the unbiased scores,
  * renormalised and scaled; idx/w in descending selection order. Replaces k3_router,
- * reference include/k3/k3.h:241-243. */
+ * reference include/k3/k3.h:241-243. n_experts is limited to 2048 (the reference takes any
+ * count; Kimi K3 has 896): the selection keeps every expert's scored record in one
+ * workgroup's LDS. A larger count aborts with a FATAL message. */
 void k3_router(int *idx, float *w, const float *x, const float *W, const float *bias,
                int hidden, int n_experts, int topk, int renorm, float routed_scale);
 

@@ -91,7 +91,9 @@ int k3d_matmul_f32(float *y, const float *x, int ntok, const float *W, int in, i
 int k3d_matmul_bf16(float *y, const float *x, int ntok, const uint16_t *W, int in, int out,
                     void *stream);
 
-/* Router over T tokens: idx/wt [T][topk] (reference k3_ops.c:419-478, per token). */
+/* Router over T tokens: idx/wt [T][topk] (reference k3_ops.c:419-478, per token).
+ * n_experts 1..2048 (the selection holds every expert's record in one workgroup's LDS);
+ * more returns an error. */
 size_t k3d_router_ws(int T, int hidden, int n_experts);
 int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const float *bias,
                int hidden, int n_experts, int topk, int renorm, float routed_scale, void *ws,

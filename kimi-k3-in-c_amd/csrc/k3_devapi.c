@@ -265,7 +265,8 @@ static int router_run(int *idx, float *wt, const float *x, int T, const float *W
         g.ctr = w->ctr;
     }
     if (k3k_router_partial(w->part, w->rbound, x, T, W, hidden, n_experts, w->chunk,
-                           gather ? w->ctr : NULL, exc, stream))
+                           gather ? w->ctr : NULL, gather ? idx : NULL, gather ? T * topk : 0, exc,
+                           stream))
         return fail("router_partial");
     if (k3k_router_final(idx, wt, w->nrecomp, w->part, w->rbound, w->chunk, x, W, bias, T, hidden,
                          n_experts, topk, renorm, routed_scale, exc, gather ? &g : NULL, stream))
@@ -621,7 +622,7 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
         rc = exc_table(&exc);
         if (rc) return rc;
         if (k3k_router_partial(r.part, r.rbound, x, T, router_w, hidden, n_experts, r.chunk, NULL,
-                               exc, stream))
+                               NULL, 0, exc, stream))
             return fail("router_partial");
         k3k_prof_mark(stream, K3D_STAGE_ROUTER);
         const RouterSel sel = {r.part, router_w, bias, renorm, routed_scale, exc, r.nrecomp, idx, wt};

@@ -94,7 +94,7 @@ static void check(int rc, const char *what)
 
 /* Reusable device buffers, one per role, grown on demand. */
 enum { B_X, B_Y, B_P, B_S, B_WS, B_BIAS, B_RW, B_IDX, B_WT, B_ARENA, B_BANK, B_Z, B_ACC,
-       B_SGU, B_SDN, B_OUT, B_W2, B_W3, B_T0, B_T1, B_T2, B_XS, B_COUNT };
+       B_SGU, B_SDN, B_OUT, B_W2, B_W3, B_T0, B_T1, B_T2, B_XS, B_SACT, B_SSDN, B_SXS, B_COUNT };
 static void *g_buf[B_COUNT];
 static size_t g_cap[B_COUNT];
 
@@ -103,7 +103,8 @@ static void *buf(int slot, size_t bytes)
     if (bytes == 0) bytes = 4;
     if (g_cap[slot] < bytes) {
         if (g_buf[slot]) {
-            check(k3k_sync(g_stream), "synchronize before buffer growth");
+            /* every stream: the library stream's side stream may still read it */
+            check(k3k_sync(NULL), "synchronize before buffer growth");
             k3k_free(g_buf[slot]);
         }
         size_t cap = bytes + bytes / 4;
@@ -125,6 +126,24 @@ static void download(void *h, const void *d, size_t bytes)
 {
     check(k3k_d2h(h, d, bytes, g_stream), "device to host copy");
     check(k3k_sync(g_stream), "synchronize");
+}
+
+/* Pinned staging for copies the host waits for by event, grown on demand. */
+static void *g_pin = NULL;
+static size_t g_pin_cap = 0;
+static void *g_pin_ev = NULL;
+
+static void *pinned(size_t bytes)
+{
+    if (g_pin_cap < bytes) {
+        check(k3k_sync(NULL), "synchronize before staging growth");
+        k3k_host_free(g_pin);
+        g_pin_cap = bytes + bytes / 4;
+        g_pin = k3k_host_alloc(g_pin_cap);
+        if (!g_pin) fatal("pinned host allocation");
+    }
+    if (!g_pin_ev && !(g_pin_ev = k3k_event_create())) fatal("event creation");
+    return g_pin;
 }
 
 /* ---------------------------------------------------------------- registry ---- */
@@ -570,21 +589,27 @@ static size_t wbytes(int wdt, int in, int out)
 /* y[t*ldy + o] = W x[t] for a tagged weight matrix (k3_mmw, reference k3.h:289-295). Up to
  * four tokens stream the weights through the vector-unit GEMV; more bf16 tokens go to the
  * matrix-core GEMM with the activations split into two bf16 terms (fp32-accurate). */
-static void mmw_dev(float *y_d, const float *x_d, int ntok, const void *W, int wdt, int in, int out,
-                    int ldy, int slot)
+static void mmw_on(float *y_d, const float *x_d, int ntok, const void *W, int wdt, int in, int out,
+                   int ldy, int slot, int xs_slot, void *stream)
 {
     const void *dw = weights(slot, W, wbytes(wdt, in, out));
     int rc;
     if (wdt == K3_WBF16 && ntok > 4 && in % 64 == 0 &&
         (unsigned long long)out * in * 2 < 0x80000000ull && (unsigned long long)ntok * in * 2 < 0x80000000ull) {
-        uint16_t *xs = (uint16_t *)buf(B_XS, (size_t)ntok * in * 4);
+        uint16_t *xs = (uint16_t *)buf(xs_slot, (size_t)ntok * in * 4);
         uint16_t *xl = xs + (size_t)ntok * in;
-        check(k3k_split_bf16(xs, xl, x_d, (size_t)ntok * in, g_stream), "activation split");
-        rc = k3k_dense_gemm(y_d, ldy, 0, (const uint16_t *)dw, xs, xl, out, ntok, in, NULL, 0, g_stream);
-    } else if (wdt == K3_WBF16) rc = k3k_gemv_bf16(y_d, x_d, (const uint16_t *)dw, in, out, ntok, ldy, g_stream);
-    else if (wdt == K3_WI8) rc = k3k_gemv_q8(y_d, x_d, dw, in, out, ntok, ldy, g_stream);
-    else rc = k3k_gemv_f32(y_d, x_d, (const float *)dw, in, out, ntok, ldy, g_stream);
+        check(k3k_split_bf16(xs, xl, x_d, (size_t)ntok * in, stream), "activation split");
+        rc = k3k_dense_gemm(y_d, ldy, 0, (const uint16_t *)dw, xs, xl, out, ntok, in, NULL, 0, stream);
+    } else if (wdt == K3_WBF16) rc = k3k_gemv_bf16(y_d, x_d, (const uint16_t *)dw, in, out, ntok, ldy, stream);
+    else if (wdt == K3_WI8) rc = k3k_gemv_q8(y_d, x_d, dw, in, out, ntok, ldy, stream);
+    else rc = k3k_gemv_f32(y_d, x_d, (const float *)dw, in, out, ntok, ldy, stream);
     check(rc, "k3_mmw");
+}
+
+static void mmw_dev(float *y_d, const float *x_d, int ntok, const void *W, int wdt, int in, int out,
+                    int ldy, int slot)
+{
+    mmw_on(y_d, x_d, ntok, W, wdt, in, out, ldy, slot, B_XS, g_stream);
 }
 
 /* ---------------------------------------------------- streamed-expert fetching ---- */
@@ -790,12 +815,40 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
                          buf(B_WS, wsb), wsb, g_stream),
               "k3_moe router");
     }
-    check(k3k_d2h(hidx, di, TK * 4, g_stream), "device to host copy");
-    download(hwt, dwt, TK * 4);
-
+    /* the routing comes back through pinned memory; the host waits for it alone, while the
+     * device goes on with the down-projection */
+    {
+        char *pin = (char *)pinned(TK * 8);
+        check(k3k_d2h(pin, di, TK * 4, g_stream), "device to host copy");
+        check(k3k_d2h(pin + TK * 4, dwt, TK * 4, g_stream), "device to host copy");
+        check(k3k_event_record(g_pin_ev, g_stream), "event");
+    }
     /* 2. down-project into the latent space */
     float *dz = (float *)buf(B_Z, (size_t)T * L * 4);
     mmw_dev(dz, dx, T, w->down, w->wdt, E, L, L, B_P);
+    /* 6. (ahead) the shared expert depends on x alone: with its weights resident it runs on
+     * the library stream's side stream, forked after the routing and the down-projection
+     * (the critical path), beside the routed experts, and joined before its sum is added */
+    const size_t wsh = wbytes(w->wdt, E, SI);
+    const int shared = SI > 0 && w->sh1 && w->sh3 && w->sh2;
+    const int shared_side = shared && k3_dev_lookup(w->sh1) && k3_dev_lookup(w->sh3) &&
+                            k3_dev_lookup(w->sh2) && wsh > 0;
+    float *sdn = NULL;
+    if (shared_side) {
+        void *side = NULL;
+        check(k3k_fork(g_stream, &side), "fork");
+        float *sgu = (float *)buf(B_SGU, (size_t)T * 2 * SI * 4);
+        float *sact = (float *)buf(B_SACT, (size_t)T * SI * 4);
+        sdn = (float *)buf(B_SSDN, (size_t)T * E * 4);
+        mmw_on(sgu, dx, T, w->sh1, w->wdt, E, SI, 2 * SI, B_P, B_SXS, side);
+        mmw_on(sgu + SI, dx, T, w->sh3, w->wdt, E, SI, 2 * SI, B_P, B_SXS, side);
+        check(k3k_act(sact, sgu, SI, T, K3_ACT_SITU, c->situ_b1, c->situ_b2, side), "shared act");
+        mmw_on(sdn, sact, T, w->sh2, w->wdt, SI, E, E, B_P, B_SXS, side);
+    }
+
+    check(k3k_event_sync(g_pin_ev), "routing copy");
+    memcpy(hidx, g_pin, TK * 4);
+    memcpy(hwt, (char *)g_pin + TK * 4, TK * 4);
 
     /* 3. routed experts, weighted sum in slot order */
     float *dacc = (float *)buf(B_ACC, (size_t)T * L * 4);
@@ -903,10 +956,13 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
     mmw_dev(dout, dacc, T, w->up, w->wdt, L, E, E, B_P);
 
     /* 6. shared expert on the original input, added unweighted */
-    if (SI > 0 && w->sh1 && w->sh3 && w->sh2) {
+    if (shared_side) {
+        check(k3k_join(g_stream), "join");
+        check(k3k_axpy_rows(dout, sdn, (size_t)T * E, g_stream), "shared add");
+    } else if (shared) {
         float *sgu = (float *)buf(B_SGU, (size_t)T * 2 * SI * 4);
-        float *sact = (float *)buf(B_Z, (size_t)T * SI * 4);
-        float *sdn = (float *)buf(B_SDN, (size_t)T * E * 4);
+        float *sact = (float *)buf(B_SACT, (size_t)T * SI * 4);
+        sdn = (float *)buf(B_SSDN, (size_t)T * E * 4);
         mmw_dev(sgu, dx, T, w->sh1, w->wdt, E, SI, 2 * SI, B_P);
         mmw_dev(sgu + SI, dx, T, w->sh3, w->wdt, E, SI, 2 * SI, B_P);
         check(k3k_act(sact, sgu, SI, T, K3_ACT_SITU, c->situ_b1, c->situ_b2, g_stream), "shared act");

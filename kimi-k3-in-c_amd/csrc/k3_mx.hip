@@ -659,11 +659,16 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
     }
     int eix;
     if constexpr (SEL) {
-        /* the token's experts: the router's selection from router_small's scored records,
-         * the same in every workgroup of the token; its first workgroup writes idx / wt */
+        /* the token's experts: the router's selection from router_small's scored records.
+         * The workgroups of slot j need only the j + 1 largest keys (the selection's first
+         * j + 1 picks do not depend on the later ones; an uncertified logit is recomputed
+         * when it could reach those), so slot 0 starts its weight stream after one
+         * extraction per level instead of topk; the first workgroup of the token's last
+         * slot selects all topk and writes idx / wt */
         __shared__ SelSmem<8> ssm;
         __shared__ int sel_id[64];
         const int t = asg / a.topk, j = asg % a.topk;
+        const bool writer = j == a.topk - 1 && tg == 0;
         ExcTable exc;
         exc.pairs = a.exc.pairs;
         exc.index = a.exc.index;
@@ -681,19 +686,19 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
         __syncthreads();
         int nre;
         const uint64_t mysel = select_rounds<8>(ssm, a.xf32 + (size_t)t * K, a.rw, a.rbias, K, a.n_experts,
-                                                a.topk, exc, nre);
+                                                j + 1, exc, nre);
         if (wv == 0) {
             int id;
             float w;
-            select_weight<8>(ssm, mysel, a.topk, a.renorm, a.rscale, id, w);
-            if (lane < a.topk) {
+            select_weight<8>(ssm, mysel, j + 1, a.renorm, a.rscale, id, w);   /* w: writer only */
+            if (lane <= j) {
                 sel_id[lane] = id >= 0 ? id : 0;            /* none left: expert 0, weight 0 */
-                if (j == 0 && tg == 0) {
+                if (writer) {
                     a.idx_out[(size_t)t * a.topk + lane] = id >= 0 ? id : 0;
                     a.wt_out[(size_t)t * a.topk + lane] = w;
                 }
             }
-            if (j == 0 && tg == 0 && lane == 0 && a.nrecomp) a.nrecomp[t] = nre;
+            if (writer && lane == 0 && a.nrecomp) a.nrecomp[t] = nre;
         }
         __syncthreads();
         eix = sel_id[j];

@@ -125,10 +125,15 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
                                                                   const float *x, int T,
                                                                   const float *W, int hidden,
                                                                   int n_experts, int chunk, int vec,
-                                                                  int deal, int *ctr)
+                                                                  int deal, int *ctr, int *idx_reset,
+                                                                  int n_reset)
 {
-    /* the final kernel's arrival counter starts every launch at zero */
-    if (ctr && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) *ctr = 0;
+    /* the final kernel's arrival counter starts every launch at zero, and the idx it gathers
+     * at -1 (its gathering workgroup waits for each entry to be set) */
+    if (ctr && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
+        if (threadIdx.x == 0) *ctr = 0;
+        for (int i = threadIdx.x; i < n_reset; i += blockDim.x) idx_reset[i] = -1;
+    }
     typedef double d4 __attribute__((ext_vector_type(4)));
     constexpr int TB = 32 * MT, EB = 32 * ME;           /* workgroup tile: tokens, experts */
     constexpr int NWP = EB / 32, NXP = TB / 32;         /* float4 pieces per thread: W, x */
@@ -759,21 +764,23 @@ __global__ __launch_bounds__(KB > 32 ? 512 : 1024) void router_final_kernel(int 
         if (nrecomp && lane == 0) nrecomp[t] = nre;
     }
     if constexpr (GATHER) {
-        /* The workgroup that finishes last runs the gather over every token's idx: each
-         * workgroup's idx stores are acknowledged (vmcnt 0) before it counts itself in with
-         * an agent-scope release, and the last one acquires at agent scope (the count is
-         * acq_rel) before it reads idx with agent-scope loads, so every idx store
-         * happens-before the gather's loads. It leaves the counter at zero (the partial
-         * kernel zeroes it before every launch as well). */
+        /* The workgroup that finishes last runs the gather over every token's idx. Each
+         * workgroup's idx stores (agent-scope atomics, written through to where every XCD
+         * reads) are acknowledged (vmcnt 0) before it counts itself in on an agent-scope
+         * counter. The partial kernel, a launch earlier on the stream, set every idx to -1
+         * and the counter to zero, so those stores happen-before this launch: an agent-scope
+         * load of an idx returns -1 or this launch's value, and the gather reads each until
+         * it is set (in practice at once: the stores were acknowledged before the count). No
+         * release fence (an L2 write-back) is needed. The last workgroup leaves the counter
+         * at zero. */
         __shared__ int s_last;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0)
-            s_last = __hip_atomic_fetch_add(g.ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+            s_last = __hip_atomic_fetch_add(g.ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                      (int)gridDim.x - 1;
         __syncthreads();
         if (s_last) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             gather_block<true>(g);
             if (tid == 0) __hip_atomic_store(g.ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -893,15 +900,23 @@ __device__ void gather_plan(const int *cnt, int *fill, int (*wtot5)[5], int *off
 }
 
 /* The one-workgroup gather (1024 threads); COH: idx was written during this launch by other
- * workgroups (agent-scope stores), so it is read with agent-scope loads. */
+ * workgroups (agent-scope stores) over the -1 the previous launch left, so it is read with
+ * agent-scope loads, each until it is set. */
 template <bool COH>
 __device__ void gather_block(const GatherDev &g)
 {
     int *offsets = g.offsets, *perm = g.perm;
     const int N = g.N, n_experts = g.n_experts;
     auto idx_at = [&](int a) {
-        return COH ? __hip_atomic_load(const_cast<int *>(g.idx) + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                   : g.idx[a];
+        if (!COH) return g.idx[a];
+        int v = __hip_atomic_load(const_cast<int *>(g.idx) + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        /* -1 until this launch's store is visible (bounded: a value never stored reads as no
+         * expert after about 2^20 polls) */
+        for (int spin = 0; v < 0 && spin < (1 << 20); spin++) {
+            __builtin_amdgcn_s_sleep(1);
+            v = __hip_atomic_load(const_cast<int *>(g.idx) + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return v;
     };
     __shared__ int cnt[G_MAXE];
     __shared__ int fill[G_MAXE];
@@ -1195,6 +1210,41 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *y, const float *x, 
     for (int i = threadIdx.x; i < n; i += 256) yr[i] = __fmul_rn(__fmul_rn(w[i], xr[i]), inv);
 }
 
+/* The same for rows of at most 256 EPT elements: each thread loads its EPT elements (and
+ * weights) once into registers, the fp64 squares are summed per thread, across the wave by
+ * butterfly and across the four waves in order, then the row is written from the registers.
+ * A short row is one load latency and one barrier instead of a loop and a barrier tree. */
+template <int EPT>
+__global__ __launch_bounds__(256) void rmsnorm_reg_kernel(float *y, const float *x, const float *w,
+                                                          int n, float eps)
+{
+    __shared__ double wsum[4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const float *xr = x + (size_t)blockIdx.x * n;
+    float *yr = y + (size_t)blockIdx.x * n;
+    float xv[EPT], wvv[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {
+        const int i = tid + 256 * k;
+        xv[k] = i < n ? xr[i] : 0.0f;
+        wvv[k] = i < n ? w[i] : 0.0f;
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < EPT; k++) ss = fma((double)xv[k], (double)xv[k], ss);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) wsum[wv] = ss;
+    __syncthreads();
+    const double tot = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {
+        const int i = tid + 256 * k;
+        if (i < n) yr[i] = __fmul_rn(__fmul_rn(wvv[k], xv[k]), inv);
+    }
+}
+
 __global__ void axpy_kernel(float *out, const float *add, size_t n)
 {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -1305,8 +1355,10 @@ static ExcTable exc_view(const K3kExc *exc)
 
 extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, int T,
                                   const float *W, int hidden, int n_experts, int chunk,
-                                  int *ctr, const K3kExc *exc, void *stream)
+                                  int *ctr, int *idx, int n_idx, const K3kExc *exc, void *stream)
 {
+    if (ctr && n_idx > 0 && !idx) return k3k_fail("router_partial: idx to reset", hipErrorInvalidValue);
+    if (!ctr) n_idx = 0;
     if (T <= 0 || n_experts <= 0) return 0;
     if (chunk <= 0 || chunk % RP_KS) return k3k_fail("router_partial: chunk", hipErrorInvalidValue);
     const int ks = (hidden + chunk - 1) / chunk;
@@ -1351,10 +1403,10 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
                          (size_t)T * hidden * 4 < 0x80000000u;
         if (buf)
             hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, true>), grid, dim3(256), 0, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec, deal, ctr);
+                               rbound, x, T, W, hidden, n_experts, chunk, vec, deal, ctr, idx, n_idx);
         else
             hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, false>), grid, dim3(256), 0, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec, deal, ctr);
+                               rbound, x, T, W, hidden, n_experts, chunk, vec, deal, ctr, idx, n_idx);
     }
     K3K_LAUNCH_CHECK("router_partial launch");
     return 0;
@@ -1419,27 +1471,29 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
                        routed_scale, e, gd)
         if (n_experts <= 512 && ks <= 16) K3_RFG(1, 8, 16);
         else if (n_experts <= 512) K3_RFG(1, 8, RF_KB);
-        else if (n_experts <= 1024) K3_RFG(1, 32, RF_KB);
+        else if (n_experts <= 1024) K3_RFG(1, 16, RF_KB);
         else K3_RFG(2, 32, RF_KB);
 #undef K3_RFG
         K3K_LAUNCH_CHECK("router_final launch");
         return 0;
     }
-    /* scored records (a few tokens): one wave loads them all; else the chunk partials, a lane
-     * per expert, all of a lane's partials in one load batch when they are at most 16 or 32,
-     * or 64 for up to 64 tokens and 512 experts (more registers, fewer waves per CU: only
-     * while the tokens do not fill the chip). Wave 0 selects over SW keys per lane: 8 up to
-     * 512 experts, else 32. */
+    /* scored records (a few tokens) or the chunk partials: a lane per expert (two past
+     * 1024), all of a lane's partials in one load batch when they are at most 16 or 32, or 64
+     * for up to 64 tokens and 512 experts (more registers, fewer waves per CU: only while the
+     * tokens do not fill the chip). The selection is two-level when the expert groups fit
+     * (select_rounds), else wave 0 selects over SW keys per lane: 8 up to 512 experts, 16 up
+     * to 1024, else 32 (each pick rescans the picking lane's SW keys). */
 #define K3_RF(SL, SW, KB, PRE, NT)                                                                  \
     hipLaunchKernelGGL((router_final_kernel<SL, SW, KB, PRE>), dim3(T), dim3(NT), 0, st, idx, wt, nrecomp, \
                        part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm,        \
                        routed_scale, e, gd)
-    if (pre && n_experts <= 512) K3_RF(8, 8, RF_KB, true, 64);
-    else if (pre) K3_RF(32, 32, RF_KB, true, 64);
+    if (pre && n_experts <= 512) K3_RF(1, 8, RF_KB, true, 64 * nw);
+    else if (pre && n_experts <= 1024) K3_RF(1, 16, RF_KB, true, 64 * nw);
+    else if (pre) K3_RF(2, 32, RF_KB, true, 64 * nw);
     else if (n_experts <= 512 && ks <= 16) K3_RF(1, 8, 16, false, 64 * nw);
     else if (n_experts <= 512 && ks > 32 && ks <= 64 && T <= 64) K3_RF(1, 8, 64, false, 64 * nw);
     else if (n_experts <= 512) K3_RF(1, 8, RF_KB, false, 64 * nw);
-    else if (n_experts <= 64 * RF_MAXW) K3_RF(1, 32, RF_KB, false, 64 * nw);
+    else if (n_experts <= 64 * RF_MAXW) K3_RF(1, 16, RF_KB, false, 64 * nw);
     else K3_RF(2, 32, RF_KB, false, 64 * nw);
 #undef K3_RF
     K3K_LAUNCH_CHECK("router_final launch");
@@ -1525,8 +1579,15 @@ extern "C" int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int 
                            void *stream)
 {
     if (rows <= 0) return 0;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, y, x, w, n,
-                       eps);
+    if (n <= 256 * 16)
+        hipLaunchKernelGGL(rmsnorm_reg_kernel<16>, dim3(rows), dim3(256), 0, (hipStream_t)stream, y, x, w,
+                           n, eps);
+    else if (n <= 256 * 32)
+        hipLaunchKernelGGL(rmsnorm_reg_kernel<32>, dim3(rows), dim3(256), 0, (hipStream_t)stream, y, x, w,
+                           n, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, y, x, w, n,
+                           eps);
     K3K_LAUNCH_CHECK("rmsnorm launch");
     return 0;
 }

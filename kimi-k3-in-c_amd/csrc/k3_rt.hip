@@ -120,6 +120,46 @@ extern "C" int k3k_zero(void *dst, size_t bytes, void *stream)
     return 0;
 }
 
+/* Pinned host memory (copies from and to it run asynchronously) and events. */
+extern "C" void *k3k_host_alloc(size_t bytes)
+{
+    void *p = nullptr;
+    hipError_t e = hipHostMalloc(&p, bytes ? bytes : 64, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        k3k_fail("hipHostMalloc", e);
+        return nullptr;
+    }
+    return p;
+}
+
+extern "C" void k3k_host_free(void *p)
+{
+    if (p) (void)hipHostFree(p);
+}
+
+extern "C" void *k3k_event_create(void)
+{
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        k3k_fail("hipEventCreate", e);
+        return nullptr;
+    }
+    return (void *)ev;
+}
+
+extern "C" int k3k_event_record(void *ev, void *stream)
+{
+    hipError_t e = hipEventRecord((hipEvent_t)ev, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : k3k_fail("hipEventRecord", e);
+}
+
+extern "C" int k3k_event_sync(void *ev)
+{
+    hipError_t e = hipEventSynchronize((hipEvent_t)ev);
+    return e == hipSuccess ? 0 : k3k_fail("hipEventSynchronize", e);
+}
+
 extern "C" int k3k_sync(void *stream)
 {
     hipError_t e = stream ? hipStreamSynchronize((hipStream_t)stream) : hipDeviceSynchronize();

@@ -175,7 +175,7 @@ struct SelSmem {
     int list[RF_LIST];
     double res[RF_LIST];
     __attribute__((aligned(16))) double prod[2][RF_BLK];
-    uint64_t cand[64];                             /* two-level selection: the waves' keys */
+    uint64_t cand[256];                            /* two-level selection: the waves' keys */
     uint64_t last;                                 /* its k-th key and count */
     int nsel;
     int wcnt[16];                                  /* listed experts per wave */
@@ -186,9 +186,11 @@ struct SelSmem {
  * Keys are unique (the expert's index in the low word), so the selection is the topk
  * largest keys in order, however they are found:
  *  - two levels, when the ng = ceil(n_experts / 64) groups of 64 experts fit the
- *    workgroup's waves and ng * topk <= 64: wave g takes the topk largest keys of group g
+ *    workgroup's waves and ng * topk <= 256: wave g takes the topk largest keys of group g
  *    (one key per lane, each extraction one wave maximum, wave_max_key_fast), then wave 0
- *    the topk largest of those ng * topk candidates (one per lane);
+ *    the topk largest of those ng * topk candidates (one to four per lane: a lane holds
+ *    candidates l + 64 i and the largest of them, and after each pick the lane that held
+ *    it takes its next);
  *  - else wave 0 alone: lane l holds the keys of experts l + 64 i (SW of them) and the
  *    largest of its keys; after each extraction the lane that held it drops the key and
  *    takes its next largest.
@@ -205,7 +207,8 @@ __device__ uint64_t select_rounds(SelSmem<SW> &sm, const float *x, const float *
 {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = (int)blockDim.x >> 6;
     const int ng = (n_experts + 63) >> 6;
-    const bool two = ng <= nw && ng <= SW && ng * topk <= 64;
+    const bool two = ng <= nw && ng <= SW && ng * topk <= 256;
+    const int nc = ng * topk;                       /* level-2 candidates, one to four per lane */
     auto key_of = [&](int e) {
         const float c = sm.c[e];
         return (e < n_experts && c > -INFINITY) ? ((uint64_t)choice_order(c) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e)
@@ -226,8 +229,8 @@ __device__ uint64_t select_rounds(SelSmem<SW> &sm, const float *x, const float *
             }
             __syncthreads();
             /* level 2: the topk largest candidates */
-            if (wv == 0) {
-                uint64_t k = lane < ng * topk ? sm.cand[lane] : 0ull;
+            if (wv == 0 && nc <= 64) {
+                uint64_t k = lane < nc ? sm.cand[lane] : 0ull;
                 int nsel = 0;
                 uint64_t last = 0ull;
                 mysel = 0ull;
@@ -238,6 +241,38 @@ __device__ uint64_t select_rounds(SelSmem<SW> &sm, const float *x, const float *
                     last = m;
                     if (lane == j) mysel = m;
                     if (k == m) k = 0ull;
+                }
+                if (lane == 0) {
+                    sm.nsel = nsel;
+                    sm.last = last;
+                }
+            } else if (wv == 0) {
+                /* more than 64 candidates: lane l holds candidates l + 64 i and the largest of
+                 * them; after each pick the lane that held it drops it and takes its next */
+                uint64_t ck[4], head = 0ull;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    ck[i] = lane + 64 * i < nc ? sm.cand[lane + 64 * i] : 0ull;
+                    head = head > ck[i] ? head : ck[i];
+                }
+                int nsel = 0;
+                uint64_t last = 0ull;
+                mysel = 0ull;
+                for (int j = 0; j < topk; j++) {
+                    const uint64_t m = wave_max_key_fast(head);
+                    if (m == 0ull) break;           /* no finite choice left */
+                    nsel++;
+                    last = m;
+                    if (lane == j) mysel = m;
+                    if (head == m) {
+                        uint64_t h2 = 0ull;
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            if (ck[i] == m) ck[i] = 0ull;
+                            h2 = h2 > ck[i] ? h2 : ck[i];
+                        }
+                        head = h2;
+                    }
                 }
                 if (lane == 0) {
                     sm.nsel = nsel;

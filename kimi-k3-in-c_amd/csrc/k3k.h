@@ -34,6 +34,12 @@ int k3k_cu_count(void);
 /* Graph capture of the work enqueued on `stream` (a created stream, not NULL). */
 /* k3k_fork: *side = a second stream that first waits for the work queued on stream;
  * k3k_join: stream waits for the work queued on the side stream since. */
+/* pinned host memory and events (host-side waits for part of a stream's work) */
+void *k3k_host_alloc(size_t bytes);
+void k3k_host_free(void *p);
+void *k3k_event_create(void);
+int k3k_event_record(void *ev, void *stream);
+int k3k_event_sync(void *ev);
 int k3k_side_init(void);
 int k3k_fork(void *stream, void **side);
 int k3k_join(void *stream);
@@ -209,10 +215,11 @@ typedef struct {
 /* 1 when k3k_router_final can run the gather (more than a few tokens, the one-workgroup
  * gather's sizes). */
 int k3k_router_gathers(int T, int hidden, int n_experts, int topk);
-/* ctr (may be NULL): set to zero, for a following k3k_router_final that gathers. */
+/* ctr (may be NULL): set to zero, and idx [n_idx] to -1, for a following k3k_router_final
+ * that gathers (its gathering workgroup waits for every idx it reads to be set). */
 int k3k_router_partial(double *part, float *rbound, const float *x, int T, const float *W,
-                       int hidden, int n_experts, int chunk, int *ctr, const K3kExc *exc,
-                       void *stream);
+                       int hidden, int n_experts, int chunk, int *ctr, int *idx, int n_idx,
+                       const K3kExc *exc, void *stream);
 /* gather (may be NULL): also run the gather of idx, as k3k_gather would. */
 int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, const float *rbound,
                      int chunk, const float *x, const float *W, const float *bias, int T,
