@@ -46,9 +46,23 @@
 #include "k3_select.h"
 
 #include <type_traits>
+#include <utility>
 #include "k3k.h"
 
 namespace {
+
+/* f(std::integral_constant<int, s>{}) for s = 0 .. N-1, unrolled at compile time (register
+ * slots of a load ring must be indexed by constants) */
+template <typename F, int... S>
+__device__ __forceinline__ void k3_static_for_impl(F &&f, std::integer_sequence<int, S...>)
+{
+    (f(std::integral_constant<int, S>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void k3_static_for(F &&f)
+{
+    k3_static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 struct ExpertQDev {
     const uint8_t *p1, *s1, *p3, *s3, *p2, *s2;
@@ -602,7 +616,7 @@ __global__ __launch_bounds__(1024) void mx_gemv_small_kernel(K3kMxArgs a, int kw
  * few tokens): the workgroup first selects its token's experts from the router's scored
  * records (select_rounds), so no separate selection kernel runs. Two activation
  * terms share one MFMA: column 0 is the hi term, column 1 the lo term, added at the end. */
-template <int MODE, int NS, int LAYOUT, int TPW, bool SEL = false, bool SPLIT = false>
+template <int MODE, int NS, int LAYOUT, int TPW, bool SEL = false, bool SPLIT = false, int DEPTH = 2>
 __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* [NS][K], zeros[512] */
@@ -728,12 +742,12 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
     /* chunk c of this wave's tile: LAYOUT 1, four contiguous 1 KB loads and one scale
      * dword (byte i = step i); LAYOUT 0, blocks 4i+g of the lane's row and the row's 16
      * scale bytes (dword i, byte g = step i) */
-    uint4 qa[2][NM][4];
-    uint4 sq[2][NM];
+    uint4 qa[DEPTH][NM][4];
+    uint4 sq[DEPTH][NM];
     /* Chunks past the wave's last are loaded too, at an offset beyond every buffer (2^31):
      * they return zeros and move no data. With no load under a branch, every wait counts
-     * exactly the loads issued after the one it waits for, so chunk c + 1 stays in flight
-     * while chunk c is multiplied. */
+     * exactly the loads issued after the one it waits for, so chunks c + 1 .. c + DEPTH - 1
+     * stay in flight while chunk c is multiplied. */
     constexpr uint32_t OOB = 0x80000000u;
     auto load = [&](int c, auto slot) {
         constexpr int S = decltype(slot)::value;
@@ -754,14 +768,12 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
             }
         }
     };
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
-    /* issued in the loop's order (slot 0, then slot 1): the waits at the loop head take the
-     * worse of the two ways in, so a reordered prologue would make them wait for slot 1 too */
-    load(c0, P0{});
-    __builtin_amdgcn_sched_barrier(0);
-    load(c0 + 1, P1{});
-    __builtin_amdgcn_sched_barrier(0);
+    /* issued in the loop's order (slot 0, 1, ...): the waits at the loop head take the worse
+     * of the two ways in, so a reordered prologue would make them wait for later slots too */
+    k3_static_for<DEPTH>([&](auto sl) {
+        load(c0 + decltype(sl)::value, sl);
+        __builtin_amdgcn_sched_barrier(0);
+    });
     for (int i = tid; i < 64; i += nthr)
         reinterpret_cast<uint4 *>(&xs[(size_t)NS * K])[i] = make_uint4(0, 0, 0, 0);
     if (MODE == K3K_MX_GATEUP) {
@@ -814,13 +826,14 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
         }
     };
     int c = c0;
-    for (; c + 1 < c1; c += 2) {
-        comp(c, P0{});
-        load(c + 2, P0{});
-        comp(c + 1, P1{});
-        load(c + 3, P1{});
-    }
-    if (c < c1) comp(c, P0{});
+    for (; c + DEPTH - 1 < c1; c += DEPTH)
+        k3_static_for<DEPTH>([&](auto sl) {
+            comp(c + decltype(sl)::value, sl);
+            load(c + decltype(sl)::value + DEPTH, sl);
+        });
+    k3_static_for<DEPTH - 1>([&](auto sl) {
+        if (c + decltype(sl)::value < c1) comp(c + decltype(sl)::value, sl);
+    });
     /* K shares in order: share 0 adds those of shares 1.. (LDS reused after the products);
      * then column 0 (hi) + column 1 (lo) */
     k3_f32x4 *red = reinterpret_cast<k3_f32x4 *>(xs);
@@ -885,7 +898,7 @@ __global__ __launch_bounds__(TPW == 4 ? 512 : 1024) void mx_decode_kernel(K3kMxA
  * (k3_ops.c:641-642). An absent slot's wave reads through an empty descriptor (zeros) and
  * its sum is left out. Two activation terms share one MFMA (columns 0 and 1), each term's
  * shares are added in order, then hi + lo. */
-template <int NS, int LAYOUT, bool GU = false>
+template <int NS, int LAYOUT, bool GU = false, int DEPTH = 2>
 __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   /* [topk][NS][K], zeros[512] */
@@ -922,8 +935,8 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
     const k3_rsrc rp = k3_make_rsrc(q.p2, valid ? prow * (uint32_t)(K >> 1) : 0u);
     const k3_rsrc rs = k3_make_rsrc(q.s2, valid ? prow * (uint32_t)nblk : 0u);
     const int row = min(tile * 16 + r16, rows - 1);
-    uint4 qa[2][4];
-    uint4 sq[2];
+    uint4 qa[DEPTH][4];
+    uint4 sq[DEPTH];
     /* chunks past the wave's last load zeros from beyond the buffer, so no load sits under
      * a branch and the waits count exactly (as in mx_decode_kernel) */
     constexpr uint32_t OOB = 0x80000000u;
@@ -963,10 +976,10 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
     };
     if constexpr (GU) load_gu(0, gv0, uv0);
     __builtin_amdgcn_sched_barrier(0);
-    load(c0, P0{});                                         /* in the loop's order */
-    __builtin_amdgcn_sched_barrier(0);
-    load(c0 + 1, P1{});
-    __builtin_amdgcn_sched_barrier(0);
+    k3_static_for<DEPTH>([&](auto sl) {                     /* in the loop's order */
+        load(c0 + decltype(sl)::value, sl);
+        __builtin_amdgcn_sched_barrier(0);
+    });
     /* this wave's slot and columns of the activation terms into [slot][term][K] (the waves
      * of one slot stage disjoint column ranges), and the row of zeros (every wave writes the
      * same zeros): no workgroup barrier before the products */
@@ -1068,13 +1081,14 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
         }
     };
     int c = c0;
-    for (; c + 1 < c1; c += 2) {
-        comp(c, P0{});
-        load(c + 2, P0{});
-        comp(c + 1, P1{});
-        load(c + 3, P1{});
-    }
-    if (c < c1) comp(c, P0{});
+    for (; c + DEPTH - 1 < c1; c += DEPTH)
+        k3_static_for<DEPTH>([&](auto sl) {
+            comp(c + decltype(sl)::value, sl);
+            load(c + decltype(sl)::value + DEPTH, sl);
+        });
+    k3_static_for<DEPTH - 1>([&](auto sl) {
+        if (c + decltype(sl)::value < c1) comp(c + decltype(sl)::value, sl);
+    });
     /* lanes of token column 0 (hi) and 1 (lo) hold the tile's 16 rows, four each */
     if (r16 < NS) {
         const k3_f32x4 sum = acc[0] + acc[1];
