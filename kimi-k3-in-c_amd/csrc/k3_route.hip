@@ -120,6 +120,30 @@ constexpr int RP_KS = 32, RP_SUB = 32;     /* chunk granule and bound sub-block,
  * for and sub-block sc + 2 stays in flight while sc is multiplied and sc + 1 stored. */
 constexpr int RM_LD = 36;
 
+/* v combined with the value of the lane DPP control CTRL names (quad_perm, row_half_mirror:
+ * each names a lane of the same group of eight) */
+template <int CTRL>
+__device__ __forceinline__ float dpp8_f32(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+/* sum / maximum over each aligned group of 8 lanes, in every lane of the group: pairs
+ * (quad_perm [1,0,3,2]), quads ([2,3,0,1]), then the two quads (row_half_mirror), so lane
+ * 8g + i holds ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)) of its group, the order of
+ * an xor-1, 2, 4 butterfly */
+__device__ __forceinline__ float group8_sum(float v)
+{
+    v += dpp8_f32<0xB1>(v);
+    v += dpp8_f32<0x4E>(v);
+    return v + dpp8_f32<0x141>(v);
+}
+__device__ __forceinline__ float group8_max(float v)
+{
+    v = fmaxf(v, dpp8_f32<0xB1>(v));
+    v = fmaxf(v, dpp8_f32<0x4E>(v));
+    return fmaxf(v, dpp8_f32<0x141>(v));
+}
+
 template <int MT, int ME, bool BUF>
 __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, float *rbound,
                                                                   const float *x, int T,
@@ -222,20 +246,16 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
         for (int i = 0; i < NWP; i++) {
             const int r = (tid + 256 * i) >> 3;
             *reinterpret_cast<float4 *>(&ws[buf][r * RM_LD + c]) = wst[S][i];
-            float a = fabsf(wst[S][i].x) + fabsf(wst[S][i].y) + fabsf(wst[S][i].z) + fabsf(wst[S][i].w);
-            a += __shfl_xor(a, 1, 64);
-            a += __shfl_xor(a, 2, 64);
-            a += __shfl_xor(a, 4, 64);
+            const float a = group8_sum(fabsf(wst[S][i].x) + fabsf(wst[S][i].y) + fabsf(wst[S][i].z) +
+                                       fabsf(wst[S][i].w));
             if ((tid & 7) == 0) wn[buf][r] = a;
         }
 #pragma unroll
         for (int i = 0; i < NXP; i++) {
             const int r = (tid + 256 * i) >> 3;
             *reinterpret_cast<float4 *>(&xs[buf][r * RM_LD + c]) = xst[S][i];
-            float m = fmaxf(fmaxf(fabsf(xst[S][i].x), fabsf(xst[S][i].y)), fmaxf(fabsf(xst[S][i].z), fabsf(xst[S][i].w)));
-            m = fmaxf(m, __shfl_xor(m, 1, 64));
-            m = fmaxf(m, __shfl_xor(m, 2, 64));
-            m = fmaxf(m, __shfl_xor(m, 4, 64));
+            const float m = group8_max(fmaxf(fmaxf(fabsf(xst[S][i].x), fabsf(xst[S][i].y)),
+                                             fmaxf(fabsf(xst[S][i].z), fabsf(xst[S][i].w))));
             if ((tid & 7) == 0) xn[buf][r] = m;
         }
     };
