@@ -305,12 +305,15 @@ __global__ __launch_bounds__(256) void dense_finish_kernel(DgArgs a)
     }
 }
 
-/* K slices: enough for two workgroups per CU, each slice at least 256 columns (4 steps);
- * 1 without a large enough partials buffer or when the output rows are not a multiple of 4. */
+/* K slices: the fewest that give every CU one and a half workgroups, each slice at least
+ * 256 columns (4 steps); 1 without a large enough partials buffer or when the output rows
+ * are not a multiple of 4. (At 512 tokens, measured: gate/up 7168 -> 2048, 128 tiles, takes
+ * 122 / 66 / 58 / 67 us at 1 / 2 / 4 / 8 slices plus 7-13 us of slice sums; down 2048 ->
+ * 7168, 224 tiles, 55 / 38 / 47 / 59 us plus 11-24 us.) */
 static int dense_slices(int tiles, int K, int R, int T, int ncol, size_t part_bytes)
 {
     if (R % 4) return 1;
-    const long want = 2L * k3k_cu_count();
+    const long want = 3L * k3k_cu_count() / 2;
     int s = 1;
     while (s < 8 && (long)tiles * s < want && K / DG_KS / (2 * s) >= 4 &&
            (size_t)(2 * s) * T * ncol * 4 <= part_bytes)
