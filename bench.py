@@ -121,9 +121,9 @@ def time_layer(layer, T, steps, warmup, nbatch=4):
     return (t1 - t0), stages, u_mean, uniq
 
 
-def time_prefill(layer, T=4096, steps=3, warmup=1):
+def time_prefill(layer, T=4096, steps=5, warmup=1, prof_reps=3):
     """Prefill layer (config 3): T tokens, bf16 activations, 96-token expert passes on the
-    matrix cores. Eager calls; the stage profile comes from the timed calls themselves."""
+    matrix cores. Eager calls; the stage profile is the mean over prof_reps more calls."""
     L = k3amd.lib()
     x = k3amd.DevBuf(T * E * 4).upload(wl.tokens(T, tag="bench.prefill"))
     out = k3amd.DevBuf(T * E * 4)
@@ -138,8 +138,9 @@ def time_prefill(layer, T=4096, steps=3, warmup=1):
         layer.run(x, out, idx, wt, T, ws, prec=1)
     k3amd.check(L.k3d_sync(None))
     t1 = time.perf_counter()
-    prof = k3amd.Profile(max_marks=64)
-    layer.run(x, out, idx, wt, T, ws, prec=1)
+    prof = k3amd.Profile(max_marks=16 * prof_reps)
+    for _ in range(prof_reps):
+        layer.run(x, out, idx, wt, T, ws, prec=1)
     k3amd.check(L.k3d_sync(None))
     st = prof.end()
     h = idx.download(np.empty((T, K), np.int32))
@@ -147,7 +148,7 @@ def time_prefill(layer, T=4096, steps=3, warmup=1):
         b.free()
     ms = (t1 - t0) / steps * 1e3
     flops = T * K * 3 * 2 * E * I                  # 2.886 TFLOP at T=4096
-    expert_ms = sum(st.get(k, (0.0, 0))[0] for k in ("gateup", "down"))
+    expert_ms = sum(st.get(k, (0.0, 0))[0] / max(st.get(k, (0.0, 1))[1], 1) for k in ("gateup", "down"))
     return {"tokens": T, "ms_per_step": round(ms, 3), "tokens_per_s": round(T / ms * 1e3, 1),
             "arithmetic": "activations rounded to bf16 (one term), weights dequantized exactly, "
                           "bf16 MFMA with fp32 accumulation; tolerance 2e-2 relative",
@@ -204,7 +205,7 @@ def time_expert_ffn(layer, per_graph=16, reps=20):
             "frac_of_peak": round(algo / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
-def time_skewed(layer, T=512, steps=5, warmup=1):
+def time_skewed(layer, T=512, steps=5, warmup=1, prof_reps=3):
     """Skewed routing + dense trunk (config 4): T tokens, router selection bias giving
     Zipf(1.2)-like expert popularity, routed experts with bf16 activations, then the
     always-on bf16 shared expert (7168 -> 2048 -> 7168) accumulated onto the output."""
@@ -233,8 +234,9 @@ def time_skewed(layer, T=512, steps=5, warmup=1):
         step()
     k3amd.check(L.k3d_sync(None))
     t1 = time.perf_counter()
-    prof = k3amd.Profile(max_marks=64)
-    step()
+    prof = k3amd.Profile(max_marks=16 * prof_reps)
+    for _ in range(prof_reps):
+        step()
     k3amd.check(L.k3d_sync(None))
     st = prof.end()
     # one more step with per-workgroup stamps of the routed expert kernels
@@ -253,9 +255,10 @@ def time_skewed(layer, T=512, steps=5, warmup=1):
         b.free()
     cnt = np.sort(np.bincount(h.ravel(), minlength=N))[::-1]
     ms = (t1 - t0) / steps * 1e3
-    sh_ms = st.get("shared", (0.0, 1))[0]
+    mean = lambda k: st.get(k, (0.0, 1))[0] / max(st.get(k, (0.0, 1))[1], 1)
+    sh_ms = mean("shared")
     sh_flops = T * 3 * 2 * E * I
-    routed_ms = sum(st.get(k, (0.0, 0))[0] for k in ("gateup", "down"))
+    routed_ms = mean("gateup") + mean("down")
     u = int((cnt > 0).sum())
     routed_bytes = u * EXPERT_BYTES
     routed_flops = T * K * 3 * 2 * E * I

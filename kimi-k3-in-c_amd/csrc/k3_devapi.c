@@ -368,7 +368,7 @@ static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n
     w->max_passes2 = prec == 1 ? (int)(N / MOE_PASS_TOK2 + N / 33 + 2) : 0;
     w->pass_job2 = prec == 1 ? (int *)take(c, (size_t)w->max_passes2 * 4) : NULL;
     w->pass_tp2 = prec == 1 ? (int *)take(c, (size_t)w->max_passes2 * 4) : NULL;
-    w->counts = (int *)take(c, 16);
+    w->counts = (int *)take(c, (size_t)(4 + K3K_QUEUE_INTS) * 4);
     {
         const size_t gs = k3k_gather_scratch(T, topk, n_experts);
         w->ghist = gs ? (int *)take(c, gs * 4) : NULL;
@@ -551,6 +551,8 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     /* the second list's gate/up and down run on a side stream beside the first's */
     void *side = NULL;
     if (pass_tok2 && k3k_fork(stream, &side)) return fail("fork");
+    a.queue = w->counts + 4;
+    a2.queue = w->counts + 4 + 2 * K3K_NXCD_Q;
     if (k3k_mx_gemm(K3K_MX_GATEUP, &a, stream)) return fail("mx_gemm gateup");
     if (pass_tok2 && k3k_mx_gemm(K3K_MX_GATEUP, &a2, side)) return fail("mx_gemm gateup (96)");
     k3k_prof_mark(stream, K3D_STAGE_GATEUP);
@@ -561,6 +563,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     a.rows = hidden;
     a.K = inter;
     a.n_xrows = T * topk;
+    a.queue = w->counts + 4 + K3K_NXCD_Q;
     if (k3k_mx_gemm(K3K_MX_DOWN, &a, stream)) return fail("mx_gemm down");
     if (pass_tok2) {
         a2.xhi = a.xhi;
@@ -569,6 +572,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
         a2.rows = a.rows;
         a2.K = a.K;
         a2.n_xrows = a.n_xrows;
+        a2.queue = w->counts + 4 + 3 * K3K_NXCD_Q;
         if (k3k_mx_gemm(K3K_MX_DOWN, &a2, side)) return fail("mx_gemm down (96)");
         if (k3k_join(stream)) return fail("join");
     }

@@ -1532,7 +1532,24 @@ void mx_prefill_kernel(K3kMxArgs a)
         if (a.stamps) k3_stamp_begin(a.stamps);
     }
 
-    for (int item = li; item < n_items; item += nlw) {
+    /* The group's next item: with a.queue, the next number of the group's counter (zero at
+     * launch), so that the workgroups that finish early take more items (fixed shares had
+     * left the median workgroup idle the last 9-10 % of the kernel: items of 16 to 56
+     * stages, 13 or 14 of them per workgroup); else the fixed share item, item + nlw, ... */
+    /* (the counter's address waits in LDS: held in registers through the loop it would
+     * spill, as the stamps pointer would) */
+    const bool queued = a.queue != nullptr;
+    __shared__ int item_sh;
+    __shared__ int *queue_sh;
+    if (tid == 0) queue_sh = queued ? a.queue + xg : nullptr;
+    auto next_item = [&](int cur) -> int {
+        if (!queued) return cur < 0 ? li : cur + nlw;
+        if (tid == 0) item_sh = __hip_atomic_fetch_add(queue_sh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        return __builtin_amdgcn_readfirstlane(item_sh);
+    };
+
+    for (int item = next_item(-1); item < n_items; item = next_item(item)) {
         const int rb = item % n_rb, pass = pbeg + item / n_rb;
         const int j = a.pass_job[pass];
         const int e = a.job_expert[j];

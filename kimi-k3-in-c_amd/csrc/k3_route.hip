@@ -934,6 +934,7 @@ __device__ void gather_plan(const int *cnt, int *fill, int (*wtot5)[5], int *off
         counts[2] = tot_d;
         counts[3] = tot_e;
     }
+    if (tid >= 4 && tid < 4 + K3K_QUEUE_INTS) counts[tid] = 0;    /* the work-item counters */
     __syncthreads();
 }
 

@@ -134,6 +134,11 @@ typedef struct {
      * start and end (s_memrealtime, 100 MHz) and the hardware id (XCC_ID << 32 | HW_ID), or
      * NULL. The launchers fill it in. */
     unsigned long long *stamps;
+    /* mx_prefill_kernel: K3K_NXCD_Q work-item counters, zero at launch (k3k_gather zeroes the
+     * K3K_QUEUE_INTS after its counts), one per XCD group of workgroups: each workgroup takes
+     * its next (pass, row block) from its group's counter instead of a fixed share. NULL:
+     * fixed shares. */
+    int *queue;
 } K3kMxArgs;
 
 /* Per-workgroup stamps (a profiling aid): while enabled, each launch of mx_moe_kernel /
@@ -227,6 +232,10 @@ int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, cons
                      const K3kExc *exc, const K3kGatherArgs *gather, void *stream);
 
 /* ---- gather / combine -------------------------------------------------------------- */
+/* Work-item counters after the gather's four counts (counts[4 ..]): K3K_NXCD_Q per expert-
+ * kernel launch, for up to four launches (gate/up and down of both pass lists). */
+#define K3K_NXCD_Q 8
+#define K3K_QUEUE_INTS (4 * K3K_NXCD_Q)
 /* Stable expert-major gather of the T*topk assignments in idx. Outputs:
  *   offsets[n_experts+1]; perm[T*topk]: sorted position -> assignment t*topk+j, experts
  *   ascending and (t, j) ascending inside one expert; jobs = experts with at least one
@@ -234,7 +243,9 @@ int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, cons
  *   of up to pass_tok tokens of one job: pass_job/pass_tp; counts[0] = n_jobs,
  *   counts[1] = n_passes, counts[2] = assignments whose bank entry is NULL (dropped).
  *   pass_tok2 > 0: jobs of more than pass_tok assignments are split into passes of up to
- *   pass_tok2 tokens in pass_job2/pass_tp2 instead, counts[3] = their number (else 0). */
+ *   pass_tok2 tokens in pass_job2/pass_tp2 instead, counts[3] = their number (else 0).
+ *   counts[4 .. 4 + K3K_QUEUE_INTS) are set to zero (the expert kernels' work-item
+ *   counters), so counts holds 4 + K3K_QUEUE_INTS ints. */
 int k3k_gather(int *offsets, int *perm, int *job_expert, int *job_off, int *job_cnt,
                int *pass_job, int *pass_tp, int *pass_job2, int *pass_tp2, int *counts,
                int *hist, const int *idx, int T, int topk, int n_experts, const void *bank,
