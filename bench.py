@@ -121,9 +121,11 @@ def time_layer(layer, T, steps, warmup, nbatch=4):
     return (t1 - t0), stages, u_mean, uniq
 
 
-def time_prefill(layer, T=4096, steps=5, warmup=1, prof_reps=3):
+def time_prefill(layer, T=4096, steps=5, warmup=3, prof_reps=3):
     """Prefill layer (config 3): T tokens, bf16 activations, 96-token expert passes on the
-    matrix cores. Eager calls; the stage profile is the mean over prof_reps more calls."""
+    matrix cores. Eager calls after `warmup` untimed ones (the expert kernels take a few
+    calls to reach their steady duration: the first timed call of a fresh process runs about
+    15 % longer); the stage profile is the mean over prof_reps more calls."""
     L = k3amd.lib()
     x = k3amd.DevBuf(T * E * 4).upload(wl.tokens(T, tag="bench.prefill"))
     out = k3amd.DevBuf(T * E * 4)
@@ -205,7 +207,7 @@ def time_expert_ffn(layer, per_graph=16, reps=20):
             "frac_of_peak": round(algo / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
-def time_skewed(layer, T=512, steps=5, warmup=1, prof_reps=3):
+def time_skewed(layer, T=512, steps=5, warmup=3, prof_reps=3):
     """Skewed routing + dense trunk (config 4): T tokens, router selection bias giving
     Zipf(1.2)-like expert popularity, routed experts with bf16 activations, then the
     always-on bf16 shared expert (7168 -> 2048 -> 7168) accumulated onto the output."""

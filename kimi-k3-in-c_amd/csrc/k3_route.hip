@@ -92,7 +92,6 @@ __device__ __forceinline__ float bound_up(double rb, double rel)
 }
 
 constexpr int RP_KS = 32, RP_SUB = 32;     /* chunk granule and bound sub-block, columns */
-constexpr int RP_SBS = 2;                  /* sub-blocks per LDS stage of the MFMA partials */
 
 /* Partials of more than four tokens on the fp64 matrix cores. v_mfma_f64_16x16x4f64 adds
  * to each element of a 16 x 16 block four exact products (fp32 operands widened to fp64
@@ -110,22 +109,21 @@ constexpr int RP_SBS = 2;                  /* sub-blocks per LDS stage of the MF
  * columns (B operand), so element (i, j) sits at lane j + 16 (i % 4), register i / 4 and
  * 16 lanes store 16 consecutive experts of one token. A wave computes MT x ME blocks
  * (16 MT tokens x 16 ME experts), the 4 waves of a workgroup 2 x 2 of those. W and x are
- * staged in LDS as fp32 a stage of SBS sub-blocks at a time (rows padded by 4 floats: the
- * 16-byte reads of 8 consecutive lanes fall on distinct banks), double buffered, with the
- * norms of each sub-block; one barrier per stage (two sub-blocks per stage: 4096 tokens
- * 0.666 -> 0.644 ms). The bound is accumulated in fp32, rounded up at the end by its
- * relative error ((nsub + 4) 2^-24).
+ * staged in LDS as fp32 (rows padded to 36 floats: the 16-byte reads of 8 consecutive
+ * lanes fall on distinct banks), double buffered, with the sub-block norms. The bound is
+ * accumulated in fp32, rounded up at the end by its relative error ((nsub + 4) 2^-24).
  *
- * The stages are loaded two ahead into a ring of two register slots. With BUF (rows a
- * multiple of 4 floats, 16-byte aligned, W and x under 2 GiB) every load is a buffer load
- * with no branch around it (rows and columns past the tile's read at an offset beyond the
- * buffer: zeros), so each wait counts exactly the loads issued after the ones it waits for
- * and stage st + 2 stays in flight while st is multiplied and st + 1 stored.
+ * The sub-blocks are loaded two ahead into a ring of two register slots. With BUF (rows
+ * a multiple of 4 floats, 16-byte aligned, W and x under 2 GiB) every load is a buffer
+ * load with no branch around it (rows and columns past the tile's read at an offset beyond
+ * the buffer: zeros), so each wait counts exactly the loads issued after the ones it waits
+ * for and sub-block sc + 2 stays in flight while sc is multiplied and sc + 1 stored.
  *
  * On gfx950 the fp64 MFMA and the vector instructions of the waves of a SIMD do not
  * overlap (measured: each fp32 FMA between two v_mfma_f64_16x16x4f64 adds 1-2 ns to the
  * SIMD's time), so the kernel's time is about the MFMAs' plus the vector work's plus the
  * latency the waves cannot hide. */
+constexpr int RM_LD = 36;
 
 /* v combined with the value of the lane DPP control CTRL names (quad_perm, row_half_mirror:
  * each names a lane of the same group of eight) */
@@ -151,7 +149,7 @@ __device__ __forceinline__ float group8_max(float v)
     return fmaxf(v, dpp8_f32<0x141>(v));
 }
 
-template <int MT, int ME, bool BUF, int SBS>
+template <int MT, int ME, bool BUF>
 __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, float *rbound,
                                                                   const float *x, int T,
                                                                   const float *W, int hidden,
@@ -167,13 +165,11 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
     }
     typedef double d4 __attribute__((ext_vector_type(4)));
     constexpr int TB = 32 * MT, EB = 32 * ME;           /* workgroup tile: tokens, experts */
-    constexpr int KSW = RP_KS * SBS, PPR = KSW / 4;      /* stage columns, float4 pieces per row */
-    constexpr int LDW = KSW + 4;                         /* LDS row stride, floats */
-    constexpr int NWP = EB * PPR / 256, NXP = TB * PPR / 256;   /* pieces per thread: W, x */
-    __shared__ __attribute__((aligned(16))) float ws[2][EB * LDW];
-    __shared__ __attribute__((aligned(16))) float xs[2][TB * LDW];
-    __shared__ float wn[2][SBS][EB];                     /* sum |w| over each sub-block */
-    __shared__ float xn[2][SBS][TB];                     /* max |x| over each sub-block */
+    constexpr int NWP = EB / 32, NXP = TB / 32;         /* float4 pieces per thread: W, x */
+    __shared__ __attribute__((aligned(16))) float ws[2][EB * RM_LD];
+    __shared__ __attribute__((aligned(16))) float xs[2][TB * RM_LD];
+    __shared__ float wn[2][EB];                          /* sum |w| over the sub-block */
+    __shared__ float xn[2][TB];                          /* max |x| over the sub-block */
     const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
     const int wt = wv >> 1, we = wv & 1;                 /* the wave's block of the tile */
     /* A one-dimensional grid dealt to the XCDs (workgroup b runs on XCD b % 8), so that
@@ -208,7 +204,6 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
     const int e0 = bx * EB, t0 = by * TB;
     const int kb0 = ks * chunk, kb1 = min(hidden, kb0 + chunk);
     const int nsub = (kb1 - kb0 + RP_KS - 1) / RP_KS;
-    const int nst = (nsub + SBS - 1) / SBS;              /* stages of SBS sub-blocks */
     const float *Wt = W + (size_t)e0 * hidden, *xt = x + (size_t)t0 * hidden;
     float4 wst[2][NWP], xst[2][NXP];                    /* the ring: two sub-blocks */
     k3_rsrc rsw, rsx;
@@ -236,40 +231,37 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
         const uint32_t off = in ? (uint32_t)(((size_t)(row0 + r) * hidden + k) * 4) : 0x80000000u;
         return __builtin_bit_cast(float4, k3_bload16(rs, off));
     };
-    /* piece p = tid + 256 i: row p / PPR, columns 4 (p % PPR) .. + 3 of the stage (256 is
-     * a multiple of PPR, so a thread's column is the same in every piece) */
-    auto load = [&](int st, auto slot) {
+    /* piece p = tid + 256 i: row p / 8, columns 4 (p % 8) .. + 3 */
+    auto load = [&](int sc, auto slot) {
         constexpr int S = decltype(slot)::value;
-        const int k0 = kb0 + st * KSW + (tid % PPR) * 4;
+        const int k0 = kb0 + sc * RP_KS + (tid & 7) * 4;
 #pragma unroll
         for (int i = 0; i < NWP; i++)
-            wst[S][i] = BUF ? fetch_buf(rsw, e0, n_experts - e0, (tid + 256 * i) / PPR, k0)
-                            : fetch(Wt, n_experts - e0, (tid + 256 * i) / PPR, k0);
+            wst[S][i] = BUF ? fetch_buf(rsw, e0, n_experts - e0, (tid + 256 * i) >> 3, k0)
+                            : fetch(Wt, n_experts - e0, (tid + 256 * i) >> 3, k0);
 #pragma unroll
         for (int i = 0; i < NXP; i++)
-            xst[S][i] = BUF ? fetch_buf(rsx, t0, T - t0, (tid + 256 * i) / PPR, k0)
-                            : fetch(xt, T - t0, (tid + 256 * i) / PPR, k0);
+            xst[S][i] = BUF ? fetch_buf(rsx, t0, T - t0, (tid + 256 * i) >> 3, k0)
+                            : fetch(xt, T - t0, (tid + 256 * i) >> 3, k0);
     };
-    /* into LDS, with each row's norms per 32-column sub-block (the aligned group of 8 lanes
-     * holding one sub-block of one row) */
     auto store = [&](int buf, auto slot) {
         constexpr int S = decltype(slot)::value;
-        const int c = (tid % PPR) * 4, sbw = (tid % PPR) >> 3;
+        const int c = (tid & 7) * 4;
 #pragma unroll
         for (int i = 0; i < NWP; i++) {
-            const int r = (tid + 256 * i) / PPR;
-            *reinterpret_cast<float4 *>(&ws[buf][r * LDW + c]) = wst[S][i];
+            const int r = (tid + 256 * i) >> 3;
+            *reinterpret_cast<float4 *>(&ws[buf][r * RM_LD + c]) = wst[S][i];
             const float a = group8_sum(fabsf(wst[S][i].x) + fabsf(wst[S][i].y) + fabsf(wst[S][i].z) +
                                        fabsf(wst[S][i].w));
-            if ((tid & 7) == 0) wn[buf][sbw][r] = a;
+            if ((tid & 7) == 0) wn[buf][r] = a;
         }
 #pragma unroll
         for (int i = 0; i < NXP; i++) {
-            const int r = (tid + 256 * i) / PPR;
-            *reinterpret_cast<float4 *>(&xs[buf][r * LDW + c]) = xst[S][i];
+            const int r = (tid + 256 * i) >> 3;
+            *reinterpret_cast<float4 *>(&xs[buf][r * RM_LD + c]) = xst[S][i];
             const float m = group8_max(fmaxf(fmaxf(fabsf(xst[S][i].x), fabsf(xst[S][i].y)),
                                              fmaxf(fabsf(xst[S][i].z), fabsf(xst[S][i].w))));
-            if ((tid & 7) == 0) xn[buf][sbw][r] = m;
+            if ((tid & 7) == 0) xn[buf][r] = m;
         }
     };
     using R0 = std::integral_constant<int, 0>;
@@ -292,26 +284,22 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
     load(1, R1{});
     store(0, R0{});
     __syncthreads();
-    /* stage st: its ring slot (st & 1) is free once it is in LDS, so st + 2 loads into it;
-     * then st's sub-blocks are multiplied out of LDS buffer st & 1 and st + 1 stored into
-     * the other */
-    auto step = [&](int st, auto slot) {
+    /* sub-block sc: its ring slot (sc & 1) is free once it is in LDS, so sc + 2 loads into
+     * it; then sc is multiplied out of LDS buffer sc & 1 and sc + 1 stored into the other */
+    auto step = [&](int sc, auto slot) {
         constexpr int S = decltype(slot)::value;
         const int buf = S;
-        load(st + 2, slot);
-#pragma unroll
-        for (int sb = 0; sb < SBS; sb++) {
+        load(sc + 2, slot);
         /* bound term of this sub-block from the chains' values at its start: element
-         * (i, j) of block (a, b) is token trow + 16 a + 4 r + q, expert erow + 16 b + r16
-         * (the zeros past the chunk's last sub-block add no term) */
-        if (SBS == 1 || st * SBS + sb < nsub) {
+         * (i, j) of block (a, b) is token trow + 16 a + 4 r + q, expert erow + 16 b + r16 */
+        {
             float xr[MT][4], we_[ME];
 #pragma unroll
             for (int a = 0; a < MT; a++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) xr[a][r] = xn[buf][sb][trow + 16 * a + 4 * r + q];
+                for (int r = 0; r < 4; r++) xr[a][r] = xn[buf][trow + 16 * a + 4 * r + q];
 #pragma unroll
-            for (int b = 0; b < ME; b++) we_[b] = wn[buf][sb][erow + 16 * b + r16];
+            for (int b = 0; b < ME; b++) we_[b] = wn[buf][erow + 16 * b + r16];
 #pragma unroll
             for (int a = 0; a < MT; a++)
 #pragma unroll
@@ -326,10 +314,10 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
             float4 xa[MT], wb[ME];
 #pragma unroll
             for (int a = 0; a < MT; a++)
-                xa[a] = *reinterpret_cast<const float4 *>(&xs[buf][(trow + 16 * a + r16) * LDW + RP_KS * sb + 8 * q + 4 * h]);
+                xa[a] = *reinterpret_cast<const float4 *>(&xs[buf][(trow + 16 * a + r16) * RM_LD + 8 * q + 4 * h]);
 #pragma unroll
             for (int b = 0; b < ME; b++)
-                wb[b] = *reinterpret_cast<const float4 *>(&ws[buf][(erow + 16 * b + r16) * LDW + RP_KS * sb + 8 * q + 4 * h]);
+                wb[b] = *reinterpret_cast<const float4 *>(&ws[buf][(erow + 16 * b + r16) * RM_LD + 8 * q + 4 * h]);
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 double av[MT], bv[ME];
@@ -344,18 +332,17 @@ __global__ __launch_bounds__(256) void router_partial_mfma_kernel(double *part, 
                         acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b], acc[a][b], 0, 0, 0);
             }
         }
-        }
         /* past the chunk the slot holds zeros (BUF) and the buffer is not read again */
         store(buf ^ 1, std::integral_constant<int, S ^ 1>{});
         __syncthreads();
     };
     /* whole pairs in the loop, so that no load or store sits under a branch there */
-    int st = 0;
-    for (; st + 1 < nst; st += 2) {
-        step(st, R0{});
-        step(st + 1, R1{});
+    int sc = 0;
+    for (; sc + 1 < nsub; sc += 2) {
+        step(sc, R0{});
+        step(sc + 1, R1{});
     }
-    if (st < nst) step(st, R0{});
+    if (sc < nsub) step(sc, R0{});
     /* relative error of the fp32 bound: (nsub + 4) roundings of 2^-24, the float sums of
      * |w| at most 2^-18 */
     const double up = 1.0 + 0x1p-17 + (double)(nsub + 4) * 0x1p-24;
@@ -1440,16 +1427,11 @@ extern "C" int k3k_router_partial(double *part, float *rbound, const float *x, i
         const dim3 grid = deal == 1 ? dim3((unsigned)(nee * ntt * ks)) : dim3((unsigned)(K3_NXCD * per * nee));
         const bool buf = vec && (size_t)n_experts * hidden * 4 < 0x80000000u &&
                          (size_t)T * hidden * 4 < 0x80000000u;
-        /* stages of two sub-blocks when the chunk has an even count of them */
-        const bool two = chunk % (RP_KS * RP_SBS) == 0;
-        if (buf && two)
-            hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, true, RP_SBS>), grid, dim3(256), 0, st, part,
-                               rbound, x, T, W, hidden, n_experts, chunk, vec, deal, ctr, idx, n_idx);
-        else if (buf)
-            hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, true, 1>), grid, dim3(256), 0, st, part,
+        if (buf)
+            hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, true>), grid, dim3(256), 0, st, part,
                                rbound, x, T, W, hidden, n_experts, chunk, vec, deal, ctr, idx, n_idx);
         else
-            hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, false, 1>), grid, dim3(256), 0, st, part,
+            hipLaunchKernelGGL((router_partial_mfma_kernel<1, 2, false>), grid, dim3(256), 0, st, part,
                                rbound, x, T, W, hidden, n_experts, chunk, vec, deal, ctr, idx, n_idx);
     }
     K3K_LAUNCH_CHECK("router_partial launch");
