@@ -94,7 +94,8 @@ static void check(int rc, const char *what)
 
 /* Reusable device buffers, one per role, grown on demand. */
 enum { B_X, B_Y, B_P, B_S, B_WS, B_BIAS, B_RW, B_IDX, B_WT, B_ARENA, B_BANK, B_Z, B_ACC,
-       B_SGU, B_SDN, B_OUT, B_W2, B_W3, B_T0, B_T1, B_T2, B_XS, B_SACT, B_SSDN, B_SXS, B_COUNT };
+       B_SGU, B_SDN, B_OUT, B_W2, B_W3, B_T0, B_T1, B_T2, B_XS, B_SACT, B_SSDN, B_SXS, B_FACT,
+       B_COUNT };
 static void *g_buf[B_COUNT];
 static size_t g_cap[B_COUNT];
 
@@ -930,7 +931,7 @@ static void moe_latent(float *out, const float *x, const K3MoeW *w, const K3Cfg 
         const float *w2 = (const float *)weights(B_T2, w->w2, per2 * N * 4);
         float *contrib = (float *)buf(B_T0, TK * L * 4);
         float *gu = (float *)buf(B_T1, (size_t)2 * I * 4);
-        float *a = (float *)buf(B_SGU, (size_t)I * 4);
+        float *a = (float *)buf(B_FACT, (size_t)I * 4);     /* not B_SGU: the side stream's */
         for (int t = 0; t < T; t++)
             for (int j = 0; j < K; j++) {
                 const int e = hidx[t * K + j];

@@ -956,8 +956,6 @@ __global__ __launch_bounds__(1024) void mx_decode_combine_kernel(K3kMxArgs a)
             sq[S] = k3_bload16<WPOL>(rs, in ? (uint32_t)row * (uint32_t)nblk + (uint32_t)c * 16u : OOB);
         }
     };
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
     /* GU: the first pieces of the gate and up sums are requested before the weights, so
      * that waiting for them (loads complete in order) leaves the weight loads in flight */
     const k3_rsrc rg = k3_make_rsrc(a.gu, GU ? (uint32_t)a.n_assign * 2u * (uint32_t)K * 4u : 0u);
