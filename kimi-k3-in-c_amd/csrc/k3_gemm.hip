@@ -159,9 +159,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 
     using R0 = std::integral_constant<int, 0>;
     using R1 = std::integral_constant<int, 1>;
+    /* A step's two 32-column halves have fragment registers of their own (f0, f1), so that
+     * each half's LDS reads are in flight under the other half's MFMAs: half 1's reads
+     * issue under half 0's MFMAs, and the next step's half 0 reads (after the barrier that
+     * publishes its LDS buffer) under half 1's. */
+    k3_bf16x8 f0a[4], f0b[NS][NJ], f1a[4], f1b[NS][NJ];
+    auto rfrag = [&](int buf, int kk, k3_bf16x8 (&af)[4], k3_bf16x8 (&bf)[NS][NJ]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            af[i] = k3_as_bf16x8(*reinterpret_cast<const uint4 *>(&As[buf][(arow[i] + r16) * DG_LD + kk + 8 * g]));
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                bf[s][j] = k3_as_bf16x8(*reinterpret_cast<const uint4 *>(
+                    &Bs[buf][s][(bcol0 + 16 * j + r16) * DG_LD + kk + 8 * g]));
+    };
+    auto mma = [&](const k3_bf16x8 (&af)[4], const k3_bf16x8 (&bf)[NS][NJ]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int s = 0; s < NS; s++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[s][j], acc[i][j], 0, 0, 0);
+    };
+    /* issue order of a half: its MFMAs, each of the first 4 + NS NJ followed by one of the
+     * other half's fragment reads */
+    constexpr int NRD = 4 + NS * NJ, NMF = 4 * NJ * NS;
+    static_assert(NRD <= NMF, "fragment reads interleave with the MFMAs");
+    auto pin = [&]() {
+#pragma unroll
+        for (int i = 0; i < NRD; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      /* MFMA */
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      /* DS read */
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
+    };
     /* step ks: its ring slot (ks & 1) is free once it is in LDS, so ks + 2 loads into it;
      * ks is multiplied out of LDS buffer ks & 1 and ks + 1 stored into the other (past the
-     * slice the slot holds zeros and that buffer is not read again) */
+     * slice the slot holds zeros, and the fragments read from that buffer go unused) */
     auto step = [&](int ks, auto slot) {
         constexpr int S = decltype(slot)::value;
         const int buf = S;
@@ -169,33 +206,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         /* issued here, ahead of the products (the compiler would otherwise sink them below
          * the next LDS store and wait for step ks + 1 with nothing else in flight) */
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int kk = 0; kk < DG_KS; kk += 32) {
-            k3_bf16x8 af[4], bf[NS][NJ];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                af[i] = k3_as_bf16x8(*reinterpret_cast<const uint4 *>(&As[buf][(arow[i] + r16) * DG_LD + kk + 8 * g]));
-#pragma unroll
-            for (int s = 0; s < NS; s++)
-#pragma unroll
-                for (int j = 0; j < NJ; j++)
-                    bf[s][j] = k3_as_bf16x8(*reinterpret_cast<const uint4 *>(
-                        &Bs[buf][s][(bcol0 + 16 * j + r16) * DG_LD + kk + 8 * g]));
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < NJ; j++)
-#pragma unroll
-                    for (int s = 0; s < NS; s++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[s][j], acc[i][j], 0, 0, 0);
-        }
+        rfrag(buf, 32, f1a, f1b);
+        mma(f0a, f0b);
+        pin();
+        __builtin_amdgcn_sched_barrier(0);
         lstore(buf ^ 1, std::integral_constant<int, S ^ 1>{});
         __syncthreads();
+        rfrag(buf ^ 1, 0, f0a, f0b);
+        mma(f1a, f1b);
+        pin();
+        __builtin_amdgcn_sched_barrier(0);
     };
     gload(0, R0{});
     gload(1, R1{});
     lstore(0, R0{});
     __syncthreads();
+    rfrag(0, 0, f0a, f0b);
     /* whole pairs in the loop, so that no load or store sits under a branch there */
     int ks = 0;
     for (; ks + 1 < nks; ks += 2) {
