@@ -66,9 +66,16 @@ template <int MODE, int NS, int BN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void dense_gemm_kernel(DgArgs a)
 {
     constexpr int NJ = BN / 32;                    /* token fragments per wave */
-    constexpr int NA = DG_BM * 8 / 256, NB = BN * 8 / 256;   /* 16-byte chunks per thread */
+    constexpr int NA = DG_BM * 8 / 256;            /* 16-byte weight chunks per thread */
+    /* a step's activation tile in LDS: NS terms of BN rows of DG_LD elements, i.e. 9
+     * 16-byte slots per row (8 of data, 1 of padding); NDMA DMA instructions per wave fill
+     * it, the slots past the tile taking zeros */
+    constexpr int BSLOT = NS * BN * DG_LD / 8, NDMA = (BSLOT + 255) / 256;
+    static_assert((BN * DG_LD / 8) % 64 == 0, "a DMA instruction stays inside one term");
     __shared__ __attribute__((aligned(16))) uint16_t As[2][DG_BM * DG_LD];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NS][BN * DG_LD];
+    /* two arrays rather than one indexed array, so that the compiler can tell a DMA into
+     * one stage buffer from reads of the other (and waits for no DMA before those reads) */
+    __shared__ __attribute__((aligned(16))) uint16_t Bs0[NDMA * 256 * 8], Bs1[NDMA * 256 * 8];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -92,26 +99,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     const k3_rsrc rxh = k3_make_rsrc(a.xhi, (uint32_t)a.T * Kb);
     const k3_rsrc rxl = k3_make_rsrc(NS == 2 ? a.xlo : a.xhi, (uint32_t)a.T * Kb);
 
-    /* global -> register staging: thread tid loads chunk c = tid + 256 i of a tile, row
-     * c / 8, 16-byte column c % 8. Rows past R or T, and steps past the slice, get an offset
-     * at 2^31, beyond every operand (each is < 2 GiB): the buffer loads return zeros there,
-     * and no load sits under a branch. Chunk i of thread tid lies in rows 32i..32i+31, so for
-     * GATEUP the first half of the chunks are gate rows and the second half up rows. */
+    /* Weights: global -> register staging: thread tid loads chunk c = tid + 256 i of the
+     * tile, row c / 8, 16-byte column c % 8. Rows past R or T, and steps past the slice, get
+     * an offset at 2^31, beyond every operand (each is < 2 GiB): the buffer loads return
+     * zeros there, and no load sits under a branch. Chunk i of thread tid lies in rows
+     * 32i..32i+31, so for GATEUP the first half of the chunks are gate rows and the second
+     * half up rows. */
     constexpr uint32_t OOB = 0x80000000u;
-    uint32_t aoff[NA], boff[NB];
+    uint32_t aoff[NA];
 #pragma unroll
     for (int i = 0; i < NA; i++) {
         const int c = tid + 256 * i, row = c >> 3, col = c & 7;
         const int wrow = MODE == K3K_MX_GATEUP ? row0 + (row & (DG_BM / 2 - 1)) : row0 + row;
         aoff[i] = wrow < a.R ? (uint32_t)wrow * Kb + (uint32_t)(ks0 * DG_KS * 2) + (uint32_t)col * 16u : OOB;
     }
+    /* Activations: straight into LDS by the buffer unit (buffer_load_dwordx4 ... lds).
+     * Instruction i of wave wv fills slots 64 (wv + 4 i) + lane of the stage buffer: term
+     * slot / (9 BN), row (slot / 9) % BN, 16-byte column slot % 9 (8: the padding slot).
+     * Padding, slots past the tile and rows past T read at OOB (zeros); the step's column
+     * offset goes in the scalar offset. */
+    uint32_t doff[NDMA];
 #pragma unroll
-    for (int i = 0; i < NB; i++) {
-        const int c = tid + 256 * i, row = c >> 3, col = c & 7;
-        const int t = tok0 + row;
-        boff[i] = t < a.T ? (uint32_t)t * Kb + (uint32_t)(ks0 * DG_KS * 2) + (uint32_t)col * 16u : OOB;
+    for (int i = 0; i < NDMA; i++) {
+        const int slot = 64 * (wv + 4 * i) + lane, term = slot / (9 * BN);
+        const int row = (slot / 9) % BN, col = slot % 9, t = tok0 + row;
+        doff[i] = slot < BSLOT && col < 8 && t < a.T && term < NS
+                      ? (uint32_t)t * Kb + (uint32_t)(ks0 * DG_KS * 2) + (uint32_t)col * 16u : OOB;
     }
-    uint4 ra[2][NA], rbh[2][NB], rbl[2][NS == 2 ? NB : 1];
+    uint4 ra[2][NA];
     auto gload = [&](int ks, auto slot) {
         constexpr int S = decltype(slot)::value;
         const bool in = ks < nks;
@@ -121,12 +136,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
             const uint32_t o = (aoff[i] == OOB || !in) ? OOB : aoff[i] + kb;
             ra[S][i] = (MODE == K3K_MX_GATEUP && i >= NA / 2) ? k3_bload16(rw1, o) : k3_bload16(rw0, o);
         }
-#pragma unroll
-        for (int i = 0; i < NB; i++) {
-            const uint32_t o = (boff[i] == OOB || !in) ? OOB : boff[i] + kb;
-            rbh[S][i] = k3_bload16(rxh, o);
-            if (NS == 2) rbl[S][i] = k3_bload16(rxl, o);
-        }
     };
     auto lstore = [&](int buf, auto slot) {
         constexpr int S = decltype(slot)::value;
@@ -135,13 +144,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
             const int c = tid + 256 * i;
             *reinterpret_cast<uint4 *>(&As[buf][(c >> 3) * DG_LD + (c & 7) * 8]) = ra[S][i];
         }
+    };
+    /* step ks's activations into stage buffer buf (past the slice: zeros) */
+    auto dma_b = [&](int ks, uint16_t *bs) {
+        const bool in = ks < nks;
 #pragma unroll
-        for (int i = 0; i < NB; i++) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<uint4 *>(&Bs[buf][0][(c >> 3) * DG_LD + (c & 7) * 8]) = rbh[S][i];
-            if (NS == 2) *reinterpret_cast<uint4 *>(&Bs[buf][NS - 1][(c >> 3) * DG_LD + (c & 7) * 8]) = rbl[S][i];
+        for (int i = 0; i < NDMA; i++) {
+            const k3_rsrc r = (NS == 2 && 64 * (wv + 4 * i) >= 9 * BN) ? rxl : rxh;
+            k3_dma16(r, &bs[64 * 8 * (wv + 4 * i)], in ? doff[i] : OOB, (uint32_t)ks * (DG_KS * 2));
         }
     };
+    /* s_waitcnt operands: vmcnt at most NA (one step's weight loads; every other counter
+     * unconstrained), and at most NDMA */
+    constexpr int WAIT_NA = (NA & 15) | (7 << 4) | (15 << 8) | ((NA >> 4) << 14);
+    constexpr int WAIT_NDMA = (NDMA & 15) | (7 << 4) | (15 << 8) | ((NDMA >> 4) << 14);
 
     /* the wave's 4 row fragments inside the 128-row tile */
     int arow[4];
@@ -164,7 +180,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
      * issue under half 0's MFMAs, and the next step's half 0 reads (after the barrier that
      * publishes its LDS buffer) under half 1's. */
     k3_bf16x8 f0a[4], f0b[NS][NJ], f1a[4], f1b[NS][NJ];
-    auto rfrag = [&](int buf, int kk, k3_bf16x8 (&af)[4], k3_bf16x8 (&bf)[NS][NJ]) {
+    auto rfrag = [&](int buf, const uint16_t *bs, int kk, k3_bf16x8 (&af)[4], k3_bf16x8 (&bf)[NS][NJ]) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
             af[i] = k3_as_bf16x8(*reinterpret_cast<const uint4 *>(&As[buf][(arow[i] + r16) * DG_LD + kk + 8 * g]));
@@ -173,7 +189,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
             for (int j = 0; j < NJ; j++)
                 bf[s][j] = k3_as_bf16x8(*reinterpret_cast<const uint4 *>(
-                    &Bs[buf][s][(bcol0 + 16 * j + r16) * DG_LD + kk + 8 * g]));
+                    &bs[(s * BN + bcol0 + 16 * j + r16) * DG_LD + kk + 8 * g]));
     };
     auto mma = [&](const k3_bf16x8 (&af)[4], const k3_bf16x8 (&bf)[NS][NJ]) {
 #pragma unroll
@@ -196,32 +212,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         }
         __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
     };
-    /* step ks: its ring slot (ks & 1) is free once it is in LDS, so ks + 2 loads into it;
-     * ks is multiplied out of LDS buffer ks & 1 and ks + 1 stored into the other (past the
-     * slice the slot holds zeros, and the fragments read from that buffer go unused) */
+    /* step ks: its weight ring slot (ks & 1) is free once it is in LDS, so ks + 2 loads into
+     * it; ks is multiplied out of LDS buffer ks & 1 and ks + 1's weights stored into the
+     * other. The activations of ks + 1 (DMA issued a step ago, before ks + 2's weight loads)
+     * have landed once at most NA loads are outstanding; after the barrier that holds for
+     * every wave, every wave is past its reads of buffer ks & 1, and ks + 2's activations
+     * go into it. Past the slice the slots and buffers hold zeros, and the fragments read
+     * from them go unused. */
     auto step = [&](int ks, auto slot) {
         constexpr int S = decltype(slot)::value;
         const int buf = S;
+        uint16_t *const bcur = S ? Bs1 : Bs0, *const bnxt = S ? Bs0 : Bs1;
         gload(ks + 2, slot);
         /* issued here, ahead of the products (the compiler would otherwise sink them below
          * the next LDS store and wait for step ks + 1 with nothing else in flight) */
         __builtin_amdgcn_sched_barrier(0);
-        rfrag(buf, 32, f1a, f1b);
+        rfrag(buf, bcur, 32, f1a, f1b);
         mma(f0a, f0b);
         pin();
         __builtin_amdgcn_sched_barrier(0);
         lstore(buf ^ 1, std::integral_constant<int, S ^ 1>{});
+        __builtin_amdgcn_s_waitcnt(WAIT_NA);
         __syncthreads();
-        rfrag(buf ^ 1, 0, f0a, f0b);
+        dma_b(ks + 2, bcur);
+        rfrag(buf ^ 1, bnxt, 0, f0a, f0b);
         mma(f1a, f1b);
         pin();
         __builtin_amdgcn_sched_barrier(0);
     };
     gload(0, R0{});
     gload(1, R1{});
+    dma_b(0, Bs0);
+    dma_b(1, Bs1);
     lstore(0, R0{});
+    __builtin_amdgcn_s_waitcnt(WAIT_NDMA);         /* all but step 1's activations */
     __syncthreads();
-    rfrag(0, 0, f0a, f0b);
+    rfrag(0, Bs0, 0, f0a, f0b);
     /* whole pairs in the loop, so that no load or store sits under a branch there */
     int ks = 0;
     for (; ks + 1 < nks; ks += 2) {
@@ -229,6 +255,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         step(ks + 1, R1{});
     }
     if (ks < nks) step(ks, R0{});
+    /* the last DMAs (zeros past the slice) land before the workgroup's LDS is released */
+    __builtin_amdgcn_s_waitcnt(0);
 
     /* epilogue: lane holds token column r16 and rows 4g..4g+3 of each 16 x 16 tile */
 #pragma unroll
