@@ -15,14 +15,17 @@
  * one activation term, 64 with two) and walks its K range 64 columns at a time. A wave owns
  * 64 rows x BN/2 tokens, 4 x BN/32 accumulator blocks: per 32 columns it reads 4 weight and
  * BN/32 (per term) activation fragments from LDS for 16 MFMAs, so the LDS delivers what the
- * matrix cores consume. Each 64-column step's A (128 x 64) and B (BN x 64 per term) tiles
- * come from global memory with 16-byte buffer loads (8 consecutive lanes read one row's
- * 128 contiguous bytes; rows past R or T read zeros from beyond the buffer), two steps ahead
- * in a ring of two register slots, and are stored into a double-buffered LDS (rows padded
- * to 72 elements: the 16 rows of a fragment read start 36 banks apart, so a 16-lane
- * group's 16-byte reads cover the 64 banks once); one barrier per step.
+ * matrix cores consume. A step's two 32-column halves read their fragments into registers
+ * of their own, each half's reads issued under the other half's MFMAs. Each 64-column
+ * step's tiles sit in a double-buffered LDS (rows padded to 72 elements: the 16 rows of a
+ * fragment read start 36 banks apart, so a 16-lane group's 16-byte reads cover the 64 banks
+ * once); one barrier per step. The weight tile A (128 x 64) comes from global memory with
+ * 16-byte buffer loads (8 consecutive lanes read one row's 128 contiguous bytes; rows past R
+ * read zeros from beyond the buffer) two steps ahead, in a ring of two register slots, and
+ * is stored into LDS; the activation tile B (BN x 64 per term) goes into LDS by buffer-load
+ * DMA one step ahead.
  *
- * When the tiles cannot give every CU two workgroups, K is split into S slices (at least
+ * When the tiles cannot give every CU a workgroup, K is split into S slices (at least
  * 256 columns each): slice s writes its fp32 sums to part[s][t][col], and a second kernel
  * adds the slices in order and finishes (the activation, or the write / accumulation of
  * y). Without a partials buffer S is 1 and the GEMM kernel finishes itself.
@@ -359,15 +362,15 @@ __global__ __launch_bounds__(256) void dense_finish_kernel(DgArgs a)
     }
 }
 
-/* K slices: the fewest that give every CU one and a half workgroups, each slice at least
- * 256 columns (4 steps); 1 without a large enough partials buffer or when the output rows
- * are not a multiple of 4. (At 512 tokens, measured: gate/up 7168 -> 2048, 128 tiles, takes
- * 122 / 66 / 58 / 67 us at 1 / 2 / 4 / 8 slices plus 7-13 us of slice sums; down 2048 ->
- * 7168, 224 tiles, 55 / 38 / 47 / 59 us plus 11-24 us.) */
+/* K slices: the fewest that give every CU a workgroup, each slice at least 256 columns (4
+ * steps); 1 without a large enough partials buffer or when the output rows are not a
+ * multiple of 4. (At 512 tokens, measured, GEMM + slice sums: gate/up 7168 -> 2048, 128
+ * tiles, 87 / 47 + 7.5 / 46 + 8.4 / 58 + 13 us at 1 / 2 / 4 / 8 slices; down 2048 -> 7168,
+ * 224 tiles, 42 / 30 + 10 / - / 54 + 24 us at 1 / 2 / 8.) */
 static int dense_slices(int tiles, int K, int R, int T, int ncol, size_t part_bytes)
 {
     if (R % 4) return 1;
-    const long want = 3L * k3k_cu_count() / 2;
+    const long want = k3k_cu_count();
     int s = 1;
     while (s < 8 && (long)tiles * s < want && K / DG_KS / (2 * s) >= 4 &&
            (size_t)(2 * s) * T * ncol * 4 <= part_bytes)
