@@ -313,28 +313,41 @@ typedef struct {
  * multiples of 512: passes of 8 tokens, or of 32 (two MFMA column blocks) when the
  * activations are single bf16 terms and the batch averages at least 8 tokens per expert
  * (prefill). Other shapes run the register-fed kernel (16, row-major bank only). */
+/* One-term (prefill) activations at 8-32 tokens per expert on average on a tiled bank: two
+ * pass lists (below). */
+static int moe_two_lists(int T, int n_experts, int topk, int prec, int layout)
+{
+    return prec == 1 && layout == K3D_LAYOUT_TILED && (long)T * topk >= 8L * n_experts &&
+           (long)T * topk < 32L * n_experts;
+}
+
 /* Tokens per expert pass. 8 for decode (fp32-accurate, weight streaming), 16 when the
- * widths are not multiples of 512; one-term (prefill) activations take 32 from 8 tokens
- * per expert on average and, for a tiled bank, 48 from 32 and 96 from 64 tokens per
- * expert. The row-major choice is never larger than the tiled one, so it sizes the
- * workspace for both. */
+ * widths are not multiples of 512; one-term (prefill) activations take, for a tiled bank, 8
+ * from 8 tokens per expert on average (with the second list), 48 from 32 and 96 from 64;
+ * for a row-major bank 32 from 8. Sizing: a row-major bank's first list has at most N / 32
+ * passes beyond one per expert; a tiled bank's at most N / 8 where there is no second list,
+ * and one per expert where there is (its experts hold at most 8 assignments). */
 static int moe_pass_tok(int T, int hidden, int inter, int n_experts, int topk, int prec, int layout)
 {
     if (hidden % 512 || inter % 512) return 16;
     if (prec == 1 && layout == K3D_LAYOUT_TILED && (long)T * topk >= 64L * n_experts) return 96;
     if (prec == 1 && layout == K3D_LAYOUT_TILED && (long)T * topk >= 32L * n_experts) return 48;
+    if (moe_two_lists(T, n_experts, topk, prec, layout)) return 8;
     if (prec == 1 && (long)T * topk >= 8L * n_experts) return 32;
     return 8;
 }
 
-/* Batches that run 32-token passes on a tiled bank (8-32 tokens per expert on average) give
- * the experts holding more than 32 assignments -- the hot ones of a skewed routing -- the
- * prefill kernel's 96-token passes instead (a second pass list): their weights stream once
- * per 96 tokens rather than per 32. */
+/* The second pass list: where moe_two_lists holds, the experts holding more than pass_tok
+ * (8) assignments -- all but the coldest, and the hot ones of a skewed routing -- take the
+ * prefill kernel's 96-token passes, so their weights stream once per 96 tokens, and the
+ * rest one 8-token pass each on the streaming kernel. (Config 4, 512 tokens with skewed
+ * routing: 309 experts of at most 32 assignments in 32-token passes and 21 hot ones in the
+ * second list took 1.47 ms for gate/up + down; 282 experts of at most 8 in 8-token passes
+ * and 48 in the second list take 1.40 ms.) */
 #define MOE_PASS_TOK2 96
-static int moe_pass_tok2(int pass_tok, int layout, int prec)
+static int moe_pass_tok2(int T, int n_experts, int topk, int prec, int layout)
 {
-    return pass_tok == 32 && layout == K3D_LAYOUT_TILED && prec == 1 ? MOE_PASS_TOK2 : 0;
+    return moe_two_lists(T, n_experts, topk, prec, layout) ? MOE_PASS_TOK2 : 0;
 }
 
 /* The decode path (k3k_mx_decode): at most 16 assignments, widths multiples of 512 up to
@@ -352,6 +365,11 @@ static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n
     const int maxjobs = (int)(N < (size_t)n_experts ? N : (size_t)n_experts);
     w->max_passes = maxjobs + (int)(N / (size_t)moe_pass_tok(T, hidden, inter, n_experts, topk, prec,
                                                                 K3D_LAYOUT_ROWS)) + 1;
+    if (!moe_two_lists(T, n_experts, topk, prec, K3D_LAYOUT_TILED)) {
+        const int pt = moe_pass_tok(T, hidden, inter, n_experts, topk, prec, K3D_LAYOUT_TILED);
+        const int mp = maxjobs + (int)(N / (size_t)pt) + 1;
+        if (mp > w->max_passes) w->max_passes = mp;
+    }
     w->xhi = (uint16_t *)take(c, (size_t)T * hidden * 2);
     w->xlo = prec == 0 ? (uint16_t *)take(c, (size_t)T * hidden * 2) : NULL;
     w->ahi = (uint16_t *)take(c, N * inter * 2);
@@ -363,9 +381,9 @@ static size_t moe_layout(Carve *c, MoeWs *w, int T, int hidden, int inter, int n
     w->job_cnt = (int *)take(c, (size_t)maxjobs * 4);
     w->pass_job = (int *)take(c, (size_t)w->max_passes * 4);
     w->pass_tp = (int *)take(c, (size_t)w->max_passes * 4);
-    /* second list (one-term activations): experts of more than 32 assignments, each pass
-     * of up to 96 tokens -- at most N / 96 full passes plus one per such expert */
-    w->max_passes2 = prec == 1 ? (int)(N / MOE_PASS_TOK2 + N / 33 + 2) : 0;
+    /* second list (one-term activations): experts of more than 8 assignments, each pass of
+     * up to 96 tokens -- at most N / 96 full passes plus one per such expert */
+    w->max_passes2 = prec == 1 ? (int)(N / MOE_PASS_TOK2 + N / 9 + 2) : 0;
     w->pass_job2 = prec == 1 ? (int *)take(c, (size_t)w->max_passes2 * 4) : NULL;
     w->pass_tp2 = prec == 1 ? (int *)take(c, (size_t)w->max_passes2 * 4) : NULL;
     w->counts = (int *)take(c, (size_t)(4 + K3K_QUEUE_INTS) * 4);
@@ -507,7 +525,7 @@ static int moe_experts_ws(float *out, const int *idx, const float *wt, const flo
     }
     /* (the routed layer runs the split beside its router, on the side stream) */
     if (!x_split && k3k_split_bf16(w->xhi, w->xlo, x, (size_t)T * hidden, stream)) return fail("split");
-    const int pass_tok2 = moe_pass_tok2(pass_tok, layout, prec);
+    const int pass_tok2 = moe_pass_tok2(T, n_experts, topk, prec, layout);
     /* (gathered: the router's final kernel has run the gather) */
     if (!gathered &&
         k3k_gather(offsets, perm, w->job_expert, w->job_off, w->job_cnt, w->pass_job, w->pass_tp,
@@ -664,7 +682,7 @@ int k3d_moe_routed(float *out, int *idx, float *wt, const float *x, int T, const
         ga.bank = bank;
         ga.topk = topk;
         ga.pass_tok = pass_tok;
-        ga.pass_tok2 = moe_pass_tok2(pass_tok, layout, prec);
+        ga.pass_tok2 = moe_pass_tok2(T, n_experts, topk, prec, layout);
         ga.ctr = r.ctr;
     }
     rc = router_run(idx, wt, x, T, router_w, bias, hidden, n_experts, topk, renorm, routed_scale,
