@@ -103,9 +103,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     const k3_rsrc rxl = k3_make_rsrc(NS == 2 ? a.xlo : a.xhi, (uint32_t)a.T * Kb);
 
     /* Weights: global -> register staging: thread tid loads chunk c = tid + 256 i of the
-     * tile, row c / 8, 16-byte column c % 8. Rows past R or T, and steps past the slice, get
-     * an offset at 2^31, beyond every operand (each is < 2 GiB): the buffer loads return
-     * zeros there, and no load sits under a branch. Chunk i of thread tid lies in rows
+     * tile, row c / 8, 16-byte column c % 8. Rows past R, and steps past the slice, get an
+     * offset at 2^31, beyond every operand (each is < 2 GiB): the buffer loads return zeros
+     * there, and no load sits under a branch. Chunk i of thread tid lies in rows
      * 32i..32i+31, so for GATEUP the first half of the chunks are gate rows and the second
      * half up rows. */
     constexpr uint32_t OOB = 0x80000000u;
