@@ -626,6 +626,49 @@ def test_moe_experts_given_routing_invalid_slots(gpu, orc, k3, T, K, I):
         assert max_err_rel_inf(out[tk], acc) <= TOL, tk
 
 
+def test_moe_experts_two_lists_invalid_slots(gpu, orc, k3):
+    """k3d_moe_experts with a caller's routing in the two-list regime (bf16 activations,
+    tiled bank, 8-32 assignments per expert on average): four hot experts in the 96-token
+    list, cold ones in one 8-token pass each, one cold expert absent from the bank and
+    slots outside the bank (-1, N, 1000). Drops count only the absent expert's slots, the
+    offsets only valid slots, and every token's output is the oracle's per-slot sum
+    without the dropped and invalid slots (2e-2 relative)."""
+    E, I, N, K, T = 1024, 512, 12, 4, 40
+    say(f"case: two pass lists with invalid slots E={E} I={I} N={N} K={K} T={T}")
+    bank = [k3.gen_expert(E, I, 223, e) for e in range(N)]
+    holed = list(bank)
+    holed[7] = None
+    rng = np.random.default_rng(227)
+    X = rng.standard_normal((T, E)).astype(np.float32)
+    t = np.arange(T)
+    idx = np.stack([t % 4, (t + 1) % 4, 4 + t % 8,
+                    np.where(t < 20, 4 + (t + 3) % 8, (t + 2) % 4)], axis=1).astype(np.int32)
+    idx[0, 1] = -1
+    idx[1, 0] = N
+    idx[-1, K - 1] = 1000
+    wt = (rng.random((T, K)) + 0.1).astype(np.float32)
+    valid = (idx >= 0) & (idx < N)
+    cnt = np.bincount(idx[valid], minlength=N)
+    assert 8 * N <= T * K < 32 * N                                   # the two-list regime
+    assert (cnt[:4] > 8).all() and (cnt[4:] <= 8).all() and cnt[7] > 0
+    b = gpu.DevBank(holed, E, I, gpu.K3D_LAYOUT_TILED)
+    try:
+        out, off, drops = gpu.moe_experts_device(b, X, idx, wt, N, prec=1, hidden=E, inter=I)
+    finally:
+        b.free()
+    assert drops == int(cnt[7])
+    assert off[N] == int(valid.sum())
+    o2 = np.zeros((T, E), np.float32)
+    for tk in range(T):
+        for j in range(K):
+            e = int(idx[tk, j])
+            if 0 <= e < N and holed[e] is not None:
+                o2[tk] += np.float32(wt[tk, j]) * orc.expert_ffn(X[tk], bank[e], E, I, act=1, wt=1.0)
+    assert np.linalg.norm(out - o2) / np.linalg.norm(o2) <= TOL_BF16
+    for tk in range(T):
+        assert max_err_rel_inf(out[tk], o2[tk]) <= 5e-2, tk
+
+
 def test_moe_device_mixed_passes(gpu, orc, k3):
     """Moderate batches on a tiled bank (8-32 tokens per expert on average) run one 8-token
     pass per expert of at most 8 assignments, and the experts holding more get the prefill
