@@ -117,6 +117,13 @@ int k3d_mxfp4_tile(uint8_t *tpacked, uint8_t *tscales, const uint8_t *packed,
  * the split fp64 sum could not certify and that were recomputed with the reference's
  * sequential chain. */
 int k3d_router_recomputed(int *h_counts, const void *ws, int T, int hidden, int n_experts);
+/* The chunk partials of the same call (more than four tokens; synchronises): *h_chunk = the
+ * chunk width, h_part / h_rbound [ks][T][n_experts] (ks = ceil(hidden / chunk), at most
+ * `cap` entries each) the chunk sums P_k and the bounds R_k, |P_k - exact| <= 2^-53 R_k and
+ * R_k >= the sum of |the chunk's exact prefix sums|, that the certification uses. Returns
+ * ks, or -1. */
+int k3d_router_partials(double *h_part, float *h_rbound, int *h_chunk, size_t cap, const void *ws, int T,
+                        int hidden, int n_experts);
 
 /* The routed MoE layer (k3_moe's routed loop, reference k3_ops.c:576-643, with z := x),
  * expert-major. bank is a DEVICE array of n_experts K3ExpertQ (k3.h) whose pointers are

@@ -230,17 +230,20 @@ typedef struct {
     int *nrecomp;
     int *ctr;                   /* the final kernel's arrival counter, when it gathers */
     int chunk;
+    void *i8;                   /* scratch of the int8 partials (NULL: the fp64 ones) */
 } RtWs;
 
 static size_t router_layout(Carve *c, RtWs *w, int T, int hidden, int n_experts)
 {
-    w->chunk = k3k_router_chunk(T, hidden, n_experts);
+    const int c8 = k3k_router_i8_chunk(T, hidden, n_experts);
+    w->chunk = c8 ? c8 : k3k_router_chunk(T, hidden, n_experts);
     const size_t ks = (size_t)((hidden + w->chunk - 1) / w->chunk);
     /* chunk partials, or (a few tokens) one 16-byte scored record per logit */
     w->part = (double *)take(c, (ks < 2 ? 2 : ks) * T * n_experts * 8);
     w->rbound = (float *)take(c, ks * T * n_experts * 4);
     w->nrecomp = (int *)take(c, (size_t)T * 4);
     w->ctr = (int *)take(c, 4);
+    w->i8 = c8 ? take(c, k3k_router_i8_bytes(T, hidden, n_experts, c8)) : NULL;
     return c->off;
 }
 
@@ -264,10 +267,18 @@ static int router_run(int *idx, float *wt, const float *x, int T, const float *W
         g = *gather;
         g.ctr = w->ctr;
     }
-    if (k3k_router_partial(w->part, w->rbound, x, T, W, hidden, n_experts, w->chunk,
-                           gather ? w->ctr : NULL, gather ? idx : NULL, gather ? T * topk : 0, exc,
-                           stream))
+    /* the int8 partials where they apply (16-byte aligned rows), else the fp64 ones with the
+     * same chunks */
+    if (w->i8 && !((((uintptr_t)x) | ((uintptr_t)W)) % 16)) {
+        if (k3k_router_partial_i8(w->part, w->rbound, w->i8, x, T, W, hidden, n_experts, w->chunk,
+                                  gather ? w->ctr : NULL, gather ? idx : NULL, gather ? T * topk : 0,
+                                  stream))
+            return fail("router_partial_i8");
+    } else if (k3k_router_partial(w->part, w->rbound, x, T, W, hidden, n_experts, w->chunk,
+                                  gather ? w->ctr : NULL, gather ? idx : NULL, gather ? T * topk : 0,
+                                  exc, stream)) {
         return fail("router_partial");
+    }
     if (k3k_router_final(idx, wt, w->nrecomp, w->part, w->rbound, w->chunk, x, W, bias, T, hidden,
                          n_experts, topk, renorm, routed_scale, exc, gather ? &g : NULL, stream))
         return fail("router_final");
@@ -282,6 +293,22 @@ int k3d_router_recomputed(int *h_counts, const void *ws, int T, int hidden, int 
     router_layout(&c, &w, T, hidden, n_experts);
     if (k3k_d2h(h_counts, w.nrecomp, (size_t)T * 4, NULL) || k3k_sync(NULL)) return fail("router_recomputed");
     return 0;
+}
+
+int k3d_router_partials(double *h_part, float *h_rbound, int *h_chunk, size_t cap, const void *ws, int T,
+                        int hidden, int n_experts)
+{
+    if (T <= 4 || k3k_router_small(T, hidden)) return bad("k3d_router_partials: a few tokens are scored whole");
+    Carve c = {(char *)ws, 0};
+    RtWs w;
+    router_layout(&c, &w, T, hidden, n_experts);
+    const int ks = (hidden + w.chunk - 1) / w.chunk;
+    const size_t n = (size_t)ks * T * n_experts;
+    if (n > cap) return bad("k3d_router_partials: cap");
+    if (k3k_d2h(h_part, w.part, n * 8, NULL) || k3k_d2h(h_rbound, w.rbound, n * 4, NULL) || k3k_sync(NULL))
+        return fail("router_partials");
+    *h_chunk = w.chunk;
+    return ks;
 }
 
 int k3d_router(int *idx, float *wt, const float *x, int T, const float *W, const float *bias,

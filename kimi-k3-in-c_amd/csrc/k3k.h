@@ -225,6 +225,15 @@ int k3k_router_gathers(int T, int hidden, int n_experts, int topk);
 int k3k_router_partial(double *part, float *rbound, const float *x, int T, const float *W,
                        int hidden, int n_experts, int chunk, int *ctr, int *idx, int n_idx,
                        const K3kExc *exc, void *stream);
+/* The same partials of many tokens on the int8 matrix cores (k3_route_i8.hip): the chunk
+ * for T tokens, or 0 where those kernels do not apply (then k3k_router_partial with
+ * k3k_router_chunk's chunk); the scratch they need; the partials (x and W 16-byte aligned,
+ * chunk from k3k_router_i8_chunk). */
+int k3k_router_i8_chunk(int T, int hidden, int n_experts);
+size_t k3k_router_i8_bytes(int T, int hidden, int n_experts, int chunk);
+int k3k_router_partial_i8(double *part, float *rbound, void *scratch, const float *x, int T,
+                          const float *W, int hidden, int n_experts, int chunk, int *ctr, int *idx,
+                          int n_idx, void *stream);
 /* gather (may be NULL): also run the gather of idx, as k3k_gather would. */
 int k3k_router_final(int *idx, float *wt, int *nrecomp, const double *part, const float *rbound,
                      int chunk, const float *x, const float *W, const float *bias, int T,

@@ -135,6 +135,7 @@ def _declare(L):
     d("k3d_router_ws", SZ, I, I, I)
     d("k3d_router", I, P, P, P, I, P, P, I, I, I, I, F, P, SZ, P)
     d("k3d_router_recomputed", I, P, P, I, I, I)
+    d("k3d_router_partials", I, P, P, P, SZ, P, I, I, I)
     d("k3d_moe_ws", SZ, I, I, I, I, I, I)
     d("k3d_moe_routed", I, P, P, P, P, I, P, P, P, I, I, I, I, I, I, F, I, F, F, I, P, SZ, P, P,
       P, P)
@@ -576,8 +577,10 @@ def moe_experts_device(bank, x, idx, wt, n_experts, act=K3_ACT_SILU, b1=4.0, b2=
             v.free()
 
 
-def router_device(x, W, bias, topk, renorm=1, routed_scale=1.0):
-    """k3d_router over T tokens on the device: host arrays in, idx/wt [T][topk] out."""
+def router_device(x, W, bias, topk, renorm=1, routed_scale=1.0, partials=False):
+    """k3d_router over T tokens on the device: host arrays in, idx/wt [T][topk] out.
+    partials: also fetch the chunk partials into router_device.partials = (part [ks][T][N],
+    rbound [ks][T][N], chunk)."""
     L = lib()
     W = _f32(W)
     n_experts, hidden = W.shape
@@ -597,6 +600,18 @@ def router_device(x, W, bias, topk, renorm=1, routed_scale=1.0):
         check(L.k3d_router_recomputed(rec.ctypes.data, dws.ptr, T, hidden, n_experts),
               "k3d_router_recomputed")
         router_device.recomputed = rec
+        if partials:
+            cap = ((hidden + 63) // 64) * T * n_experts
+            part = np.empty(cap, np.float64)
+            rb = np.empty(cap, np.float32)
+            ch = np.zeros(1, np.int32)
+            ks = L.k3d_router_partials(part.ctypes.data, rb.ctypes.data, ch.ctypes.data, cap, dws.ptr, T,
+                                       hidden, n_experts)
+            if ks <= 0:
+                raise RuntimeError("k3d_router_partials: " + L.k3d_error().decode())
+            n = ks * T * n_experts
+            router_device.partials = (part[:n].reshape(ks, T, n_experts), rb[:n].reshape(ks, T, n_experts),
+                                      int(ch[0]))
         return (di.download(np.empty((T, topk), np.int32)),
                 dw.download(np.empty((T, topk), np.float32)))
     finally:
