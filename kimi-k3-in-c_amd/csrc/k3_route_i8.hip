@@ -68,12 +68,32 @@ constexpr int RI_XB = RI_TT / 16 * RI_ND, RI_WB = RI_TE / 16 * RI_ND, RI_SB = RI
 
 /* What the bound needs of one row's chunk, from digit_scale_kernel: the scale exponent
  * (RI_BAD: a non-finite value), bounds on rho = sum |V - digits|, l2 = ||V||_2,
- * mx = max |V| and n1[i] >= sum |d_i| over the chunk. */
+ * mx = max |V|, and n1 >= sum |d_1|, n2 >= sum |d_i| for every later digit i. */
 struct RiRow {
     double rho, l2, mx;
     int s;
-    int n1[RI_ND];
+    int n1, n2;
 };
+
+/* Weights of the products' bound terms by level group (left out: i + j > RI_LMAX; levels
+ * 5 .. RI_LMAX; levels 2-4) and by whether i and j are the first digit: sum 127 2^-7(i+j-2)
+ * over the group's pairs of that class, so that sum over the group of 127 min(n_w,i, n_x,j)
+ * 2^-7(i+j-2) = sum over the classes of the weight times min(n_w, n_x) of the class. */
+struct RiGw {
+    double c[3][2][2];
+};
+constexpr RiGw ri_gw()
+{
+    RiGw g = {};
+    for (int i = 1; i <= RI_ND; i++)
+        for (int j = 1; j <= RI_ND; j++) {
+            double w = 127.0;
+            for (int q = 0; q < i + j - 2; q++) w *= 0x1p-7;
+            const int grp = i + j > RI_LMAX ? 0 : i + j >= 5 ? 1 : 2;
+            g.c[grp][i > 1][j > 1] += w;
+        }
+    return g;
+}
 
 /* ---- digit split ---------------------------------------------------------------------- */
 struct RiSplit {
@@ -188,9 +208,8 @@ __global__ __launch_bounds__(256) void digit_scale_kernel(RiSplit a)
         r.l2 = sqrt((double)sq * (1.0 + 0x1p-10)) * (1.0 + 0x1p-30) + fl * 64.0;
         r.mx = (double)mx + fl;
         r.s = s;
-        r.n1[0] = (int)ceil((double)l1 * (1.0 + 0x1p-10) + fl * a.chunk);
-#pragma unroll
-        for (int p = 1; p < RI_ND; p++) r.n1[p] = 127 * nnz;
+        r.n1 = (int)ceil((double)l1 * (1.0 + 0x1p-10) + fl * a.chunk);
+        r.n2 = 127 * nnz;
         (isx ? a.rx : a.rw)[rc] = r;
     }
 }
@@ -383,6 +402,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int e = et * RI_TE + 16 * we + (lane & 15);
     if (e >= a.E) return;
     const double C = (double)a.chunk;
+    constexpr RiGw GW = ri_gw();
     const RiRow we_ = a.rw[(size_t)e * a.ks + k];
 #pragma unroll
     for (int h = 0; h < 2; h++)
@@ -412,26 +432,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 tv = fma(tv, 0x1p-7, (double)acc[l][h][r]);
                 errc += fabs(tv);
             }
-            /* 127 min(n1_w[i], n1_x[j]) >= sum |d_w,i d_x,j| over the chunk, by level group:
+            /* 127 min(n_w,i, n_x,j) >= sum |d_w,i d_x,j| over the chunk, by level group:
              * left out (above RI_LMAX), levels 5 .. RI_LMAX (not in the prefix estimate),
              * levels 2-4 (their fp32 rounding in it) */
-            double om = 0.0, t5 = 0.0, f4 = 0.0;
+            const double m[2][2] = {{(double)min(we_.n1, xt.n1), (double)min(we_.n1, xt.n2)},
+                                    {(double)min(we_.n2, xt.n1), (double)min(we_.n2, xt.n2)}};
+            double gs[3];
 #pragma unroll
-            for (int i = 1; i <= RI_ND; i++) {
-                double wl = 127.0;
-#pragma unroll
-                for (int q = 1; q < i; q++) wl *= 0x1p-7;
-#pragma unroll
-                for (int j = 1; j <= RI_ND; j++) {
-                    double w2 = wl;
-#pragma unroll
-                    for (int q = 1; q < j; q++) w2 *= 0x1p-7;
-                    const double g2 = w2 * (double)min(we_.n1[i - 1], xt.n1[j - 1]);
-                    if (i + j > RI_LMAX) om += g2;
-                    else if (i + j >= 5) t5 += g2;
-                    else f4 += g2;
-                }
-            }
+            for (int q = 0; q < 3; q++)
+                gs[q] = (GW.c[q][0][0] * m[0][0] + GW.c[q][0][1] * m[0][1]) + (GW.c[q][1][0] * m[1][0] + GW.c[q][1][1] * m[1][1]);
+            const double om = gs[0], t5 = gs[1], f4 = gs[2];
             const double rho = we_.rho * xt.mx + (we_.mx + 0x1p-35) * xt.rho;
             const double esc = om + rho + 1.01 * 0x1p-53 * errc;
             const double rref = 64.0 * (double)snap[h][r] * (1.0 + 0x1p-15) +
@@ -446,8 +456,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 /* ---- host side ------------------------------------------------------------------------ */
 /* The int8 partials serve batches of at least RI_MIN_T tokens with rows of a multiple of
- * 64 columns; fewer tokens keep the fp64 kernels. */
-constexpr int RI_MIN_T = 256;
+ * 256 columns; fewer tokens keep the fp64 kernels (at 512 tokens those took 84 us against
+ * 100 us for the digits and the int8 partials). */
+constexpr int RI_MIN_T = 1024;
 
 static int ri_round(int v, int m) { return (v + m - 1) / m * m; }
 
