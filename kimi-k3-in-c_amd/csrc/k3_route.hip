@@ -539,7 +539,8 @@ __device__ __forceinline__ Certified certify_score(double Q, double bs, const Ex
  *   k order (Q_{k+1} = Q_k + P_k, the rounding the bound describes) on broadcast LDS reads
  *   and keeps its own Q_k, Q_{k+1}; lane k forms C_k |Q_k| + 2 R_k + |Q_{k+1}|, the wave
  *   adds those (any order: bs only bounds); lane 0 certifies (certify_score), its
- *   exception-bitmap word loaded as soon as the sum is known, and stores pre[t][e] =
+ *   exception-bitmap word requested before the ordered sum for the sum in any order (the
+ *   two round to the same float but for rare ties, which load it again), and stores pre[t][e] =
  *   {score, score of the upper end, uncertified ? 1 : 0, 0}. */
 template <bool VEC>
 __device__ __forceinline__ float4 rs_load4(k3_rsrc r, uint32_t col)
@@ -668,6 +669,10 @@ __global__ __launch_bounds__(256) void router_small_kernel(float4 *pre, const fl
     /* rounded up: the float sums of |w| carry at most a 2^-18 relative error */
     const double R = (double)bound_up(rb, 1.0 + 0x1p-17);
     jsh[t][lane] = J;
+    /* the exception-bitmap word of the sum in any order, requested now: the ordered sum
+     * below rounds to the same float (same bits) but for rare ties, which load it again */
+    const double Sa = wave_sum_f64(J);
+    const uint32_t fwa = exc_word((float)Sa, exc);
     __builtin_amdgcn_wave_barrier();
     /* the sum in k order in every lane (broadcast reads); lane k keeps Q_k and Q_{k+1} */
     double pk[64];
@@ -685,7 +690,7 @@ __global__ __launch_bounds__(256) void router_small_kernel(float4 *pre, const fl
         if (k == lane) q1 = q;
     }
     const double S = q;
-    const uint32_t fw = exc_word((float)S, exc);
+    const uint32_t fw = __float_as_uint((float)S) == __float_as_uint((float)Sa) ? fwa : exc_word((float)S, exc);
     const double ck = (double)min(RS_CH, hidden - min(lane, ks - 1) * RS_CH);
     const double term = lane < ks ? fma(ck, fabs(q0), fma(2.0, R, fabs(q1))) : 0.0;
     const double bs = wave_sum_f64(term);
