@@ -12,7 +12,8 @@ every branch of the split: rows whose largest value is 128 or more (scaled down,
 values may lose bits to the subnormal range), zero rows, values spread over many binades
 (left-out remainders), tiny and subnormal values, and a non-finite value (its chunk falls
 back to a plain fp64 chain). idx and weight bits equal the oracle's per-token router
-(k3_ops.c:419-478) for every token. The int8 partials serve 1024 tokens and more."""
+(k3_ops.c:419-478) for every token. The int8 partials serve 1024 tokens and more; the fp64
+matrix-core partials of fewer tokens are held to the same contract."""
 import sys
 
 import numpy as np
@@ -94,6 +95,26 @@ def test_router_i8_partials_and_selection(gpu, orc, T, N, K):
     assert np.isnan(part[:, 5]).any() or np.isinf(part[:, 5]).any()   # the non-finite row
     for t in range(T):
         i2, w2 = orc.router(X[t], W, None, K)
+        assert np.array_equal(idx[t], i2), t
+        assert np.array_equal(bits(wt[t]), bits(w2)), t
+
+
+@pytest.mark.parametrize("T,N", [(300, 384), (64, 200)])
+def test_router_fp64_partials_contract(gpu, orc, T, N):
+    """The same contract for the fp64 matrix-core partials that serve 5 to 1023 tokens
+    (router_partial_mfma_kernel, k3_route.hip), on the same special rows: the chunk sums
+    within 2^-53 R_k of the exact ones, R_k above the exact prefix magnitudes, and idx /
+    weight bits equal to the oracle's."""
+    say(f"case: fp64 router partials T={T} N={N}")
+    W, X = special_inputs(T, N, 7 * T + N)
+    idx, wt = gpu.router_device(X, W, None, 8, partials=True)
+    part, rb, chunk = gpu.router_device.partials
+    say(f"  chunk {chunk} ({part.shape[0]} chunks), recomputed logits: "
+        f"{int(gpu.router_device.recomputed.sum())}")
+    e, p = check_contract(part, rb, chunk, W, X, list(range(12)) + [T - 1])
+    say(f"  worst |P - exact| / (2^-53 R): {e:.3g}; worst sum|prefix| / R: {p:.3g}")
+    for t in range(T):
+        i2, w2 = orc.router(X[t], W, None, 8)
         assert np.array_equal(idx[t], i2), t
         assert np.array_equal(bits(wt[t]), bits(w2)), t
 
