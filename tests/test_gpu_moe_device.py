@@ -223,14 +223,16 @@ def test_moe_device_tiled_decode_golden(gpu, wl, gold):
     (3, 7168, 384, 8, True), (4, 8192, 96, 8, False), (2, 8200, 64, 4, True),
     (7, 7168, 384, 8, True), (31, 1001, 70, 5, True),
     (33, 1000, 70, 5, False), (64, 7168, 384, 8, False), (100, 520, 131, 16, True),
-    (129, 7168, 384, 8, False), (300, 1000, 200, 5, True),
+    (129, 7168, 384, 8, False), (300, 1000, 200, 5, True), (1100, 1000, 200, 5, True),
+    (1024, 2304, 130, 8, False),
     (2, 1024, 1000, 8, True), (40, 512, 1500, 8, False), (20, 256, 2048, 16, True)])
 def test_router_device_bit_exact(gpu, orc, T, hidden, N, K, biased):
     """Every partial kernel (a workgroup per expert for a few tokens up to 64 chunks of 128
-    columns, one lane per chunk past that, the matrix cores for more tokens), widths that
-    are not a multiple of the staging chunk (and an odd one: scalar loads), expert and
-    token counts that are not multiples of the tiles: idx and weight bits equal to the
-    oracle's per-token router."""
+    columns, one lane per chunk past that, the matrix cores for more tokens: fp64, and int8
+    digit products from 1024 tokens when the rows are a multiple of 256 columns, else fp64
+    again), widths that are not a multiple of the staging chunk (and an odd one: scalar
+    loads), expert and token counts that are not multiples of the tiles: idx and weight
+    bits equal to the oracle's per-token router."""
     say(f"case: router T={T} hidden={hidden} N={N} K={K} bias={biased}")
     rng = np.random.default_rng(T * 1000 + hidden)
     W = (rng.standard_normal((N, hidden)) * 0.02).astype(np.float32)
