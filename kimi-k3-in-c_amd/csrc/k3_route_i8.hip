@@ -108,16 +108,10 @@ constexpr int RI_CMAX = 4096;          /* longest chunk: 16 pieces of 4 columns 
 
 /* Four values -> their digits (word p holds digit p + 1 of value c in byte c), in fp32:
  * every digit step is exact, and so is V = v 2^s except where it scales down into the
- * subnormal range (|V| < 2^-126, all digits zero). The sums of |remainder| (units of 2^-35),
- * of V^2 and the largest |V| go into rem, sq, mx. */
-__device__ __forceinline__ void ri_digits4(float4 v, int s, uint32_t (&w)[RI_ND], float &rem, float &sq, float &mx)
+ * subnormal range (|V| < 2^-126, all digits zero). */
+__device__ __forceinline__ void ri_digits4(float4 v, int s, uint32_t (&w)[RI_ND])
 {
     float r[4] = {ldexpf(v.x, s), ldexpf(v.y, s), ldexpf(v.z, s), ldexpf(v.w, s)};
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        sq = fmaf(r[c], r[c], sq);
-        mx = fmaxf(mx, fabsf(r[c]));
-    }
 #pragma unroll
     for (int p = 0; p < RI_ND; p++) {
         uint32_t word = 0u;
@@ -129,8 +123,6 @@ __device__ __forceinline__ void ri_digits4(float4 v, int s, uint32_t (&w)[RI_ND]
         }
         w[p] = word;
     }
-#pragma unroll
-    for (int c = 0; c < 4; c++) rem += fabsf(r[c]);
 }
 
 /* A wave per (row, chunk) of x, then of W, every load of the row's chunk in flight at once:
@@ -240,9 +232,8 @@ __global__ __launch_bounds__(64 * RI_SPS) void digit_split_kernel(RiSplit a)
     const int s = row < rows ? (isx ? a.rx : a.rw)[(size_t)row * a.ks + k].s : RI_BAD;
     const bool live = s != RI_BAD;
     uint32_t w[4][RI_ND];
-    float rem = 0.0f, sq = 0.0f, mx = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 4; q++) ri_digits4(live ? val[q] : make_float4(0.f, 0.f, 0.f, 0.f), live ? s : 0, w[q], rem, sq, mx);
+    for (int q = 0; q < 4; q++) ri_digits4(live ? val[q] : make_float4(0.f, 0.f, 0.f, 0.f), live ? s : 0, w[q]);
     uint4 *blk = reinterpret_cast<uint4 *>((isx ? a.dx : a.dw) + ((size_t)gst * ntile + tile) * (RI_ND * RI_BLK)) + L;
 #pragma unroll
     for (int p = 0; p < RI_ND; p++) blk[p * (RI_BLK / 16)] = make_uint4(w[0][p], w[1][p], w[2][p], w[3][p]);
