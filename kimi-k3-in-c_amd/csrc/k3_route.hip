@@ -1509,11 +1509,13 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
         return 0;
     }
     /* scored records (a few tokens) or the chunk partials: a lane per expert (two past
-     * 1024), all of a lane's partials in one load batch when they are at most 16 or 32, or 64
-     * for up to 64 tokens and 512 experts (more registers, fewer waves per CU: only while the
-     * tokens do not fill the chip). The selection is two-level when the expert groups fit
-     * (select_rounds), else wave 0 selects over SW keys per lane: 8 up to 512 experts, 16 up
-     * to 1024, else 32 (each pick rescans the picking lane's SW keys). */
+     * 1024), all of a lane's partials in one load batch when they are at most 32 -- up to 512
+     * experts the batch is sized to the chunk count (2, 4, 8 or 16: no repeated loads, fewer
+     * registers, more workgroups per CU) -- or 64 for up to 64 tokens and 512 experts (more
+     * registers, fewer waves per CU: only while the tokens do not fill the chip). The
+     * selection is two-level when the expert groups fit (select_rounds), else wave 0 selects
+     * over SW keys per lane: 8 up to 512 experts, 16 up to 1024, else 32 (each pick rescans
+     * the picking lane's SW keys). */
 #define K3_RF(SL, SW, KB, PRE, NT)                                                                  \
     hipLaunchKernelGGL((router_final_kernel<SL, SW, KB, PRE>), dim3(T), dim3(NT), 0, st, idx, wt, nrecomp, \
                        part, rbound, ks, chunk, x, W, bias, T, hidden, n_experts, topk, renorm,        \
@@ -1521,6 +1523,9 @@ extern "C" int k3k_router_final(int *idx, float *wt, int *nrecomp, const double 
     if (pre && n_experts <= 512) K3_RF(1, 8, RF_KB, true, 64 * nw);
     else if (pre && n_experts <= 1024) K3_RF(1, 16, RF_KB, true, 64 * nw);
     else if (pre) K3_RF(2, 32, RF_KB, true, 64 * nw);
+    else if (n_experts <= 512 && ks <= 2) K3_RF(1, 8, 2, false, 64 * nw);
+    else if (n_experts <= 512 && ks <= 4) K3_RF(1, 8, 4, false, 64 * nw);
+    else if (n_experts <= 512 && ks <= 8) K3_RF(1, 8, 8, false, 64 * nw);
     else if (n_experts <= 512 && ks <= 16) K3_RF(1, 8, 16, false, 64 * nw);
     else if (n_experts <= 512 && ks > 32 && ks <= 64 && T <= 64) K3_RF(1, 8, 64, false, 64 * nw);
     else if (n_experts <= 512) K3_RF(1, 8, RF_KB, false, 64 * nw);
