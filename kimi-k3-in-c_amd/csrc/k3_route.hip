@@ -26,20 +26,34 @@ __device__ __forceinline__ bool expert_present(const void *bank, int e)
 }
 
 /* ---- fp32 -> bf16 hi/lo ----------------------------------------------------------- */
-/* four elements per thread: float4 loads, 8-byte stores (n % 4 == 0, 16-byte aligned x) */
+/* four elements per float4: 16-byte loads, 8-byte stores (n % 4 == 0, 16-byte aligned x).
+ * A thread takes SPLIT_U float4s a grid stride apart and requests them all before it
+ * converts any, so each lane keeps SPLIT_U loads in flight (with one, a full chip of
+ * waves keeps too few bytes in flight to cover the memory latency). */
+constexpr int SPLIT_U = 4;
+__device__ __forceinline__ void split4_store(uint2 *hi, uint2 *lo, size_t i, float4 v)
+{
+    uint16_t h[4], l[4];
+    k3_split2(v.x, h[0], l[0]);
+    k3_split2(v.y, h[1], l[1]);
+    k3_split2(v.z, h[2], l[2]);
+    k3_split2(v.w, h[3], l[3]);
+    hi[i] = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+    if (lo) lo[i] = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+}
+
 __global__ void split4_kernel(uint2 *hi, uint2 *lo, const float4 *x, size_t n4)
 {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const float4 v = x[i];
-        uint16_t h[4], l[4];
-        k3_split2(v.x, h[0], l[0]);
-        k3_split2(v.y, h[1], l[1]);
-        k3_split2(v.z, h[2], l[2]);
-        k3_split2(v.w, h[3], l[3]);
-        hi[i] = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
-        if (lo) lo[i] = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + (SPLIT_U - 1) * stride < n4; i += SPLIT_U * stride) {
+        float4 v[SPLIT_U];
+#pragma unroll
+        for (int u = 0; u < SPLIT_U; u++) v[u] = x[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < SPLIT_U; u++) split4_store(hi, lo, i + u * stride, v[u]);
     }
+    for (; i < n4; i += stride) split4_store(hi, lo, i, x[i]);
 }
 
 __global__ void split_kernel(uint16_t *hi, uint16_t *lo, const float *x, size_t n)
@@ -1306,7 +1320,12 @@ extern "C" int k3k_split_bf16(uint16_t *hi, uint16_t *lo, const float *x, size_t
     const bool v4 = n % 4 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)hi % 8) == 0 &&
                     ((uintptr_t)lo % 8) == 0;
     if (v4)
-        hipLaunchKernelGGL(split4_kernel, dim3(grid1d(n / 4, 256)), dim3(256), 0, (hipStream_t)stream,
+        /* SPLIT_U float4s per thread from 2^21 float4s on (4096 x 7168: 73 -> 62 us); below
+         * that one per thread, the grid's full width (512 x 7168: 7.0 against 7.9 us) */
+        hipLaunchKernelGGL(split4_kernel,
+                           dim3(n / 4 >= ((size_t)1 << 21) ? grid1d((n / 4 + SPLIT_U - 1) / SPLIT_U, 256)
+                                                           : grid1d(n / 4, 256)),
+                           dim3(256), 0, (hipStream_t)stream,
                            reinterpret_cast<uint2 *>(hi), reinterpret_cast<uint2 *>(lo),
                            reinterpret_cast<const float4 *>(x), n / 4);
     else
